@@ -1,0 +1,249 @@
+"""Benchmark of the fp8 decode GEMV (headline) and the fp8 prefill GEMM.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm]
+
+Headline workload (headline shape): esimd_gemv_fp8_pern
+with M = 1, K = 4096, N = 14336: fp16 activations, e4m3 weights with an fp32
+per-output-channel scale, fp16 output.  A step is one GEMV call; step i reads
+weight copy i % C, with C copies totalling > 2 GB so that no step finds its
+weights in the 256 MB Infinity Cache.  All inputs are resident in HBM before
+the timed region.
+
+Timing: W untimed warm-up steps, then exactly K steps captured in one HIP
+graph (so host launch cost is not measured) and replayed once between
+device synchronisations; ms_per_step = wall time / K.  The dominant kernel's
+average launch duration is measured with HIP events on the launch stream
+around the same graph replay; it feeds roofline.achieved.
+
+cpu_baseline: the reference's torch CPU path restated in oracle/
+((x.float() @ W8.to(fp16).float().T) * s) on this host's cores, timed on the
+same shape (2 warm-ups, median of 5).
+"""
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, spec
+FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA, spec
+ROTATE_BYTES = 2.2e9
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(M, N, K):
+    # weights + activations + fp32 scales + fp16 outputs
+    return N * K + M * K * 2 + N * 4 + M * N * 2
+
+
+def gemm_a8w8_bytes(M, N, K):
+    return M * K + N * K + 2 * M * N + 4 * M + 4 * N
+
+
+def time_graph(fn_list, torch, stream):
+    """Capture fn_list (one launch each) in a graph, replay once, return (wall_s, event_ms)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for fn in fn_list:
+            fn()
+    torch.cuda.synchronize()
+    g.replay()                      # warm replay (graph upload)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, e0.elapsed_time(e1), g
+
+
+def load_traffic(kernel_key):
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel_key)
+    except Exception:
+        return None
+
+
+def bench_gemv(ops, torch, steps, warmup, M=1, K=4096, N=14336):
+    from esimd_learning_amd import synthetic
+    dev = "cuda:0"
+    W8, s = synthetic.weight_fp8(N, K, seed=0)
+    x = synthetic.activations(M, K, seed=1).to(dev)
+    copies = max(2, math.ceil(ROTATE_BYTES / (N * K)))
+    log(f"gemv: M={M} K={K} N={N}, {copies} weight copies ({copies * N * K / 1e9:.2f} GB)")
+    Wd = W8.to(dev)
+    Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
+    Ss = [s.to(dev).clone() for _ in range(copies)]
+    y = torch.empty(M, N, dtype=torch.float16, device=dev)
+    stream = torch.cuda.Stream()
+
+    def step(i):
+        return lambda: ops.esimd_gemv_fp8_pern(x, Ws[i % copies], Ss[i % copies], y, N, K)
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)()
+    torch.cuda.synchronize()
+    wall, ev_ms, _ = time_graph([step(i) for i in range(steps)], torch, stream)
+    nbytes = gemv_bytes(M, N, K)
+    avg_launch_us = ev_ms * 1e3 / steps
+    res = {
+        "ms_per_step": wall * 1e3 / steps,
+        "value": nbytes * steps / wall / 1e9,
+        "avg_launch_us": avg_launch_us,
+        "achieved": nbytes / (avg_launch_us * 1e-6) / 1e9,
+        "bytes": nbytes,
+    }
+    # eager launches with one event pair each (host launch cost excluded from
+    # each pair only if the queue stays ahead; reported for reference)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(64)]
+    with torch.cuda.stream(stream):
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            step(i)()
+            b.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    res["eager_event_us_median"] = per[len(per) // 2]
+    # correctness spot check against the first copy (cheap, CPU oracle at M=1)
+    return res, (x, Wd, s, y)
+
+
+def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
+    from esimd_learning_amd import synthetic
+    dev = "cuda:0"
+    log(f"gemm a8w8: M={M} K={K} N={N}")
+    x = synthetic.activations(M, K, seed=2).to(dev)
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+    sa = torch.empty(M, dtype=torch.float32, device=dev)
+    ops.esimd_per_token_quant_fp8(x, q, sa)
+    W8, sb = synthetic.weight_fp8(N, K, seed=3)
+    Wd, sbd = W8.to(dev), sb.to(dev)
+    y = torch.empty(M, N, dtype=torch.float16, device=dev)
+    stream = torch.cuda.Stream()
+    fn = lambda: ops.esimd_gemm_fp8_a8w8(q, sa, Wd, sbd, y)  # noqa: E731
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.synchronize()
+    wall, ev_ms, _ = time_graph([fn] * steps, torch, stream)
+    flops = 2.0 * M * N * K
+    us = ev_ms * 1e3 / steps
+    return {"config": f"a8w8 M={M} K={K} N={N}", "avg_launch_us": us,
+            "tflops": flops / (us * 1e-6) / 1e12,
+            "wall_tflops": flops * steps / wall / 1e12,
+            "roofline": {"bound": "mfma", "achieved": flops / (us * 1e-6) / 1e12, "peak": FP8_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": flops / (us * 1e-6) / 1e12 / FP8_PEAK_TFLOPS,
+                         "traffic": None}}
+
+
+def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
+    from esimd_learning_amd import synthetic
+    from oracle import gemv as ogemv
+    torch.set_num_threads(os.cpu_count() or 1)
+    W8, s = synthetic.weight_fp8(N, K, seed=0)
+    x = synthetic.activations(M, K, seed=1)
+    ts = []
+    for i in range(2 + reps):
+        t0 = time.perf_counter()
+        ogemv.gemv_fp8_pern(x, W8, s)
+        if i >= 2:
+            ts.append(time.perf_counter() - t0)
+    ts.sort()
+    med = ts[len(ts) // 2]
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": gemv_bytes(M, N, K) / med / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle gemv_fp8_pern (dequant fp8->fp16->fp32 + fp32 matmul + scale) on CPU, "
+                      f"M={M} K={K} N={N}, median of {reps} after 2 warm-ups, {med * 1e3:.1f} ms/call; "
+                      f"os.cpu_count()={os.cpu_count()}; cpu '{model}'"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the op pack has no "
+              f"multi-GPU path. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import esimd_learning_amd
+    ops = esimd_learning_amd.ops()
+    assert torch.cuda.is_available(), "no GPU visible"
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    g, (x, Wd, s, y) = bench_gemv(ops, torch, a.steps, a.warmup)
+    log(f"gemv: {g['avg_launch_us']:.2f} us/launch, {g['achieved']:.0f} GB/s; eager event median "
+        f"{g['eager_event_us_median']:.2f} us; wall {g['ms_per_step'] * 1e3:.2f} us/step")
+    # spot check of the measured output
+    from oracle import gemv as ogemv
+    torch.cuda.synchronize()
+    ref = ogemv.gemv_fp8_pern(x.cpu(), Wd.cpu(), s)
+    err = (y.cpu().float() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item(), f"bench output check failed: {err}"
+
+    out = {
+        "metric": "fp8 GEMV HBM GB/s & %peak (M=1,K4096,N14336); fp8 GEMM TFLOPS M=2048",
+        "value": round(g["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(g["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights quantised per row to e4m3; N(0,1) fp16 activations)",
+        "config": {"workload": "esimd_gemv_fp8_pern decode GEMV, BASELINE config 2 headline shape",
+                   "M": 1, "K": 4096, "N": 14336, "scale": "fp32 per output channel",
+                   "weight_copies_rotated_GB": round(math.ceil(ROTATE_BYTES / (4096 * 14336)) * 4096 * 14336 / 1e9, 2),
+                   "timing": "K launches captured in one HIP graph, replayed once"},
+        "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("gemv_dot_kernel_m1_k4096_n14336"),
+                     "algorithmic_bytes": g["bytes"], "avg_launch_us": round(g["avg_launch_us"], 3)},
+    }
+    if not a.no_gemm:
+        out["gemm"] = bench_gemm(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
+        log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")
+    if not a.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(torch)
+    out["host"] = platform.node()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,123 @@
+// cek_common.h -- device/host helpers shared by the gfx950 kernels.
+//
+// fp8 decode uses the gfx950 OCP conversion instructions
+// (v_cvt_scalef32_pk_{f16,bf16}_{fp8,bf8}, v_cvt_pk_f32_fp8): exact OCP
+// e4m3fn / e5m2 decoding, subnormals kept, NaN codes decode to NaN.  This is
+// the decode of the reference's torch oracle (weight_fp8.to(torch.float16),
+// tests/test_gemv_fp8.py:31), not the reference kernels' approximate decode
+// (fp8_GEMV_v2.h:15-38 flushes subnormals and maps NaN to +-480).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "cek.h"
+
+namespace cek {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int i4 __attribute__((ext_vector_type(4)));
+typedef int i8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// 16-bit activation element types, stored as raw bits.
+struct F16 {
+  static constexpr int code = CEK_F16;
+  typedef h2 pair;
+  __device__ static inline float to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+  __device__ static inline uint16_t from_f32(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+};
+struct BF16 {
+  static constexpr int code = CEK_BF16;
+  typedef bf2 pair;
+  __device__ static inline float to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+  // v_cvt_pk_bf16_f32 on gfx950: round to nearest even, NaN stays NaN.
+  __device__ static inline uint16_t from_f32(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+};
+
+// Decode the two fp8 bytes in the low (HI=false) or high (HI=true) half of
+// `w` into a pair of the activation type; FMT is CEK_E4M3 or CEK_E5M2.
+template <typename T, int FMT, bool HI>
+__device__ inline typename T::pair fp8x2_to_pair(uint32_t w);
+
+template <> __device__ inline h2 fp8x2_to_pair<F16, CEK_E4M3, false>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false); }
+template <> __device__ inline h2 fp8x2_to_pair<F16, CEK_E4M3, true>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true); }
+template <> __device__ inline h2 fp8x2_to_pair<F16, CEK_E5M2, false>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false); }
+template <> __device__ inline h2 fp8x2_to_pair<F16, CEK_E5M2, true>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true); }
+template <> __device__ inline bf2 fp8x2_to_pair<BF16, CEK_E4M3, false>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false); }
+template <> __device__ inline bf2 fp8x2_to_pair<BF16, CEK_E4M3, true>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true); }
+template <> __device__ inline bf2 fp8x2_to_pair<BF16, CEK_E5M2, false>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false); }
+template <> __device__ inline bf2 fp8x2_to_pair<BF16, CEK_E5M2, true>(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true); }
+
+// acc + a.x*b.x + a.y*b.y with fp32 accumulation (v_dot2_f32_{f16,bf16}).
+__device__ inline float dot2(h2 a, h2 b, float acc) { return __builtin_amdgcn_fdot2(a, b, acc, false); }
+__device__ inline float dot2(bf2 a, bf2 b, float acc) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false); }
+
+// C += A * B^T on one 16 x 16 x 32 MFMA block, 16-bit operands (8 per lane).
+template <typename T>
+__device__ inline f4 mfma16x16x32(u4 a, u4 b, f4 c);
+template <>
+__device__ inline f4 mfma16x16x32<F16>(u4 a, u4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f4 mfma16x16x32<BF16>(u4 a, u4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+}
+
+// Exact decode of one fp8 byte to fp32 (used by the generic paths).
+template <int FMT>
+__device__ inline float fp8_to_f32(uint32_t byte) {
+  if (FMT == CEK_E4M3) {
+    f2 v = __builtin_amdgcn_cvt_pk_f32_fp8(byte, false);
+    return v.x;
+  } else {
+    f2 v = __builtin_amdgcn_cvt_pk_f32_bf8(byte, false);
+    return v.x;
+  }
+}
+
+// fp32 -> e4m3fn byte, round to nearest even.  The input must already be
+// clamped to [-448, 448] (v_cvt_pk_fp8_f32 does not saturate otherwise).
+__device__ inline uint32_t f32_to_e4m3(float v) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xFFu;
+}
+__device__ inline uint32_t f32x4_to_e4m3x4(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// Butterfly sum over the 64 lanes of a wave; every lane gets the total.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ inline u4 load_u4(const void* p) { return *reinterpret_cast<const u4*>(p); }
+// Streaming (non-temporal) 16-byte load for data read exactly once.
+__device__ inline u4 load_u4_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+}
+
+}  // namespace cek
+
+// ---- host-side helpers ----------------------------------------------------
+namespace cek {
+int record_hip_error(hipError_t e);  // stores the message, returns CEK_ERR_HIP
+inline int check_launch() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? CEK_OK : record_hip_error(e);
+}
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+}  // namespace cek

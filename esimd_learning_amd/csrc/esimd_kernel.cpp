@@ -1,0 +1,224 @@
+// esimd_kernel.cpp -- torch shims of the GEMV, norm, quant, activation and
+// RoPE ops (takes over the reference's csrc/xpu/esimd_kernel.sycl).
+//
+// Every shim: dtype checks with the reference's messages, then the checks the
+// reference leaves out (device, contiguity, sizes), a device guard, the
+// current HIP stream of the input's device, and one C-ABI call.  Outputs are
+// written in place and returned as the reference does; nothing synchronises.
+#include "torch_ops.h"
+
+#include <algorithm>
+
+#include "shim_common.h"
+
+using namespace cek_shim;
+
+static void check_gemv_io(const at::Tensor& input, const at::Tensor& output, const char* op) {
+  TORCH_CHECK(is_io(input.scalar_type()), op, ": input must be fp16 or bf16");
+  TORCH_CHECK(is_io(output.scalar_type()), op, ": output must be fp16 or bf16");
+  TORCH_CHECK(input.scalar_type() == output.scalar_type(), op, ": input and output must have the same dtype");
+}
+
+// Rows of `input` that the op computes.  The reference kernels compute row 0
+// only (csrc/xpu/esimd_kernels/fp8_GEMV_v2.h:62-75); here every row that both
+// input and output hold, i.e. a superset that equals the reference for M = 1.
+static int64_t gemv_rows(const at::Tensor& input, const at::Tensor& output, int64_t N, int64_t K) {
+  return std::min(input.numel() / K, output.numel() / N);
+}
+
+static void run_gemv(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                     const at::Tensor& output, int64_t N, int64_t K, bool per_tensor, const char* op) {
+  check_gemv_io(input, output, op);
+  check_fp8_weight(weight, op);
+  check_device(weight, input, op, "weight");
+  check_device(scale, input, op, "weight_scale");
+  check_device(output, input, op, "output");
+  check_contig(input, op, "input");
+  check_contig(weight, op, "weight");
+  check_contig(output, op, "output");
+  check_contig(scale, op, "weight_scale");
+  TORCH_CHECK(N > 0 && K > 0, op, ": N and K must be positive");
+  TORCH_CHECK(weight.numel() >= N * K, op, ": weight holds ", weight.numel(), " elements, need N*K = ", N * K);
+  TORCH_CHECK(input.numel() >= K, op, ": input holds fewer than K elements");
+  TORCH_CHECK(output.numel() >= N, op, ": output holds fewer than N elements");
+  int scale_code = CEK_F32;
+  if (per_tensor) {
+    TORCH_CHECK(scale.scalar_type() == at::ScalarType::Float && scale.numel() >= 1, op,
+                ": weight_scale must be an fp32 scalar tensor");
+  } else {
+    const auto st = scale.scalar_type();
+    TORCH_CHECK(st == at::ScalarType::Half || st == at::ScalarType::BFloat16 || st == at::ScalarType::Float, op,
+                ": weight_scale must be fp16, bf16 or fp32");
+    TORCH_CHECK(scale.numel() >= N, op, ": weight_scale must hold N elements");
+    scale_code = st == at::ScalarType::Float ? CEK_F32 : (st == at::ScalarType::Half ? CEK_F16 : CEK_BF16);
+  }
+  const int64_t M = gemv_rows(input, output, N, K);
+  c10::OptionalDeviceGuard guard(input.device());
+  void* st = current_stream(input);
+  const int io = io_code(input.scalar_type());
+  const int fmt = fp8_code(weight);
+  const size_t esz = input.element_size();
+  // The kernels take up to 16 rows per launch; larger M is split into slabs.
+  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    const int64_t mb = std::min<int64_t>(16, M - m0);
+    const char* x = static_cast<const char*>(input.data_ptr()) + m0 * K * esz;
+    char* y = static_cast<char*>(output.data_ptr()) + m0 * N * esz;
+    int rc = per_tensor
+                 ? cek_gemv_fp8_pert(x, weight.data_ptr(), static_cast<const float*>(scale.data_ptr()), y, mb, N, K,
+                                     io, fmt, st)
+                 : cek_gemv_fp8_pern(x, weight.data_ptr(), scale.data_ptr(), y, mb, N, K, io, fmt, scale_code, st);
+    check_rc(rc, op);
+  }
+}
+
+at::Tensor esimd_gemv_fp8_pern(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                               at::Tensor output, int64_t N, int64_t K) {
+  run_gemv(input, weight, weight_scale, output, N, K, false, "esimd_gemv_fp8_pern");
+  return output;
+}
+
+at::Tensor esimd_gemv_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                               at::Tensor output) {
+  TORCH_CHECK(weight.dim() == 2, "esimd_gemv_fp8_pert: weight must be [N, K]");
+  run_gemv(input, weight, weight_scale, output, weight.size(0), weight.size(1), true, "esimd_gemv_fp8_pert");
+  return output;
+}
+
+static void check_norm(const at::Tensor& h, const at::Tensor& r, const at::Tensor& w, const char* op) {
+  TORCH_CHECK(is_io(h.scalar_type()), op, ": hidden_states must be fp16 or bf16");
+  TORCH_CHECK(r.scalar_type() == h.scalar_type() && w.scalar_type() == h.scalar_type(), op,
+              ": residual and weight must have the dtype of hidden_states");
+  check_device(r, h, op, "residual");
+  check_device(w, h, op, "weight");
+  check_contig(h, op, "hidden_states");
+  check_contig(r, op, "residual");
+  check_contig(w, op, "weight");
+  TORCH_CHECK(h.dim() >= 1 && h.size(-1) > 0, op, ": hidden_states must have a non-empty last dimension");
+  TORCH_CHECK(r.numel() == h.numel(), op, ": residual must match hidden_states");
+  TORCH_CHECK(w.numel() == h.size(-1), op, ": weight must have hidden_states.size(-1) elements");
+}
+
+at::Tensor esimd_fused_add_rms_norm_batched(at::Tensor hidden_states, at::Tensor residual,
+                                            at::Tensor weight, double eps) {
+  const char* op = "esimd_fused_add_rms_norm_batched";
+  check_norm(hidden_states, residual, weight, op);
+  const int64_t H = hidden_states.size(-1);
+  const int64_t rows = hidden_states.numel() / H;
+  c10::OptionalDeviceGuard guard(hidden_states.device());
+  check_rc(cek_fused_add_rms_norm(hidden_states.data_ptr(), residual.data_ptr(), weight.data_ptr(), rows, H,
+                                  (float)eps, io_code(hidden_states.scalar_type()), current_stream(hidden_states)),
+           op);
+  return hidden_states;
+}
+
+static void check_quant_out(const at::Tensor& ref, const at::Tensor& q, const at::Tensor& s, int64_t rows,
+                            const char* op) {
+  TORCH_CHECK(q.element_size() == 1, op, ": out_q must be an 8-bit tensor (float8_e4m3fn or uint8)");
+  TORCH_CHECK(q.scalar_type() != at::ScalarType::Float8_e5m2, op, ": out_q must be e4m3, not e5m2");
+  TORCH_CHECK(s.scalar_type() == at::ScalarType::Float, op, ": out_scale must be fp32");
+  check_device(q, ref, op, "out_q");
+  check_device(s, ref, op, "out_scale");
+  check_contig(q, op, "out_q");
+  check_contig(s, op, "out_scale");
+  TORCH_CHECK(q.numel() == ref.numel(), op, ": out_q must have as many elements as the input");
+  TORCH_CHECK(s.numel() == rows, op, ": out_scale must have one element per token (", rows, ")");
+}
+
+void esimd_fused_add_rms_norm_quant_fp8(at::Tensor hidden_states, at::Tensor residual, at::Tensor weight,
+                                        double eps, at::Tensor out_q, at::Tensor out_scale) {
+  const char* op = "esimd_fused_add_rms_norm_quant_fp8";
+  check_norm(hidden_states, residual, weight, op);
+  const int64_t H = hidden_states.size(-1);
+  const int64_t rows = hidden_states.numel() / H;
+  check_quant_out(hidden_states, out_q, out_scale, rows, op);
+  c10::OptionalDeviceGuard guard(hidden_states.device());
+  check_rc(cek_fused_add_rms_norm_quant_fp8(hidden_states.data_ptr(), residual.data_ptr(), weight.data_ptr(), rows,
+                                            H, (float)eps, io_code(hidden_states.scalar_type()),
+                                            static_cast<uint8_t*>(out_q.data_ptr()),
+                                            static_cast<float*>(out_scale.data_ptr()), current_stream(hidden_states)),
+           op);
+}
+
+void esimd_per_token_quant_fp8(at::Tensor input, at::Tensor out_q, at::Tensor out_scale) {
+  const char* op = "esimd_per_token_quant_fp8";
+  TORCH_CHECK(is_io(input.scalar_type()), op, ": input must be fp16 or bf16");
+  TORCH_CHECK(input.is_cuda(), op, ": input must be a GPU tensor");
+  check_contig(input, op, "input");
+  TORCH_CHECK(input.dim() >= 1 && input.size(-1) > 0, op, ": input must have a non-empty last dimension");
+  const int64_t H = input.size(-1);
+  const int64_t rows = input.numel() / H;
+  check_quant_out(input, out_q, out_scale, rows, op);
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_per_token_quant_fp8(input.data_ptr(), rows, H, io_code(input.scalar_type()),
+                                   static_cast<uint8_t*>(out_q.data_ptr()), static_cast<float*>(out_scale.data_ptr()),
+                                   current_stream(input)),
+           op);
+}
+
+void esimd_gelu_and_mul(at::Tensor out, at::Tensor input) {
+  const char* op = "esimd_gelu_and_mul";
+  TORCH_CHECK(is_io(input.scalar_type()) && out.scalar_type() == input.scalar_type(), op,
+              ": input and out must be fp16 or bf16 of the same dtype");
+  check_device(out, input, op, "out");
+  TORCH_CHECK(input.dim() >= 1 && input.size(-1) % 2 == 0, op, ": input's last dimension must be even");
+  const int64_t d = input.size(-1) / 2;
+  TORCH_CHECK(out.size(-1) == d, op, ": out's last dimension must be half of input's");
+  TORCH_CHECK(input.stride(-1) == 1 && out.stride(-1) == 1, op, ": last dimensions must be contiguous");
+  // Rows may be strided (e.g. a view into a wider buffer); leading dims flatten.
+  const int64_t T = input.numel() / input.size(-1);
+  TORCH_CHECK(out.numel() / d == T, op, ": out and input must have the same number of rows");
+  const int64_t xs = input.dim() >= 2 ? input.stride(-2) : 2 * d;
+  const int64_t os = out.dim() >= 2 ? out.stride(-2) : d;
+  if (input.dim() > 2) TORCH_CHECK(input.is_contiguous(), op, ": >2-D input must be contiguous");
+  if (out.dim() > 2) TORCH_CHECK(out.is_contiguous(), op, ": >2-D out must be contiguous");
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_gelu_and_mul(out.data_ptr(), input.data_ptr(), T, d, xs, os, io_code(input.scalar_type()),
+                            current_stream(input)),
+           op);
+}
+
+// q / k are [T, n * hd] or [T, n, hd] views (rows may be strided, heads
+// contiguous within a row), modified in place.
+static int64_t rows_and_stride(const at::Tensor& t, int64_t hd, int64_t& n_heads, const char* op,
+                               const char* name) {
+  TORCH_CHECK(t.dim() == 2 || t.dim() == 3, op, ": ", name, " must be [T, n*hd] or [T, n, hd]");
+  TORCH_CHECK(t.stride(-1) == 1, op, ": ", name, "'s last dimension must be contiguous");
+  if (t.dim() == 3) {
+    TORCH_CHECK(t.size(2) == hd && t.stride(1) == hd, op, ": ", name, " heads must be contiguous of size hd");
+    n_heads = t.size(1);
+  } else {
+    TORCH_CHECK(t.size(1) % hd == 0, op, ": ", name, "'s width must be a multiple of head_dim");
+    n_heads = t.size(1) / hd;
+  }
+  return t.stride(0);
+}
+
+void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions,
+                        double eps, double theta, bool is_neox) {
+  const char* op = "esimd_qk_norm_rope";
+  TORCH_CHECK(is_io(q.scalar_type()), op, ": q must be fp16 or bf16");
+  TORCH_CHECK(k.scalar_type() == q.scalar_type() && q_weight.scalar_type() == q.scalar_type() &&
+                  k_weight.scalar_type() == q.scalar_type(),
+              op, ": q, k and the weights must share one dtype");
+  TORCH_CHECK(positions.scalar_type() == at::ScalarType::Long, op, ": positions must be int64");
+  check_device(k, q, op, "k");
+  check_device(q_weight, q, op, "q_weight");
+  check_device(k_weight, q, op, "k_weight");
+  check_device(positions, q, op, "positions");
+  check_contig(q_weight, op, "q_weight");
+  check_contig(k_weight, op, "k_weight");
+  check_contig(positions, op, "positions");
+  const int64_t hd = q_weight.numel();
+  TORCH_CHECK(k_weight.numel() == hd, op, ": q_weight and k_weight must both have head_dim elements");
+  TORCH_CHECK(hd > 0 && hd % 2 == 0 && hd <= 512, op, ": head_dim must be even and <= 512");
+  int64_t nq = 0, nk = 0;
+  const int64_t qs = rows_and_stride(q, hd, nq, op, "q");
+  const int64_t ks = rows_and_stride(k, hd, nk, op, "k");
+  const int64_t T = q.size(0);
+  TORCH_CHECK(k.size(0) == T && positions.numel() == T, op, ": q, k and positions must have T rows");
+  c10::OptionalDeviceGuard guard(q.device());
+  check_rc(cek_qk_norm_rope(q.data_ptr(), k.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(),
+                            static_cast<const int64_t*>(positions.data_ptr()), T, nq, nk, hd, qs, ks, (float)eps,
+                            (float)theta, is_neox ? 1 : 0, io_code(q.scalar_type()), current_stream(q)),
+           op);
+}

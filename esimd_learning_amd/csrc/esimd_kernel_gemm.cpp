@@ -1,0 +1,70 @@
+// esimd_kernel_gemm.cpp -- torch shims of the GEMM ops (takes over the
+// reference's csrc/xpu/esimd_kernel_gemm.sycl).
+//
+// esimd_gemm_fp8_pert keeps the reference's contract (fp16|bf16 input and
+// output of one dtype, fp8 weight, fp32 scalar scale, N and K from the weight,
+// M from the input).  The reference converts bf16 input to fp16 and back
+// around its fp16-only kernels (esimd_kernel_gemm.sycl:43-48,61-63); here the
+// kernels take bf16 directly, so no temporaries are allocated.
+#include "torch_ops.h"
+
+#include "shim_common.h"
+
+using namespace cek_shim;
+
+at::Tensor esimd_gemm_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                               at::Tensor output) {
+  const char* op = "esimd_gemm_fp8_pert";
+  TORCH_CHECK(is_io(input.scalar_type()), op, ": input must be fp16 or bf16");
+  TORCH_CHECK(is_io(output.scalar_type()), op, ": output must be fp16 or bf16");
+  TORCH_CHECK(input.scalar_type() == output.scalar_type(), op, ": input and output must have the same dtype");
+  check_fp8_weight(weight, op);
+  TORCH_CHECK(weight.dim() == 2, op, ": weight must be [N, K]");
+  check_device(weight, input, op, "weight");
+  check_device(weight_scale, input, op, "weight_scale");
+  check_device(output, input, op, "output");
+  check_contig(input, op, "input");
+  check_contig(weight, op, "weight");
+  check_contig(output, op, "output");
+  TORCH_CHECK(weight_scale.scalar_type() == at::ScalarType::Float && weight_scale.numel() >= 1, op,
+              ": weight_scale must be an fp32 scalar tensor");
+  const int64_t N = weight.size(0), K = weight.size(1);
+  TORCH_CHECK(N > 0 && K > 0, op, ": weight must be non-empty");
+  TORCH_CHECK(input.numel() % K == 0, op, ": input's element count must be a multiple of K");
+  const int64_t M = input.numel() / K;
+  TORCH_CHECK(output.numel() >= M * N, op, ": output must hold M*N elements");
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_gemm_fp8_pert(input.data_ptr(), weight.data_ptr(), static_cast<const float*>(weight_scale.data_ptr()),
+                             output.data_ptr(), M, N, K, io_code(input.scalar_type()), fp8_code(weight),
+                             current_stream(input)),
+           op);
+  return output;
+}
+
+at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
+                               at::Tensor output) {
+  const char* op = "esimd_gemm_fp8_a8w8";
+  TORCH_CHECK(a.element_size() == 1 && b.element_size() == 1, op, ": a and b must be 8-bit (e4m3) tensors");
+  TORCH_CHECK(a.scalar_type() != at::ScalarType::Float8_e5m2 && b.scalar_type() != at::ScalarType::Float8_e5m2, op,
+              ": a and b must be e4m3");
+  TORCH_CHECK(a_scale.scalar_type() == at::ScalarType::Float && b_scale.scalar_type() == at::ScalarType::Float, op,
+              ": scales must be fp32");
+  TORCH_CHECK(is_io(output.scalar_type()), op, ": output must be fp16 or bf16");
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2 && a.size(1) == b.size(1), op, ": a [M, K] and b [N, K] required");
+  for (auto* t : {&a_scale, &b, &b_scale, &output}) check_device(*t, a, op, "operand");
+  check_contig(a, op, "a");
+  check_contig(b, op, "b");
+  check_contig(a_scale, op, "a_scale");
+  check_contig(b_scale, op, "b_scale");
+  check_contig(output, op, "output");
+  const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
+  TORCH_CHECK(K % 16 == 0, op, ": K must be a multiple of 16");
+  TORCH_CHECK(a_scale.numel() == M && b_scale.numel() == N, op, ": a_scale [M] and b_scale [N] required");
+  TORCH_CHECK(output.numel() == M * N, op, ": output must be [M, N]");
+  c10::OptionalDeviceGuard guard(a.device());
+  check_rc(cek_gemm_fp8_a8w8(static_cast<const uint8_t*>(a.data_ptr()), static_cast<const float*>(a_scale.data_ptr()),
+                             static_cast<const uint8_t*>(b.data_ptr()), static_cast<const float*>(b_scale.data_ptr()),
+                             output.data_ptr(), M, N, K, io_code(output.scalar_type()), current_stream(a)),
+           op);
+  return output;
+}

@@ -1,0 +1,36 @@
+// torch_ops.h -- at::Tensor entry points of the custom_esimd_kernels_vllm ops.
+//
+// The first four keep the reference's C++ signatures (reference
+// include/kernel_ops.h:11-14,17-19,21-23,28-30); the rest are new ops in the
+// same namespace.  Each shim validates its tensors, takes the current HIP
+// stream of the input's device and calls the C ABI in include/cek.h.
+#pragma once
+
+#include <ATen/ATen.h>
+
+at::Tensor esimd_gemv_fp8_pern(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                               at::Tensor output, int64_t N, int64_t K);
+
+at::Tensor esimd_gemv_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                               at::Tensor output);
+
+at::Tensor esimd_fused_add_rms_norm_batched(at::Tensor hidden_states, at::Tensor residual,
+                                            at::Tensor weight, double eps);
+
+at::Tensor esimd_gemm_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                               at::Tensor output);
+
+// ---- new ops (no reference counterpart) ----
+void esimd_fused_add_rms_norm_quant_fp8(at::Tensor hidden_states, at::Tensor residual,
+                                        at::Tensor weight, double eps, at::Tensor out_q,
+                                        at::Tensor out_scale);
+
+void esimd_per_token_quant_fp8(at::Tensor input, at::Tensor out_q, at::Tensor out_scale);
+
+void esimd_gelu_and_mul(at::Tensor out, at::Tensor input);
+
+void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Tensor k_weight,
+                        at::Tensor positions, double eps, double theta, bool is_neox);
+
+at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
+                               at::Tensor output);

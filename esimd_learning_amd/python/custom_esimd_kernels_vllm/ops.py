@@ -1,0 +1,101 @@
+"""Python wrappers of the ``torch.ops.custom_esimd_kernels_vllm`` ops.
+
+The first four keep the reference's names, signatures and forwarding
+(reference python/custom_esimd_kernels_vllm/ops.py:7-67); the docstrings
+state this build's contract.  The rest wrap the new ops of the same
+namespace.
+"""
+
+import torch
+
+_ops = torch.ops.custom_esimd_kernels_vllm
+
+
+def esimd_gemv_fp8_pern(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+    output: torch.Tensor,
+    N: int, K: int,
+) -> torch.Tensor:
+    """fp8-weight GEMV with a per-output-channel scale, fp32 accumulation.
+
+    input/output: [M, K]/[M, N] fp16 or bf16 of one dtype (every row is
+    computed; the reference computes row 0); weight: [N, K] float8_e4m3fn or
+    float8_e5m2; weight_scale: [N] fp16, bf16 or fp32.  Returns ``output``.
+    """
+    return _ops.esimd_gemv_fp8_pern(input, weight, weight_scale, output, N, K)
+
+
+def esimd_gemv_fp8_pert(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+    output: torch.Tensor,
+) -> torch.Tensor:
+    """fp8-weight GEMV with a per-tensor fp32 scale (read on the device).
+
+    N and K are taken from weight's shape.  Returns ``output``.
+    """
+    return _ops.esimd_gemv_fp8_pert(input, weight, weight_scale, output)
+
+
+def esimd_fused_add_rms_norm_batched(
+    hidden_states: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float,
+) -> torch.Tensor:
+    """Batched fused residual add + RMSNorm (Gemma-style), in place.
+
+    residual = hidden_states + residual; hidden_states = rmsnorm(residual) *
+    weight, with weight already shifted (w + 1.0).  Any number of rows.
+    Returns ``hidden_states``.
+    """
+    return _ops.esimd_fused_add_rms_norm_batched(hidden_states, residual, weight, eps)
+
+
+def esimd_gemm_fp8_pert(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+    output: torch.Tensor,
+) -> torch.Tensor:
+    """fp8-weight GEMM with a per-tensor fp32 scale, any M.
+
+    input/output: [M, K]/[M, N] fp16 or bf16 of one dtype; weight [N, K] fp8.
+    M <= 16 runs the decode GEMV kernels, larger M the MFMA GEMM.
+    """
+    return _ops.esimd_gemm_fp8_pert(input, weight, weight_scale, output)
+
+
+# ---- new ops -------------------------------------------------------------
+
+def esimd_fused_add_rms_norm_quant_fp8(
+    hidden_states: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+    out_q: torch.Tensor, out_scale: torch.Tensor,
+) -> None:
+    """residual += hidden_states (in place); per-token e4m3 codes of
+    rmsnorm(residual) * weight into out_q [T, H] and fp32 scales into
+    out_scale [T].  hidden_states is only read."""
+    _ops.esimd_fused_add_rms_norm_quant_fp8(hidden_states, residual, weight, eps, out_q, out_scale)
+
+
+def esimd_per_token_quant_fp8(input: torch.Tensor, out_q: torch.Tensor, out_scale: torch.Tensor) -> None:
+    """Per-token e4m3 quantisation: out_scale[t] = max(amax_t / 448, 1/(448*512))."""
+    _ops.esimd_per_token_quant_fp8(input, out_q, out_scale)
+
+
+def esimd_gelu_and_mul(out: torch.Tensor, input: torch.Tensor) -> None:
+    """out = gelu_tanh(input[..., :d]) * input[..., d:]."""
+    _ops.esimd_gelu_and_mul(out, input)
+
+
+def esimd_qk_norm_rope(
+    q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+    positions: torch.Tensor, eps: float, theta: float = 10000.0, is_neox: bool = True,
+) -> None:
+    """Per-head RMSNorm then rotary embedding of q and k, in place."""
+    _ops.esimd_qk_norm_rope(q, k, q_weight, k_weight, positions, eps, theta, is_neox)
+
+
+def esimd_gemm_fp8_a8w8(
+    a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
+    output: torch.Tensor,
+) -> torch.Tensor:
+    """output[m, n] = a_scale[m] * b_scale[n] * sum_k a[m, k] * b[n, k] (e4m3 x e4m3)."""
+    return _ops.esimd_gemm_fp8_a8w8(a, a_scale, b, b_scale, output)

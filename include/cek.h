@@ -1,0 +1,140 @@
+/*
+ * cek.h -- C ABI of the MI355X (gfx950) fp8 decode/prefill op pack.
+ *
+ * Library: libcek.so (built with hipcc --offload-arch=gfx950).
+ * All pointers are HIP device pointers unless stated; sizes are element
+ * counts; `stream` is a hipStream_t passed as void* (NULL = legacy default
+ * stream).  Every entry point only enqueues work on `stream`: no host
+ * synchronisation, no host read of device scales, no allocation.  Entry
+ * points are stateless and re-entrant.  Return value: CEK_OK (0) or a
+ * CEK_ERR_* code; cek_error_string() names it.  Nothing throws across the
+ * ABI.
+ *
+ * The reference (Intel-XPU SYCL-ESIMD package custom_esimd_kernels_vllm)
+ * has no C ABI: its boundary is torch ops whose host shims extract raw
+ * pointers and launch kernels.  Each entry point below names the reference
+ * shim / host function it takes over (paths relative to the reference
+ * repository root).  Functions marked NEW have no reference counterpart.
+ */
+#ifndef CEK_H
+#define CEK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of activation / output tensors */
+enum cek_dtype { CEK_F16 = 0, CEK_BF16 = 1, CEK_F32 = 2 };
+/* fp8 weight encodings (reference get_fp8_mode, csrc/xpu/esimd_kernel.sycl:14-16) */
+enum cek_fp8 { CEK_E4M3 = 0, CEK_E5M2 = 1 };
+
+enum cek_status {
+  CEK_OK = 0,
+  CEK_ERR_INVALID = 1,      /* bad size, pointer, alignment or enum value */
+  CEK_ERR_UNSUPPORTED = 2,  /* valid request this build has no kernel for */
+  CEK_ERR_HIP = 3           /* a HIP runtime call or launch failed */
+};
+
+const char* cek_error_string(int status);
+/* Last HIP error message seen by this thread (empty string if none). */
+const char* cek_last_hip_error(void);
+/* ABI version: major * 10000 + minor * 100 + patch. */
+int cek_version(void);
+
+/*
+ * fp8-weight GEMV with per-output-channel scale, M <= 16 rows.
+ *   y[m, n] = Out( (sum_k f32(x[m, k]) * dq(w[n, k])) * f32(scale[n]) )
+ * x [M, K] io_dtype (F16|BF16), w [N, K] fp8 row-major (K contiguous),
+ * scale [N] of scale_dtype (F16|BF16|F32), y [M, N] io_dtype.
+ * Replaces esimd_gemv_fp8_pern, csrc/xpu/esimd_kernel.sycl:22-53 ->
+ * GEMV_fp8_pern_host, csrc/xpu/esimd_kernels/fp8_GEMV_v2.h:127-191 (which
+ * computes row 0 only; here every row m < M).
+ */
+int cek_gemv_fp8_pern(const void* x, const void* w, const void* scale, void* y,
+                      int64_t M, int64_t N, int64_t K,
+                      int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+
+/*
+ * Same with a per-tensor fp32 scale read on the device (*scale).
+ * Replaces esimd_gemv_fp8_pert, csrc/xpu/esimd_kernel.sycl:57-89 ->
+ * GEMV_fp8_pert_host, csrc/xpu/esimd_kernels/fp8_GEMV_v2.h:370-434.
+ */
+int cek_gemv_fp8_pert(const void* x, const void* w, const float* scale, void* y,
+                      int64_t M, int64_t N, int64_t K,
+                      int io_dtype, int fp8_fmt, void* stream);
+
+/*
+ * fp8-weight GEMM, fp16|bf16 activations, per-tensor fp32 scale, any M.
+ *   Y[m, n] = Out( (sum_k f32(X[m, k]) * dq(W[n, k])) * (*scale) )
+ * M <= 16 uses the GEMV kernels; larger M a w8a16 MFMA GEMM.
+ * Replaces esimd_gemm_fp8_pert, csrc/xpu/esimd_kernel_gemm.sycl:23-65 ->
+ * GEMM_fp8_pert_dispatch, csrc/xpu/esimd_kernels/fp8_GEMM_pert.h:4017-4062.
+ */
+int cek_gemm_fp8_pert(const void* x, const void* w, const float* scale, void* y,
+                      int64_t M, int64_t N, int64_t K,
+                      int io_dtype, int fp8_fmt, void* stream);
+
+/*
+ * Batched fused residual add + RMSNorm, in place:
+ *   residual = f16(hidden + residual);
+ *   hidden   = f16(residual * rsqrt(mean((hidden+residual)^2) + eps) * weight)
+ * hidden, residual [rows, H] io_dtype; weight [H] io_dtype (Gemma w+1).
+ * Replaces esimd_fused_add_rms_norm_batched, csrc/xpu/esimd_kernel.sycl:92-109
+ * -> fused_add_rms_norm_batched_host,
+ * csrc/xpu/esimd_kernels/fused_add_rms_norm_batched.h:66-76.
+ */
+int cek_fused_add_rms_norm(void* hidden, void* residual, const void* weight,
+                           int64_t rows, int64_t H, float eps, int io_dtype, void* stream);
+
+/*
+ * NEW: fused residual add + RMSNorm + per-token e4m3 quantisation.
+ * residual is updated as above; hidden is only read.  The normed row is
+ * rounded to io_dtype, then
+ *   scale[t] = max(amax_t / 448, 1 / (448 * 512))     (fp32)
+ *   q[t, i]  = e4m3_rne(clamp(normed[t, i] / scale[t], -448, 448))
+ * q [rows, H] bytes; scale [rows] fp32.  Equal, bit for bit, to
+ * cek_fused_add_rms_norm followed by cek_per_token_quant_fp8.
+ */
+int cek_fused_add_rms_norm_quant_fp8(const void* hidden, void* residual, const void* weight,
+                                     int64_t rows, int64_t H, float eps, int io_dtype,
+                                     uint8_t* q, float* scale, void* stream);
+
+/* NEW: per-token e4m3 quantisation of x [rows, H] (same formula as above). */
+int cek_per_token_quant_fp8(const void* x, int64_t rows, int64_t H, int io_dtype,
+                            uint8_t* q, float* scale, void* stream);
+
+/*
+ * NEW: a8w8 GEMM on fp8 MFMA.
+ *   Y[m, n] = Out( sa[m] * sb[n] * sum_k dq(A[m, k]) * dq(B[n, k]) )
+ * A [M, K], B [N, K] e4m3 row-major; sa [M], sb [N] fp32; Y [M, N] out_dtype
+ * (F16|BF16).  K % 16 == 0.
+ */
+int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
+                      void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
+
+/*
+ * NEW: out[t, i] = gelu_tanh(x[t, i]) * x[t, d + i], fp32 math.
+ * x rows have stride x_stride elements (>= 2d), out rows out_stride (>= d).
+ */
+int cek_gelu_and_mul(void* out, const void* x, int64_t T, int64_t d,
+                     int64_t x_stride, int64_t out_stride, int io_dtype, void* stream);
+
+/*
+ * NEW: per-head RMSNorm (weight qw / kw of length head_dim, Gemma w+1) then
+ * rotary embedding, in place on q [T, n_q * head_dim] and
+ * k [T, n_k * head_dim] (row strides q_stride / k_stride elements, so both
+ * may be views into one QKV buffer).  positions [T] int64 on the device.
+ * is_neox != 0: rotate-half pairs (i, i + hd/2); else interleaved (2i, 2i+1).
+ */
+int cek_qk_norm_rope(void* q, void* k, const void* qw, const void* kw, const int64_t* positions,
+                     int64_t T, int64_t n_q, int64_t n_k, int64_t head_dim,
+                     int64_t q_stride, int64_t k_stride, float eps, float theta,
+                     int is_neox, int io_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CEK_H */

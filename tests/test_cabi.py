@@ -1,0 +1,111 @@
+"""C ABI (include/cek.h, libcek.so): load, exports, host-side argument checks.
+
+CPU tests: the library loads, exports every function the header declares,
+the ctypes signatures cover exactly those, and invalid arguments are rejected
+on the host before any GPU work.  GPU tests: calls through the C ABI with
+device pointers agree with the torch ops and the oracle.
+"""
+
+import ctypes as C
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_fp
+from esimd_learning_amd import LIBCEK, cabi, synthetic
+from oracle import gemv as ogemv
+from oracle import norm as onorm
+
+
+def test_library_exports_header_functions():
+    assert LIBCEK.exists(), "libcek.so not built"
+    declared = cabi.header_functions()
+    assert len(declared) >= 12
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIBCEK)], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.split()[-2:-1] == ["T"]}
+    missing = [f for f in declared if f not in exported]
+    assert not missing, missing
+    assert sorted(cabi.SIGNATURES) == declared
+
+
+def test_library_loads_and_reports():
+    lib = cabi.load()
+    assert lib.cek_version() == 100
+    assert lib.cek_error_string(cabi.CEK_OK) == b"ok"
+    assert b"invalid" in lib.cek_error_string(cabi.CEK_ERR_INVALID)
+    assert lib.cek_last_hip_error() == b""
+
+
+def test_host_rejects_invalid_arguments():
+    """Argument checks return before any HIP call, so they run without a GPU."""
+    lib = cabi.load()
+    p = C.c_void_p(16)   # never dereferenced: every call below fails validation first
+    E = cabi.CEK_ERR_INVALID
+    assert lib.cek_gemv_fp8_pern(p, p, p, p, 17, 8, 64, 0, 0, 2, None) == E          # M > 16
+    assert lib.cek_gemv_fp8_pern(p, p, p, p, 1, 8, 64, 0, 0, 7, None) == E           # scale dtype
+    assert lib.cek_gemv_fp8_pert(p, p, p, p, 1, 8, 0, 0, 0, None) == E               # K = 0
+    assert lib.cek_gemv_fp8_pert(None, p, p, p, 1, 8, 64, 0, 0, None) == E           # null x
+    assert lib.cek_gemv_fp8_pert(p, p, p, p, 1, 8, 64, 5, 0, None) == E              # io dtype
+    assert lib.cek_gemm_fp8_pert(p, p, p, p, 1, 8, 64, 0, 9, None) == E              # fp8 fmt
+    assert lib.cek_gemm_fp8_a8w8(p, p, p, p, p, 4, 4, 40, 0, None) == E              # K % 16
+    assert lib.cek_gemm_fp8_a8w8(C.c_void_p(17), p, p, p, p, 4, 4, 64, 0, None) == E  # alignment
+    assert lib.cek_fused_add_rms_norm(p, p, p, 4, 0, 1e-6, 0, None) == E             # H = 0
+    assert lib.cek_fused_add_rms_norm_quant_fp8(p, p, p, 4, 64, 1e-6, 0, None, p, None) == E
+    assert lib.cek_per_token_quant_fp8(p, -1, 64, 0, p, p, None) == E
+    assert lib.cek_gelu_and_mul(p, p, 4, 64, 100, 64, 0, None) == E                  # x stride < 2d
+    assert lib.cek_qk_norm_rope(p, p, p, p, p, 4, 2, 2, 1024, 2048, 2048, 1e-6, 1e4, 1, 0, None) == E
+    assert lib.cek_qk_norm_rope(p, p, p, p, p, 4, 2, 2, 128, 100, 256, 1e-6, 1e4, 1, 0, None) == E
+    # empty problems are no-ops that succeed without touching memory
+    assert lib.cek_gemv_fp8_pern(None, None, None, None, 0, 8, 64, 0, 0, 2, None) == cabi.CEK_OK
+    assert lib.cek_fused_add_rms_norm(None, None, None, 0, 64, 1e-6, 0, None) == cabi.CEK_OK
+
+
+# ------------------------------------------------------------------ GPU
+@pytest.mark.gpu
+def test_cabi_gemv_matches_torch_op(ops, dev):
+    lib = cabi.load()
+    M, K, N = 3, 4096, 2048
+    W8, s = synthetic.weight_fp8(N, K, seed=21)
+    x = synthetic.activations(M, K, seed=22)
+    xd, wd, sd = x.to(dev), W8.to(dev), s.to(dev)
+    y1 = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    y2 = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    cabi.check(lib.cek_gemv_fp8_pern(cabi.ptr(xd), cabi.ptr(wd), cabi.ptr(sd), cabi.ptr(y1), M, N, K,
+                                     cabi.CEK_F16, cabi.CEK_E4M3, cabi.CEK_F32, cabi.stream_ptr()))
+    ops.esimd_gemv_fp8_pern(xd, wd, sd, y2, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert_close_fp(y1.cpu(), ogemv.gemv_fp8_pern(x, W8, s), "cabi gemv")
+
+
+@pytest.mark.gpu
+def test_cabi_norm_quant_on_side_stream(ops, dev):
+    lib = cabi.load()
+    T, H = 8, 4096
+    h = synthetic.activations(T, H, seed=31)
+    r = synthetic.activations(T, H, seed=32)
+    w = synthetic.norm_weight(H)
+    hd, rd, wd = h.to(dev), r.to(dev), w.to(dev)
+    q = torch.empty(T, H, dtype=torch.uint8, device=dev)
+    s = torch.empty(T, dtype=torch.float32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        cabi.check(lib.cek_fused_add_rms_norm_quant_fp8(cabi.ptr(hd), cabi.ptr(rd), cabi.ptr(wd), T, H, 1e-6,
+                                                        cabi.CEK_F16, cabi.ptr(q), cabi.ptr(s),
+                                                        cabi.stream_ptr(side)))
+    side.synchronize()
+    r_ref, _, s_ref, _ = onorm.fused_add_rms_norm_quant(h, r, w, 1e-6)
+    assert torch.equal(rd.cpu(), r_ref)
+    assert np.allclose(s.cpu().numpy(), s_ref.numpy(), rtol=1e-3)
+
+
+@pytest.mark.gpu
+def test_cabi_error_string_after_invalid(ops, dev):
+    lib = cabi.load()
+    rc = lib.cek_gemv_fp8_pern(None, None, None, None, 1, 8, 64, 0, 0, 2, None)
+    assert rc == cabi.CEK_ERR_INVALID
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        cabi.check(rc)

@@ -1,0 +1,110 @@
+"""GPU parity of the fp8 GEMMs.
+
+esimd_gemm_fp8_pert: the reference's GEMM test grid (reference
+tests/test_gemm_fp8.py:13-23: M in {1..64} x 6 (N, K), e4m3/e5m2,
+fp16/bf16 IO, scale 0.05..0.15) plus prefill M.
+esimd_gemm_fp8_a8w8: BASELINE config 4 at M = 512 against the CPU oracle,
+and at M = 2048 against a float32 torch GPU matmul of the dequantised codes
+(the oracle's formula on the GPU; the CPU oracle at that size takes minutes).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_fp
+from esimd_learning_amd import synthetic
+from oracle import gemm as ogemm
+from oracle import gemv as ogemv
+from oracle import norm as onorm
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+REF_SHAPES = [(2560, 2048), (512, 2048), (2048, 512), (128, 2048), (3072, 2048), (1024, 1024)]
+
+
+@pytest.mark.parametrize("fmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("io", [torch.float16, torch.bfloat16])
+def test_gemm_pert_reference_grid(ops, dev, fmt, io):
+    g = torch.Generator().manual_seed(0)
+    for N, K in REF_SHAPES:
+        for M in (1, 2, 4, 8, 16, 32, 64):
+            _say(f"gemm pert M={M} N={N} K={K} {fmt} {io}")
+            W8 = (torch.randn(N, K, generator=g).half() * 0.1).to(fmt)
+            sv = torch.tensor(0.05 + torch.rand(1, generator=g).item() * 0.1)
+            x = (torch.randn(M, K, generator=g) * 0.1).to(io)
+            y = torch.zeros(M, N, dtype=io, device=dev)
+            ops.esimd_gemm_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+            torch.cuda.synchronize()
+            assert_close_fp(y.cpu(), ogemv.gemm_fp8_pert(x, W8, sv), f"M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 4096, 6144), (512, 4096, 4096), (100, 1000, 300), (33, 64, 17)])
+def test_gemm_pert_prefill(ops, dev, M, K, N):
+    _say(f"gemm pert prefill M={M} K={K} N={N}")
+    W8, _ = synthetic.weight_fp8(N, K, seed=M)
+    x = synthetic.activations(M, K, seed=M + 1)
+    sv = torch.tensor(0.01)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemm_fp8_pert(x, W8, sv), f"prefill M={M}")
+
+
+def _a8w8_inputs(M, K, N, seed):
+    x = synthetic.activations(M, K, seed=seed)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=seed + 1)
+    return q, sa, W8.view(torch.uint8), sb
+
+
+@pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 28672), (14336, 4096)])
+def test_a8w8_config4_m512(ops, dev, K, N):
+    M = 512
+    _say(f"a8w8 M={M} K={K} N={N}")
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=K + N)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemm.gemm_a8w8(q, sa, W8, sb), f"a8w8 K={K} N={N}")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 6144), (14336, 4096)])
+def test_a8w8_m2048_vs_gpu_fp32(ops, dev, K, N):
+    M = 2048
+    _say(f"a8w8 M={M} K={K} N={N} vs fp32 torch")
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=K)
+    qd, Wd = q.to(dev), W8.to(dev)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_a8w8(qd, sa.to(dev), Wd, sb.to(dev), y)
+    A = qd.view(torch.float8_e4m3fn).float()
+    B = Wd.view(torch.float8_e4m3fn).float()
+    ref = (A @ B.T) * sa.to(dev)[:, None] * sb.to(dev)[None, :]
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ref.cpu(), f"a8w8 M=2048 K={K} N={N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 16), (17, 48, 33), (64, 256, 64), (130, 1040, 250)])
+def test_a8w8_ragged(ops, dev, M, K, N):
+    _say(f"a8w8 ragged M={M} K={K} N={N}")
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M * 31 + K)
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.zeros(M, N, dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ogemm.gemm_a8w8(q, sa, W8, sb), f"ragged {out_dt}")
+
+
+def test_a8w8_rejects_bad_k(ops, dev):
+    a = torch.zeros(4, 40, dtype=torch.uint8, device=dev)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        ops.esimd_gemm_fp8_a8w8(a, torch.ones(4, device=dev), a, torch.ones(4, device=dev),
+                                torch.zeros(4, 4, dtype=torch.float16, device=dev))

@@ -1,0 +1,166 @@
+"""GPU parity of fused add+RMSNorm, per-token fp8 quant and their fusion.
+
+* residual output: bit-exact (f16(h + r) is fully determined);
+* normed output: within the op tolerance of the oracle;
+* quantised codes: bit-exact against the oracle given the kernel's own input
+  values and fp32 scale (per-token quant), ties counted and reported;
+* the fused norm+quant: bit-identical to norm followed by quant on the GPU.
+Shapes: BASELINE config 3 (T in {1,8,32,64}, H in {4096,5120}), the
+reference's norm test sizes (reference
+tests/test_fused_add_rms_norm_batched_fp8.py:34), and odd H for the scalar
+path.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_fp
+from esimd_learning_amd import synthetic
+from oracle import fp8 as ofp8
+from oracle import norm as onorm
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _inputs(T, H, dtype=torch.float16, seed=0):
+    h = synthetic.activations(T, H, seed=seed, dtype=dtype)
+    r = synthetic.activations(T, H, seed=seed + 1, dtype=dtype)
+    w = synthetic.norm_weight(H, seed=seed + 2, dtype=dtype)
+    return h, r, w
+
+
+CASES = [(T, H) for T in (1, 8, 32, 64) for H in (4096, 5120)] + \
+        [(1, 512), (1, 1024), (1, 2048), (3, 100), (5, 8200), (2, 16384)]
+
+
+@pytest.mark.parametrize("T,H", CASES)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_add_rms_norm(ops, dev, T, H, dtype):
+    _say(f"add_rmsnorm T={T} H={H} {dtype}")
+    h, r, w = _inputs(T, H, dtype, seed=T + H)
+    hd, rd = h.to(dev), r.to(dev)
+    out = ops.esimd_fused_add_rms_norm_batched(hd, rd, w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == hd.data_ptr()
+    r_ref, n_ref = onorm.fused_add_rms_norm(h, r, w, 1e-6)
+    assert torch.equal(rd.cpu(), r_ref), "residual must be bit-exact"
+    assert_close_fp(hd.cpu(), n_ref, f"normed T={T} H={H}")
+    # count elements whose rounding differs from the oracle's rounding
+    diff = (hd.cpu() != n_ref.to(dtype)).sum().item()
+    print(f"  normed elements differing from oracle rounding: {diff} / {T * H}")
+
+
+def test_norm_reference_case(ops, dev):
+    # reference tests/test_fused_add_rms_norm_batched_fp8.py:36-58: seed 42,
+    # weight randn * 0.1 (not shifted), max abs diff < 0.1 on the normed output
+    torch.manual_seed(42)
+    for K in (512, 1024, 2048, 4096):
+        h = torch.randn(1, K, dtype=torch.float16)
+        r = torch.randn(1, K, dtype=torch.float16)
+        w = torch.randn(K, dtype=torch.float16) * 0.1
+        hd, rd = h.to(dev), r.to(dev)
+        ops.esimd_fused_add_rms_norm_batched(hd, rd, w.to(dev), 1e-6)
+        torch.cuda.synchronize()
+        _, ref = onorm.fused_add_rms_norm_testformula(h, r, w, 1e-6)
+        assert (hd.cpu().float() - ref).abs().max().item() < 0.1
+
+
+def _quant_check(x, q, s):
+    """Codes bit-exact given the kernel's scale; returns (#ties, #elements)."""
+    xf = x.float().numpy()
+    s_np = s.numpy()
+    q_ref, s_ref = ofp8.per_token_quant(xf)
+    assert np.array_equal(s_np.view(np.uint32), s_ref.view(np.uint32)), "scales must be bit-exact"
+    v = np.clip((xf / s_np[:, None]).astype(np.float32), -448, 448).astype(np.float32)
+    ties = int(ofp8.e4m3_is_tie(v).sum())
+    mism = q.numpy() != q_ref
+    assert not mism.any(), f"{int(mism.sum())} code mismatches ({ties} ties in input)"
+    return ties, v.size
+
+
+@pytest.mark.parametrize("T,H", [(1, 4096), (8, 4096), (64, 5120), (4, 100), (2048, 4096), (3, 14336)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_per_token_quant_bit_exact(ops, dev, T, H, dtype):
+    _say(f"per_token_quant T={T} H={H} {dtype}")
+    x = synthetic.activations(T, H, seed=T * 3 + H, dtype=dtype)
+    if T > 2:
+        x[1] = 0                                 # zero row -> floor scale
+    q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(T, dtype=torch.float32, device=dev)
+    ops.esimd_per_token_quant_fp8(x.to(dev), q, s)
+    torch.cuda.synchronize()
+    ties, n = _quant_check(x, q.view(torch.uint8).cpu(), s.cpu())
+    print(f"  ties: {ties} of {n}")
+
+
+def test_quant_ties_and_subnormals(ops, dev):
+    """Inputs built to land exactly on e4m3 midpoints and in the subnormal range."""
+    pos = np.unique(np.abs(ofp8.E4M3_TABLE[np.isfinite(ofp8.E4M3_TABLE)])).astype(np.float64)
+    mids = (pos[1:] + pos[:-1]) / 2                   # 125 exact midpoints
+    row = np.concatenate([[448.0], mids, -mids, pos, -pos]).astype(np.float32)
+    H = (len(row) + 7) // 8 * 8
+    x = np.zeros((1, H), dtype=np.float32)
+    x[0, :len(row)] = row
+    # fp32 values are not all fp16-representable; use those that are (s = 1 exactly)
+    xt = torch.from_numpy(x).half()
+    assert (xt.float().numpy() == x).mean() > 0.9
+    q = torch.empty(1, H, dtype=torch.uint8, device=dev)
+    s = torch.empty(1, dtype=torch.float32, device=dev)
+    ops.esimd_per_token_quant_fp8(xt.to(dev), q, s)
+    torch.cuda.synchronize()
+    assert s.item() == 1.0
+    ties, _ = _quant_check(xt, q.cpu(), s.cpu())
+    assert ties >= 200, ties
+
+
+@pytest.mark.parametrize("T,H", [(1, 4096), (8, 4096), (32, 5120), (64, 5120), (3, 100)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_quant_equals_unfused(ops, dev, T, H, dtype):
+    _say(f"fused add_rmsnorm_quant T={T} H={H} {dtype}")
+    h, r, w = _inputs(T, H, dtype, seed=T * 5 + H)
+    hd, rd, wd = h.to(dev), r.to(dev), w.to(dev)
+    # fused
+    r1 = rd.clone()
+    q1 = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+    s1 = torch.empty(T, dtype=torch.float32, device=dev)
+    ops.esimd_fused_add_rms_norm_quant_fp8(hd, r1, wd, 1e-6, q1, s1)
+    # unfused: norm (in place on copies) then quant
+    h2, r2 = hd.clone(), rd.clone()
+    ops.esimd_fused_add_rms_norm_batched(h2, r2, wd, 1e-6)
+    q2 = torch.empty_like(q1)
+    s2 = torch.empty_like(s1)
+    ops.esimd_per_token_quant_fp8(h2, q2, s2)
+    torch.cuda.synchronize()
+    assert torch.equal(hd.cpu(), h), "hidden_states must not be written by the fused op"
+    assert torch.equal(r1, r2)
+    assert torch.equal(s1, s2)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))
+    # against the oracle: residual exact; codes equal except where the normed
+    # value rounds differently (reduction order) -- those differ by one code
+    r_ref, q_ref, s_ref, _ = onorm.fused_add_rms_norm_quant(h, r, w, 1e-6)
+    assert torch.equal(r1.cpu(), r_ref)
+    qa = q1.view(torch.uint8).cpu().numpy().astype(np.int64)
+    qb = q_ref.numpy().astype(np.int64)
+    dq = ofp8.decode_e4m3(qa.astype(np.uint8)) * s1.cpu().numpy()[:, None]
+    dr = ofp8.decode_e4m3(qb.astype(np.uint8)) * s_ref.numpy()[:, None]
+    assert_close_fp(torch.from_numpy(dq), torch.from_numpy(dr), "dequantised codes")
+    print(f"  codes differing from oracle: {(qa != qb).sum()} / {qa.size}")
+
+
+def test_norm_rejects_bad_input(ops, dev):
+    h = torch.zeros(2, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="residual and weight"):
+        ops.esimd_fused_add_rms_norm_batched(h, h.clone().float(), torch.ones(64, device=dev).half(), 1e-6)
+    with pytest.raises(RuntimeError, match="weight must have"):
+        ops.esimd_fused_add_rms_norm_batched(h, h.clone(), torch.ones(32, device=dev).half(), 1e-6)
+    q = torch.empty(2, 64, dtype=torch.float8_e5m2, device=dev)
+    with pytest.raises(RuntimeError, match="e4m3"):
+        ops.esimd_per_token_quant_fp8(h, q, torch.empty(2, device=dev))

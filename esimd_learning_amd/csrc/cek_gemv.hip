@@ -87,14 +87,13 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m >= M) break;
-        const u4* xp = reinterpret_cast<const u4*>(x + (size_t)m * K + (size_t)idx * 16);
-        u4 xa = xp[0], xb = xp[1];
+        // Read the 16 activations as 8 pairs through a pair-typed pointer
+        // (two 16-byte loads).  Bit-casting elements of a loaded u4 instead
+        // is mis-lowered by this hipcc (every element reads element 0).
+        const P* xp = reinterpret_cast<const P*>(x + (size_t)m * K + (size_t)idx * 16);
         P xv[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          xv[j] = __builtin_bit_cast(P, xa[j]);
-          xv[4 + j] = __builtin_bit_cast(P, xb[j]);
-        }
+        for (int j = 0; j < 8; ++j) xv[j] = xp[j];
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll

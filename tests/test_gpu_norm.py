@@ -147,12 +147,25 @@ def test_fused_quant_equals_unfused(ops, dev, T, H, dtype):
     # value rounds differently (reduction order) -- those differ by one code
     r_ref, q_ref, s_ref, _ = onorm.fused_add_rms_norm_quant(h, r, w, 1e-6)
     assert torch.equal(r1.cpu(), r_ref)
+    # scales: amax of the normed row, equal up to one rounding step of the
+    # activation type
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    assert np.allclose(s1.cpu().numpy(), s_ref.numpy(), rtol=ulp, atol=0)
+    # codes: the kernel's normed values may round differently from the
+    # oracle's in a few places (sum-of-squares order); such a place moves the
+    # code by one step at most and must be rare.  Exactness of the codes given
+    # identical inputs and scale is test_per_token_quant_bit_exact's job.
     qa = q1.view(torch.uint8).cpu().numpy().astype(np.int64)
     qb = q_ref.numpy().astype(np.int64)
-    dq = ofp8.decode_e4m3(qa.astype(np.uint8)) * s1.cpu().numpy()[:, None]
-    dr = ofp8.decode_e4m3(qb.astype(np.uint8)) * s_ref.numpy()[:, None]
-    assert_close_fp(torch.from_numpy(dq), torch.from_numpy(dr), "dequantised codes")
-    print(f"  codes differing from oracle: {(qa != qb).sum()} / {qa.size}")
+    mag = lambda c: np.where(c & 0x80, -(c & 0x7F), c & 0x7F)   # monotone code order  # noqa: E731
+    diff = np.abs(mag(qa) - mag(qb))
+    n_diff = int((diff != 0).sum())
+    print(f"  codes differing from oracle: {n_diff} / {qa.size}")
+    assert diff.max() <= 1
+    same_scale = np.array_equal(s1.cpu().numpy(), s_ref.numpy(), equal_nan=False)
+    same_rows = (s1.cpu().numpy() == s_ref.numpy())
+    n_diff_same = int((diff[same_rows] != 0).sum())
+    assert n_diff_same <= max(4, int(same_rows.sum()) * H // 1000), (n_diff_same, same_scale)
 
 
 def test_norm_rejects_bad_input(ops, dev):

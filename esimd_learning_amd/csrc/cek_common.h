@@ -98,6 +98,20 @@ __device__ inline float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
+// 64-lane sum with DPP row permutes (xor 1, xor 2, half-mirror, mirror give
+// each 16-lane row its total) plus four readlanes; the result is uniform.
+// Cheaper than the ds_bpermute butterfly when a kernel reduces many values.
+#define CEK_DPP_F32(v, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true))
+__device__ inline float wave_sum_dpp(float v) {
+  v += CEK_DPP_F32(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += CEK_DPP_F32(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += CEK_DPP_F32(v, 0x141);  // row_half_mirror
+  v += CEK_DPP_F32(v, 0x140);  // row_mirror
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+}
 __device__ inline float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -6,13 +6,13 @@
 // W is [N, K] row-major fp8 and is the only large operand: the kernels are
 // HBM-bound and are built to stream W once with 16-byte loads per lane.
 //
-//  * gemv_dot_kernel (M <= 4): one wave owns RPW output rows.  For a row, the
-//    64 lanes of the wave read 1 KB of contiguous weight bytes per load
-//    instruction (lane l reads bytes [16 l, 16 l + 16) of the chunk), decode
-//    them with v_cvt_scalef32_pk_{f16,bf16}_fp8 into activation-typed pairs,
-//    and accumulate with v_dot2_f32_{f16,bf16} (fp32 accumulation).  The
-//    activation slice a lane needs is re-read from L1/L2 (x is tiny).  A
-//    wave-wide butterfly sum ends each row.
+//  * gemv_dot_kernel (M <= 4): a 256-thread workgroup owns 2 output rows;
+//    one load instruction of the workgroup reads 4 KB of contiguous weight
+//    bytes of a row (thread t reads bytes [16 t, 16 t + 16) of the chunk),
+//    which are decoded with v_cvt_scalef32_pk_{f16,bf16}_fp8 into
+//    activation-typed pairs and accumulated with v_dot2_f32_{f16,bf16}
+//    (fp32 accumulation).  The activation slice a thread needs is re-read
+//    from L1/L2 (x is tiny).  DPP wave sums and an LDS combine end a row.
 //  * gemv_mfma_kernel (4 < M <= 16): the 16 x 16 x 32 f16/bf16 MFMA does
 //    the M x 16-row dot products; lane l streams row (l & 15) of a 16-row
 //    tile at k-offset 16 * (l >> 4) of each 64-byte step, so a tile is read
@@ -37,48 +37,55 @@ __device__ inline float load_scale(const void* s, int kind, int n) {
 }
 
 // ---------------------------------------------------------------------------
-// M <= MT (MT in {1, 2, 4}): v_dot2 path.
+// M <= MT (MT in {1, 2, 4}): v_dot2 path.  A 256-thread workgroup owns R
+// consecutive output rows; thread t handles the 16-byte weight units
+// t, t + 256, ... of every one of them, U units per round, so one load
+// instruction of the workgroup covers 4 KB of a row and the R rows x U units
+// are in flight together.  Per-wave DPP sums, then an LDS combine of the four
+// waves.  Small workgroups dispatched in order keep the rows being read in
+// a sliding window of HBM, which streams better than long-lived persistent
+// waves each walking its own region.
 // ---------------------------------------------------------------------------
-template <typename T, int FMT, int MT, int RPW, int UNROLL>
+template <typename T, int FMT, int MT, int R, int U>
 __global__ __launch_bounds__(256) void gemv_dot_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
     const void* __restrict__ scale, int skind, uint16_t* __restrict__ y,
     int M, int N, int K) {
   typedef typename T::pair P;
-  const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
-  if (row0 >= N) return;
+  __shared__ float red[4][MT * R];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int row0 = blockIdx.x * R;
   const int K16 = K >> 4;
 
-  float acc[MT][RPW];
+  const uint8_t* wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r < N ? row0 + r : N - 1;  // clamped rows are never stored
+    wrow[r] = w + (size_t)row * K;
+  }
+  float acc[MT][R];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[m][r] = 0.f;
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
 
-  const uint8_t* wrow[RPW];
+  for (int base = t; base < K16; base += 256 * U) {
+    u4 wv[U][R];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    int row = row0 + r < N ? row0 + r : N - 1;  // clamped rows are never stored
-    wrow[r] = w + (size_t)row * K;
-  }
-
-  for (int base = 0; base < K16; base += 64 * UNROLL) {
-    u4 wv[UNROLL][RPW];
+    for (int u = 0; u < U; ++u) {
+      const int idx = base + u * 256;
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int idx = base + u * 64 + lane;
-#pragma unroll
-      for (int r = 0; r < RPW; ++r)
+      for (int r = 0; r < R; ++r)
         wv[u][r] = idx < K16 ? load_u4_stream(wrow[r] + (size_t)idx * 16) : u4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int idx = base + u * 64 + lane;
+    for (int u = 0; u < U; ++u) {
+      const int idx = base + u * 256;
       if (idx >= K16) break;
-      P wp[RPW][8];
+      P wp[R][8];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           wp[r][2 * j] = fp8x2_to_pair<T, FMT, false>(wv[u][r][j]);
@@ -87,15 +94,15 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m >= M) break;
-        // Read the 16 activations as 8 pairs through a pair-typed pointer
-        // (two 16-byte loads).  Bit-casting elements of a loaded u4 instead
-        // is mis-lowered by this hipcc (every element reads element 0).
+        // 16 activations as 8 pairs through a pair-typed pointer (two 16-byte
+        // loads).  Bit-casting elements of a loaded u4 instead is mis-lowered
+        // by this hipcc (every element reads element 0).
         const P* xp = reinterpret_cast<const P*>(x + (size_t)m * K + (size_t)idx * 16);
         P xv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) xv[j] = xp[j];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[m][r] = dot2(xv[j], wp[r][j], acc[m][r]);
       }
@@ -105,13 +112,18 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      float s = wave_sum(acc[m][r]);
-      if (lane == m * RPW + r && m < M && row0 + r < N) {
-        const int n = row0 + r;
-        y[(size_t)m * N + n] = T::from_f32(s * load_scale(scale, skind, n));
-      }
+    for (int r = 0; r < R; ++r) {
+      const float s = wave_sum_dpp(acc[m][r]);
+      if (lane == 0) red[wave][m * R + r] = s;
     }
+  __syncthreads();
+  if (t < MT * R) {
+    const int m = t / R, r = t % R, n = row0 + r;
+    if (m < M && n < N) {
+      const float s = red[0][t] + red[1][t] + red[2][t] + red[3][t];
+      y[(size_t)m * N + n] = T::from_f32(s * load_scale(scale, skind, n));
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -242,14 +254,18 @@ static int launch_gemv_t(const void* x, const void* w, const void* scale, int sk
   uint16_t* yp = static_cast<uint16_t*>(y);
   const bool vec16 = (K % 16 == 0) && aligned(x, 16) && aligned(w, 16);
   if (vec16 && M <= 4) {
-    constexpr int RPW = 4;
-    dim3 grid((N + 4 * RPW - 1) / (4 * RPW));
-    if (M == 1)
-      gemv_dot_kernel<T, FMT, 1, RPW, 2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-    else if (M == 2)
-      gemv_dot_kernel<T, FMT, 2, RPW, 2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-    else
-      gemv_dot_kernel<T, FMT, 4, RPW, 2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+    // R = 2 rows per workgroup; U = 16-byte units per thread and row in
+    // flight (K = 4096 -> 1, K = 14336 -> 4).
+    constexpr int R = 2;
+    const int K16 = K / 16;
+    dim3 grid((N + R - 1) / R);
+#define CEK_DOT(MT, U) gemv_dot_kernel<T, FMT, MT, R, U><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
+#define CEK_DOT_M(MT) do { if (K16 <= 256) CEK_DOT(MT, 1); else if (K16 <= 512) CEK_DOT(MT, 2); else CEK_DOT(MT, 4); } while (0)
+    if (M == 1) CEK_DOT_M(1);
+    else if (M == 2) CEK_DOT_M(2);
+    else CEK_DOT_M(4);
+#undef CEK_DOT_M
+#undef CEK_DOT
   } else if (vec16 && K % 64 == 0 && M <= 16) {
     constexpr int NT = 1;
     dim3 grid((N + 16 * NT - 1) / (16 * NT));

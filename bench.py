@@ -191,6 +191,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="first run 10 plain device copies of N*K bytes (reference for HBM counter scaling)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the op pack has no "
@@ -202,6 +204,14 @@ def main():
     ops = esimd_learning_amd.ops()
     assert torch.cuda.is_available(), "no GPU visible"
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if a.copy_ref:
+        src = torch.empty(14336 * 4096, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy reference: 10 x {src.numel()} bytes")
+        del src, dst
 
     g, (x, Wd, s, y) = bench_gemv(ops, torch, a.steps, a.warmup)
     log(f"gemv: {g['avg_launch_us']:.2f} us/launch, {g['achieved']:.0f} GB/s; eager event median "

@@ -254,22 +254,28 @@ static int launch_gemv_t(const void* x, const void* w, const void* scale, int sk
   uint16_t* yp = static_cast<uint16_t*>(y);
   const bool vec16 = (K % 16 == 0) && aligned(x, 16) && aligned(w, 16);
   if (vec16 && M <= 4) {
-    // R = 2 rows per workgroup; U = 16-byte units per thread and row in
-    // flight (K = 4096 -> 1, K = 14336 -> 4).
-    constexpr int R = 2;
+    // Rows per workgroup (measured on MI355X, one pass over > 2 GB of
+    // rotating weights): 2 for M = 1 up to K = 4096; 4 for longer rows and
+    // for M >= 2 on wide N, where each workgroup's re-read of the
+    // activations is amortised over more weight rows.  One 16-byte unit per
+    // thread and row per round.
     const int K16 = K / 16;
-    dim3 grid((N + R - 1) / R);
-#define CEK_DOT(MT, U) gemv_dot_kernel<T, FMT, MT, R, U><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
-#define CEK_DOT_M(MT) do { if (K16 <= 256) CEK_DOT(MT, 1); else if (K16 <= 512) CEK_DOT(MT, 2); else CEK_DOT(MT, 4); } while (0)
-    if (M == 1) CEK_DOT_M(1);
-    else if (M == 2) CEK_DOT_M(2);
-    else CEK_DOT_M(4);
-#undef CEK_DOT_M
+    const bool r2 = (M == 1 && K16 <= 256) || (M == 2 && N <= 8192);
+#define CEK_DOT(MT, R) gemv_dot_kernel<T, FMT, MT, R, 1><<<dim3((N + R - 1) / R), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
+    if (M == 1) { if (r2) CEK_DOT(1, 2); else CEK_DOT(1, 4); }
+    else if (M == 2) { if (r2) CEK_DOT(2, 2); else CEK_DOT(2, 4); }
+    else CEK_DOT(4, 4);
 #undef CEK_DOT
   } else if (vec16 && K % 64 == 0 && M <= 16) {
-    constexpr int NT = 1;
-    dim3 grid((N + 16 * NT - 1) / (16 * NT));
-    gemv_mfma_kernel<T, FMT, NT, 4><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+    // Two 16-row tiles per wave where N leaves >= 256 workgroups, else one
+    // tile with 16 K-steps in flight (short K) or 4 (long K).
+    if (N >= 8192) {
+      gemv_mfma_kernel<T, FMT, 2, 8><<<dim3((N + 31) / 32), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+    } else if (K <= 4096) {
+      gemv_mfma_kernel<T, FMT, 1, 16><<<dim3((N + 15) / 16), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+    } else {
+      gemv_mfma_kernel<T, FMT, 1, 4><<<dim3((N + 15) / 16), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+    }
   } else {
     dim3 grid((N + 3) / 4);
     gemv_generic_kernel<T, FMT><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);

@@ -64,7 +64,7 @@ def build_cabi(jobs=8):
         objs = list(ex.map(compile_one, CABI_SOURCES))
     tmp = LIBCEK.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-          "-Wl,-soname,libcek.so"])
+          "-Wl,-soname,libcek.so", "-Wl,--no-undefined"])
     os.replace(tmp, LIBCEK)
     return LIBCEK
 

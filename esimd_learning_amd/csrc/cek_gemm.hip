@@ -91,6 +91,148 @@ __global__ __launch_bounds__(256) void gemm_a8w8_simple_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// a8w8, LDS-tiled: block tile BM x BN, K step 128, four waves in a WM x WN
+// grid (wave tile (BM/WM) x (BN/WN), i.e. FM x FN MFMA blocks of 16 x 16).
+//
+// The A and B K-slices are staged row-major in LDS (128 bytes per row, eight
+// 16-byte chunks), double-buffered, by direct-to-LDS loads
+// (global_load_lds_dwordx4: one instruction moves 1 KB = 8 full rows; lane
+// i's 16 bytes land at LDS + 16 i).  Chunk c of row r is stored at position
+// c ^ s(r).  An operand fragment gives lane l row (l & 15) and two chunks
+// (LAYOUT 0: 2g and 2g+1; LAYOUT 1: g and g+4; g = l >> 4) -- the same K
+// positions for A and B, so any assignment sums the right products.  The
+// swizzles s(r) = (r ^ ((r >> 3) & 1)) & 7 (LAYOUT 0) and r & 7 (LAYOUT 1) make
+// each 16-lane group of such a ds_read_b128 hit distinct banks (measured
+// with SQ_LDS_BANK_CONFLICT on MI355X).
+// The stage written during step k+1 was last read in step k-1; the barrier
+// at the top of each step (which also drains this wave's outstanding loads)
+// separates the two.  Tiles are numbered so that consecutive workgroups on
+// one XCD (workgroup i runs on XCD i % 8) share A rows and B columns in that
+// XCD's L2.  Requires K % 128 == 0 and 16-byte aligned A and B.
+// ---------------------------------------------------------------------------
+template <int LAYOUT>
+__device__ inline int swz(int row) { return LAYOUT == 0 ? ((row ^ ((row >> 3) & 1)) & 7) : (row & 7); }
+
+template <int BM, int BN, int GROUP_M>
+__device__ inline void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int T = tiles_m * tiles_n;
+  int t = b;
+  if ((T & 7) == 0) t = (b & 7) * (T >> 3) + (b >> 3);  // XCD-contiguous numbering
+  const int per_group = GROUP_M * tiles_n;
+  const int group = t / per_group;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int tin = t - group * per_group;
+  tm = first_m + tin % gsize;
+  tn = tin / gsize;
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Direct-to-LDS loads of one K step (128 bytes) of the A and B slices into a
+// stage: this wave's 1 KB writer chunks j = wave + 4 i (rows 8 j .. 8 j + 7).
+template <int BM, int BN, int ACH, int BCH>
+__device__ inline void a8w8_issue(uint8_t* smem, int stage, int kb, int wave,
+                                  const uint8_t* const (&ga)[ACH], const uint8_t* const (&gb)[BCH]) {
+#if defined(__HIP_DEVICE_COMPILE__)  // device-only builtin; the host pass only needs the kernel's stub
+  uint8_t* sA = smem + stage * (BM + BN) * 128;
+  uint8_t* sB = sA + BM * 128;
+#pragma unroll
+  for (int i = 0; i < ACH; ++i)
+    __builtin_amdgcn_global_load_lds(ga[i] + kb, (lds_ptr_t)(sA + (wave + 4 * i) * 1024), 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < BCH; ++i)
+    __builtin_amdgcn_global_load_lds(gb[i] + kb, (lds_ptr_t)(sB + (wave + 4 * i) * 1024), 16, 0, 0);
+#endif
+}
+
+__device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
+  const u4 lo = *reinterpret_cast<const u4*>(row + p0 * 16);
+  const u4 hi = *reinterpret_cast<const u4*>(row + p1 * 16);
+  return i8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int LAYOUT, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sa,
+    const uint8_t* __restrict__ B, const float* __restrict__ sb,
+    uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int BK = 128;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int ACH = BM / 8 / 4, BCH = BN / 8 / 4;  // 1 KB writer chunks per wave per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // writer chunk j: lane i fills row 8 j + (i >> 3), position i & 7, i.e.
+  // logical chunk (i & 7) ^ s(row)
+  const uint8_t* ga[ACH];
+  const uint8_t* gb[BCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int row = (wave + 4 * i) * 8 + (lane >> 3);
+    ga[i] = A + (size_t)min(m0 + row, M - 1) * K + ((lane & 7) ^ swz<LAYOUT>(row)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int row = (wave + 4 * i) * 8 + (lane >> 3);
+    gb[i] = B + (size_t)min(n0 + row, N - 1) * K + ((lane & 7) ^ swz<LAYOUT>(row)) * 16;
+  }
+
+  // reader: row (lane & 15) of each 16-row block; both swizzles depend only
+  // on row & 15, and blocks start at multiples of 16, so s(row) = s(lane & 15)
+  const int r16 = lane & 15, g = lane >> 4;
+  const int c0 = LAYOUT == 0 ? 2 * g : g;
+  const int c1 = LAYOUT == 0 ? 2 * g + 1 : g + 4;
+  const int p0 = c0 ^ swz<LAYOUT>(r16), p1 = c1 ^ swz<LAYOUT>(r16);
+
+  f4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  a8w8_issue<BM, BN, ACH, BCH>(smem, 0, 0, wave, ga, gb);
+  for (int kt = 0; kt < KT; ++kt) {
+    __syncthreads();  // this step's stage has landed; the other stage is free
+    if (kt + 1 < KT) a8w8_issue<BM, BN, ACH, BCH>(smem, (kt + 1) & 1, (kt + 1) * BK, wave, ga, gb);
+    const uint8_t* sA = smem + (kt & 1) * STAGE + (wm * TM + r16) * BK;
+    const uint8_t* sB = smem + (kt & 1) * STAGE + (BM + wn * TN + r16) * BK;
+    i8 bf[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = lds_frag(sB + j * 16 * BK, p0, p1);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const i8 af = lds_frag(sA + i * 16 * BK, p0, p1);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_fp8_16x16x128(af, bf[j], acc[i][j]);
+    }
+  }
+
+  // epilogue: D[4 (l >> 4) + v][l & 15] of each block
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * TN + j * 16 + r16;
+    if (n >= N) continue;
+    const float sn = sb[n];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + wm * TM + i * 16 + g * 4 + v;
+        if (m < M) Y[(size_t)m * N + n] = T::from_f32(acc[i][j][v] * sa[m] * sn);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // w8a16, direct-from-global v0: 64 x 64 C tile per workgroup, K step 64.
 // ---------------------------------------------------------------------------
 
@@ -167,6 +309,10 @@ __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
 
 using namespace cek;
 
+#ifndef CEK_A8W8_LAYOUT
+#define CEK_A8W8_LAYOUT 1
+#endif
+
 extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scale, void* y,
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, void* stream) {
@@ -198,8 +344,36 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
   if (!a || !sa || !b || !sb || !y) return CEK_ERR_INVALID;
   if (!aligned(a, 16) || !aligned(b, 16)) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
   uint16_t* yp = static_cast<uint16_t*>(y);
+  if (K % 128 == 0 && (out_dtype == CEK_F16 || out_dtype == CEK_BF16)) {
+    // Tile choice (measured on MI355X over the BASELINE prefill shapes):
+    // 128 x 128 tiles let two workgroups share a CU, so one's MFMAs cover the
+    // other's LDS and barrier waits; 64 x 128 gives more tiles when there are
+    // too few to fill 256 CUs twice; 256 x 256 halves the L2 -> LDS traffic
+    // per flop and wins once there are many tiles per CU anyway.
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    int cfg;
+    if (K >= 8192) cfg = t128 < 256 ? 0 : 1;
+    else cfg = t128 < 1024 ? 0 : (t128 < 4096 ? 1 : 2);
+#define CEK_A8W8(TY, BM, BN, OCC)                                                                      \
+  do {                                                                                               \
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                          \
+    gemm_a8w8_lds_kernel<TY, BM, BN, 2, 2, CEK_A8W8_LAYOUT, OCC><<<dim3((unsigned)(tm * tn)), 256, 0, st>>>( \
+        a, sa, b, sb, yp, M, N, K, tm, tn);                                                          \
+  } while (0)
+    if (out_dtype == CEK_F16) {
+      if (cfg == 0) CEK_A8W8(F16, 64, 128, 2);
+      else if (cfg == 1) CEK_A8W8(F16, 128, 128, 2);
+      else CEK_A8W8(F16, 256, 256, 1);
+    } else {
+      if (cfg == 0) CEK_A8W8(BF16, 64, 128, 2);
+      else if (cfg == 1) CEK_A8W8(BF16, 128, 128, 2);
+      else CEK_A8W8(BF16, 256, 256, 1);
+    }
+#undef CEK_A8W8
+    return check_launch();
+  }
+  dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
   if (out_dtype == CEK_F16) gemm_a8w8_simple_kernel<F16><<<grid, 256, 0, st>>>(a, sa, b, sb, yp, M, N, K);
   else if (out_dtype == CEK_BF16) gemm_a8w8_simple_kernel<BF16><<<grid, 256, 0, st>>>(a, sa, b, sb, yp, M, N, K);
   else return CEK_ERR_INVALID;

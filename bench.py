@@ -155,6 +155,36 @@ def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
                          "traffic": None}}
 
 
+def bench_layer(torch, steps, M=4):
+    """one Gemma-style decoder-layer decode step, HIP-graph replayed."""
+    from esimd_learning_amd import synthetic
+    from esimd_learning_amd.layer import GemmaDecodeLayer
+    dev = "cuda:0"
+    p = synthetic.gemma_layer(seed=10)
+    layer = GemmaDecodeLayer(p, M, dev)
+    h = synthetic.activations(M, p["hidden"], seed=20).to(dev)
+    r = synthetic.activations(M, p["hidden"], seed=21).to(dev)
+    pos = synthetic.positions(M, seed=22).to(dev)
+    layer.step(h, r, pos)
+    torch.cuda.synchronize()
+    g = layer.capture(h, r, pos)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    wb = layer.weight_bytes()
+    return {"config": "Gemma-style decoder layer decode step, M=4, hidden 3072, 16q/16kv x 256, MLP 24576 "
+                      "(attention stood in by a copy of q)",
+            "us_per_step": round(us, 2), "weight_bytes": wb, "weight_GBps": round(wb / us / 1e3, 1),
+            "timing": f"one HIP graph of the step, replayed {steps} times back to back"}
+
+
 def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
     from esimd_learning_amd import synthetic
     from oracle import gemv as ogemv
@@ -191,6 +221,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run 10 plain device copies of N*K bytes (reference for HBM counter scaling)")
     a = ap.parse_args()
@@ -248,6 +279,9 @@ def main():
     if not a.no_gemm:
         out["gemm"] = bench_gemm(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")
+    if not a.no_layer:
+        out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))
+        log(f"layer: {out['decoder_layer']['us_per_step']} us/step, {out['decoder_layer']['weight_GBps']} GB/s")
     if not a.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch)

@@ -1,0 +1,77 @@
+"""One Gemma-style decoder-layer decode step from the custom ops.
+
+    h1, r1 = add_rmsnorm(hidden, residual, w_in)          esimd_fused_add_rms_norm_batched
+    qkv    = h1 @ Wqkv^T * sqkv                           esimd_gemv_fp8_pern
+    q, k   = per-head RMSNorm + RoPE (in place in qkv)     esimd_qk_norm_rope
+    a      = attention(q, k, v)        -- out of scope: q stands in for its output
+    o      = a @ Wo^T * so                                esimd_gemv_fp8_pern
+    h2, r2 = add_rmsnorm(o, r1, w_post)                   esimd_fused_add_rms_norm_batched
+    gu     = h2 @ Wgu^T * sgu                             esimd_gemv_fp8_pern
+    g      = gelu_tanh(gu[:, :d]) * gu[:, d:]             esimd_gelu_and_mul
+    out    = g @ Wd^T * sd                                esimd_gemv_fp8_pern
+
+All intermediate buffers are allocated once in the constructor, so a step
+enqueues only kernels: it can be captured in a HIP graph (``capture``) and
+replayed, which removes host launch overhead from the latency-bound small
+kernels between the GEMVs.
+"""
+
+import torch
+
+
+class GemmaDecodeLayer:
+    def __init__(self, params, M, device="cuda:0", dtype=torch.float16):
+        from . import ops as _load_ops
+        self.ops = _load_ops()
+        p = params
+        self.M, self.dev, self.dtype = M, device, dtype
+        self.hidden, self.hd, self.nq, self.nk = p["hidden"], p["head_dim"], p["n_q"], p["n_kv"]
+        self.mlp, self.eps, self.theta = p["mlp"], p["eps"], p["theta"]
+        t = lambda x: x.to(device)  # noqa: E731
+        self.Wqkv, self.sqkv = t(p["Wqkv"]), t(p["sqkv"])
+        self.Wo, self.so = t(p["Wo"]), t(p["so"])
+        self.Wgu, self.sgu = t(p["Wgu"]), t(p["sgu"])
+        self.Wd, self.sd = t(p["Wd"]), t(p["sd"])
+        self.w_in, self.w_post = t(p["w_in"]).to(dtype), t(p["w_post"]).to(dtype)
+        self.qw, self.kw = t(p["qw"]).to(dtype), t(p["kw"]).to(dtype)
+        nqkv = self.Wqkv.shape[0]
+        mk = lambda n: torch.empty(M, n, dtype=dtype, device=device)  # noqa: E731
+        self.qkv = mk(nqkv)
+        self.attn = mk(self.nq * self.hd)
+        self.o = mk(self.hidden)
+        self.gu = mk(2 * self.mlp)
+        self.act = mk(self.mlp)
+        self.out = mk(self.hidden)
+        self.graph = None
+
+    def weight_bytes(self):
+        return sum(w.numel() for w in (self.Wqkv, self.Wo, self.Wgu, self.Wd))
+
+    def step(self, hidden, residual, positions):
+        """hidden, residual: [M, hidden] (residual updated in place); returns out."""
+        o, hd, nq, nk = self.ops, self.hd, self.nq, self.nk
+        o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, self.eps)
+        o.esimd_gemv_fp8_pern(hidden, self.Wqkv, self.sqkv, self.qkv, self.Wqkv.shape[0], self.hidden)
+        o.esimd_qk_norm_rope(self.qkv[:, : nq * hd], self.qkv[:, nq * hd:(nq + nk) * hd], self.qw, self.kw,
+                             positions, self.eps, self.theta, True)
+        self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
+        o.esimd_gemv_fp8_pern(self.attn, self.Wo, self.so, self.o, self.hidden, nq * hd)
+        o.esimd_fused_add_rms_norm_batched(self.o, residual, self.w_post, self.eps)
+        o.esimd_gemv_fp8_pern(self.o, self.Wgu, self.sgu, self.gu, 2 * self.mlp, self.hidden)
+        o.esimd_gelu_and_mul(self.act, self.gu)
+        o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
+        return self.out
+
+    def capture(self, hidden, residual, positions, stream=None):
+        """Capture one step on fixed input buffers in a HIP graph; replay with replay()."""
+        s = stream or torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=s):
+            self.step(hidden, residual, positions)
+        torch.cuda.current_stream().wait_stream(s)
+        return self.graph
+
+    def replay(self):
+        self.graph.replay()
+        return self.out

@@ -232,10 +232,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// w8a16, direct-from-global v0: 64 x 64 C tile per workgroup, K step 64.
-// ---------------------------------------------------------------------------
-
+// Decode 16 fp8 bytes into two u4 of activation-typed values (k-slots 0-7, 8-15).
 template <typename T, int FMT>
 __device__ inline void decode16(u4 w, u4& lo, u4& hi) {
   typedef typename T::pair P;
@@ -250,6 +247,118 @@ __device__ inline void decode16(u4 w, u4& lo, u4& hi) {
   hi = u4{__builtin_bit_cast(uint32_t, p[4]), __builtin_bit_cast(uint32_t, p[5]),
           __builtin_bit_cast(uint32_t, p[6]), __builtin_bit_cast(uint32_t, p[7])};
 }
+
+// ---------------------------------------------------------------------------
+// w8a16, LDS-tiled: block tile BM x BN, K step 64, four waves 2 x 2.
+// LDS stage: A as BM rows of 128 bytes (64 activations, eight 16-byte chunks,
+// chunk c of row r at c ^ sA(r)), B as BN rows of 64 bytes (64 fp8 codes,
+// four chunks, chunk c of row r at c ^ sB(r)); both filled by direct-to-LDS
+// loads (one instruction: 8 A rows or 16 B rows).  Lane l of a wave takes
+// row (l & 15) of a 16-row block and K positions 16 g .. 16 g + 15, g = l >> 4:
+// 32 bytes of A (two chunks) and 16 bytes of B (one chunk), decoded to the
+// activation type in registers; two 16 x 16 x 32 MFMAs consume them.
+// ---------------------------------------------------------------------------
+__device__ inline int swzA(int row) { return (row ^ ((row >> 3) & 1)) & 7; }
+__device__ inline int swzB(int row) { return (row >> 2) & 3; }
+
+template <int BM, int BN, int ACH, int BCH>
+__device__ inline void w8a16_issue(uint8_t* smem, int stage, int kb, int wave,
+                                   const uint8_t* const (&ga)[ACH], const uint8_t* const (&gb)[BCH]) {
+#if defined(__HIP_DEVICE_COMPILE__)  // device-only builtin; the host pass only needs the kernel's stub
+  uint8_t* sA = smem + stage * (BM * 128 + BN * 64);
+  uint8_t* sB = sA + BM * 128;
+#pragma unroll
+  for (int i = 0; i < ACH; ++i)
+    __builtin_amdgcn_global_load_lds(ga[i] + 2 * kb, (lds_ptr_t)(sA + (wave + 4 * i) * 1024), 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < BCH; ++i)
+    __builtin_amdgcn_global_load_lds(gb[i] + kb, (lds_ptr_t)(sB + (wave + 4 * i) * 1024), 16, 0, 0);
+#endif
+}
+
+template <typename T, int FMT, int BM, int BN, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_w8a16_lds_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
+    uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int BK = 64;
+  constexpr int TM = BM / 2, TN = BN / 2;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int STAGE = BM * 128 + BN * 64;
+  constexpr int ACH = BM / 8 / 4, BCH = BN / 16 / 4;   // 1 KB writer chunks per wave per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const uint8_t* Xb = reinterpret_cast<const uint8_t*>(X);
+
+  // A writer chunk j: lane i -> row 8 j + (i >> 3), position i & 7
+  // B writer chunk j: lane i -> row 16 j + (i >> 2), position i & 3
+  const uint8_t* ga[ACH];
+  const uint8_t* gb[BCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int row = (wave + 4 * i) * 8 + (lane >> 3);
+    ga[i] = Xb + ((size_t)min(m0 + row, M - 1) * K) * 2 + ((lane & 7) ^ swzA(row)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int row = (wave + 4 * i) * 16 + (lane >> 2);
+    gb[i] = W + (size_t)min(n0 + row, N - 1) * K + ((lane & 3) ^ swzB(row)) * 16;
+  }
+
+  const int r16 = lane & 15, g = lane >> 4;
+  const int pa0 = (2 * g) ^ swzA(r16), pa1 = (2 * g + 1) ^ swzA(r16), pb = g ^ swzB(r16);
+
+  f4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  w8a16_issue<BM, BN, ACH, BCH>(smem, 0, 0, wave, ga, gb);
+  for (int kt = 0; kt < KT; ++kt) {
+    __syncthreads();  // this step's stage has landed; the other stage is free
+    if (kt + 1 < KT) w8a16_issue<BM, BN, ACH, BCH>(smem, (kt + 1) & 1, (kt + 1) * BK, wave, ga, gb);
+    const uint8_t* sA = smem + (kt & 1) * STAGE + (wm * TM + r16) * 128;
+    const uint8_t* sB = smem + (kt & 1) * STAGE + BM * 128 + (wn * TN + r16) * 64;
+    u4 blo[FN], bhi[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) decode16<T, FMT>(*reinterpret_cast<const u4*>(sB + j * 16 * 64 + pb * 16), blo[j], bhi[j]);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const u4 alo = *reinterpret_cast<const u4*>(sA + i * 16 * 128 + pa0 * 16);
+      const u4 ahi = *reinterpret_cast<const u4*>(sA + i * 16 * 128 + pa1 * 16);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = mfma16x16x32<T>(alo, blo[j], acc[i][j]);
+        acc[i][j] = mfma16x16x32<T>(ahi, bhi[j], acc[i][j]);
+      }
+    }
+  }
+
+  const float sc = *scale;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * TN + j * 16 + r16;
+    if (n >= N) continue;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = m0 + wm * TM + i * 16 + g * 4 + v;
+        if (m < M) Y[(size_t)m * N + n] = T::from_f32(acc[i][j][v] * sc);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// w8a16, direct-from-global v0: 64 x 64 C tile per workgroup, K step 64.
+// ---------------------------------------------------------------------------
+
 
 template <typename T, int FMT>
 __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
@@ -325,6 +434,21 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   if (M <= 16) return launch_gemv(x, w, scale, 3 /* f32 scalar */, y, M, N, K, io_dtype, fp8_fmt, st);
   if (K % 64 != 0 || !aligned(x, 16) || !aligned(w, 16) || M > 65535 * 64)
     return launch_gemv_generic(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
+  {
+    constexpr int BM = 128, BN = 128;
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
+    dim3 grid((unsigned)(tm * tn));
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    const uint8_t* wp = static_cast<const uint8_t*>(w);
+    uint16_t* yp = static_cast<uint16_t*>(y);
+#define CEK_W8A16(TY, F) gemm_w8a16_lds_kernel<TY, F, BM, BN, 2><<<grid, 256, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn)
+    if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_W8A16(F16, CEK_E4M3);
+    else if (io_dtype == CEK_F16) CEK_W8A16(F16, CEK_E5M2);
+    else if (fp8_fmt == CEK_E4M3) CEK_W8A16(BF16, CEK_E4M3);
+    else CEK_W8A16(BF16, CEK_E5M2);
+#undef CEK_W8A16
+    return check_launch();
+  }
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint8_t* wp = static_cast<const uint8_t*>(w);

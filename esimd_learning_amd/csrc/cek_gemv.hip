@@ -79,10 +79,28 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(
       for (int r = 0; r < R; ++r)
         wv[u][r] = idx < K16 ? load_u4_stream(wrow[r] + (size_t)idx * 16) : u4{0, 0, 0, 0};
     }
+    // All activation loads of the round are issued before any arithmetic
+    // (rows m >= M read row M - 1 and are never stored), so their L2 round
+    // trips overlap each other and the weight loads.  Pairs are read through
+    // a pair-typed pointer: bit-casting elements of a loaded u4 instead is
+    // mis-lowered by this hipcc (every element reads element 0).
+    P xv[U][MT][8];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int idx = base + u * 256;
-      if (idx >= K16) break;
+      const int idx = min(base + u * 256, K16 - 1);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const P* xp = reinterpret_cast<const P*>(x + (size_t)min(m, M - 1) * K + (size_t)idx * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[u][m][j] = xp[j];
+      }
+    }
+    // Keep the scheduler from sinking the loads into the arithmetic below (it
+    // otherwise serialises them through one register quad).
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + u * 256 >= K16) break;
       P wp[R][8];
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -92,20 +110,11 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(
           wp[r][2 * j + 1] = fp8x2_to_pair<T, FMT, true>(wv[u][r][j]);
         }
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m >= M) break;
-        // 16 activations as 8 pairs through a pair-typed pointer (two 16-byte
-        // loads).  Bit-casting elements of a loaded u4 instead is mis-lowered
-        // by this hipcc (every element reads element 0).
-        const P* xp = reinterpret_cast<const P*>(x + (size_t)m * K + (size_t)idx * 16);
-        P xv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[j] = xp[j];
+      for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[m][r] = dot2(xv[j], wp[r][j], acc[m][r]);
-      }
+          for (int j = 0; j < 8; ++j) acc[m][r] = dot2(xv[u][m][j], wp[r][j], acc[m][r]);
     }
   }
 
@@ -177,6 +186,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(
         xb[u] = u4{0, 0, 0, 0};
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // all loads of the round before any arithmetic
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
 #pragma unroll
@@ -255,27 +265,26 @@ static int launch_gemv_t(const void* x, const void* w, const void* scale, int sk
   const bool vec16 = (K % 16 == 0) && aligned(x, 16) && aligned(w, 16);
   if (vec16 && M <= 4) {
     // Rows per workgroup (measured on MI355X, one pass over > 2 GB of
-    // rotating weights): 2 for M = 1 up to K = 4096; 4 for longer rows and
-    // for M >= 2 on wide N, where each workgroup's re-read of the
-    // activations is amortised over more weight rows.  One 16-byte unit per
-    // thread and row per round.
+    // rotating weights): 2 for M = 1 up to K = 4096, else 4, which amortises
+    // each workgroup's re-read of the M activation rows over more weight
+    // rows.  One 16-byte unit per thread and row per round.
     const int K16 = K / 16;
-    const bool r2 = (M == 1 && K16 <= 256) || (M == 2 && N <= 8192);
+    const bool r2 = M == 1 && K16 <= 256;
 #define CEK_DOT(MT, R) gemv_dot_kernel<T, FMT, MT, R, 1><<<dim3((N + R - 1) / R), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
     if (M == 1) { if (r2) CEK_DOT(1, 2); else CEK_DOT(1, 4); }
-    else if (M == 2) { if (r2) CEK_DOT(2, 2); else CEK_DOT(2, 4); }
+    else if (M == 2) CEK_DOT(2, 4);
     else CEK_DOT(4, 4);
 #undef CEK_DOT
   } else if (vec16 && K % 64 == 0 && M <= 16) {
-    // Two 16-row tiles per wave where N leaves >= 256 workgroups, else one
-    // tile with 16 K-steps in flight (short K) or 4 (long K).
-    if (N >= 8192) {
-      gemv_mfma_kernel<T, FMT, 2, 8><<<dim3((N + 31) / 32), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-    } else if (K <= 4096) {
-      gemv_mfma_kernel<T, FMT, 1, 16><<<dim3((N + 15) / 16), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-    } else {
-      gemv_mfma_kernel<T, FMT, 1, 4><<<dim3((N + 15) / 16), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-    }
+    // 16-row tiles per wave (NT) and 64-byte K steps in flight per wave
+    // (UNROLL), measured per shape class: wide N amortises the activation
+    // reads over more tiles; narrow N needs more workgroups and deeper K.
+#define CEK_MF(NT, UN) gemv_mfma_kernel<T, FMT, NT, UN><<<dim3((N + 16 * NT - 1) / (16 * NT)), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
+    if (N >= 16384) CEK_MF(4, 4);
+    else if (N >= 8192) { if (M > 8) CEK_MF(4, 2); else if (K <= 3072) CEK_MF(1, 8); else CEK_MF(2, 8); }
+    else if (K <= 4096) { if (N >= 6144) CEK_MF(2, 16); else CEK_MF(1, 16); }
+    else CEK_MF(1, 4);
+#undef CEK_MF
   } else {
     dim3 grid((N + 3) / 4);
     gemv_generic_kernel<T, FMT><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);

@@ -70,6 +70,22 @@ __device__ inline f4 mfma16x16x32<BF16>(u4 a, u4 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
 }
 
+// Decode 16 fp8 bytes into two u4 of activation-typed values (k-slots 0-7, 8-15).
+template <typename T, int FMT>
+__device__ inline void decode16(u4 w, u4& lo, u4& hi) {
+  typedef typename T::pair P;
+  P p[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    p[2 * j] = fp8x2_to_pair<T, FMT, false>(w[j]);
+    p[2 * j + 1] = fp8x2_to_pair<T, FMT, true>(w[j]);
+  }
+  lo = u4{__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
+          __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3])};
+  hi = u4{__builtin_bit_cast(uint32_t, p[4]), __builtin_bit_cast(uint32_t, p[5]),
+          __builtin_bit_cast(uint32_t, p[6]), __builtin_bit_cast(uint32_t, p[7])};
+}
+
 // Exact decode of one fp8 byte to fp32 (used by the generic paths).
 template <int FMT>
 __device__ inline float fp8_to_f32(uint32_t byte) {

@@ -232,21 +232,6 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
   }
 }
 
-// Decode 16 fp8 bytes into two u4 of activation-typed values (k-slots 0-7, 8-15).
-template <typename T, int FMT>
-__device__ inline void decode16(u4 w, u4& lo, u4& hi) {
-  typedef typename T::pair P;
-  P p[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    p[2 * j] = fp8x2_to_pair<T, FMT, false>(w[j]);
-    p[2 * j + 1] = fp8x2_to_pair<T, FMT, true>(w[j]);
-  }
-  lo = u4{__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
-          __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3])};
-  hi = u4{__builtin_bit_cast(uint32_t, p[4]), __builtin_bit_cast(uint32_t, p[5]),
-          __builtin_bit_cast(uint32_t, p[6]), __builtin_bit_cast(uint32_t, p[7])};
-}
 
 // ---------------------------------------------------------------------------
 // w8a16, LDS-tiled: block tile BM x BN, K step 64, four waves 2 x 2.

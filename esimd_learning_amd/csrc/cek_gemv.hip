@@ -6,7 +6,15 @@
 // W is [N, K] row-major fp8 and is the only large operand: the kernels are
 // HBM-bound and are built to stream W once with 16-byte loads per lane.
 //
-//  * gemv_dot_kernel (M <= 4): a 256-thread workgroup owns 2 output rows;
+// Every launch covers a table of 1..8 weight matrices ("segments") that share
+// the activations x -- one matrix for esimd_gemv_fp8_pern/pert, several for
+// the fused variants (QKV or gate/up in one launch, what the reference's
+// unregistered GEMV_fp8_pern_fused_kernel / GEMV_fp8_pert_fused_kernel do,
+// fp8_GEMV_v2.h:197-316, 440-558).  The table is passed by value in the
+// kernel arguments; workgroup b finds its segment from the table's prefix
+// sums of workgroups per segment.
+//
+//  * gemv_dot_kernel (M <= 4): a 256-thread workgroup owns R output rows;
 //    one load instruction of the workgroup reads 4 KB of contiguous weight
 //    bytes of a row (thread t reads bytes [16 t, 16 t + 16) of the chunk),
 //    which are decoded with v_cvt_scalef32_pk_{f16,bf16}_fp8 into
@@ -36,33 +44,60 @@ __device__ inline float load_scale(const void* s, int kind, int n) {
   }
 }
 
+constexpr int MAX_SEGS = 8;
+
+// Weight matrices sharing one x; gstart[i] = first workgroup of segment i.
+struct GemvSegs {
+  const uint8_t* w[MAX_SEGS];
+  const void* s[MAX_SEGS];
+  uint16_t* y[MAX_SEGS];
+  int n[MAX_SEGS];
+  int gstart[MAX_SEGS + 1];
+  int count;
+};
+
+struct SegRef {
+  const uint8_t* w;
+  const void* s;
+  uint16_t* y;
+  int n, group;
+};
+
+__device__ inline SegRef find_seg(const GemvSegs& sg, int b) {
+  int i = 0;
+#pragma unroll
+  for (int j = 1; j < MAX_SEGS; ++j)
+    if (j < sg.count && b >= sg.gstart[j]) i = j;
+  return SegRef{sg.w[i], sg.s[i], sg.y[i], sg.n[i], b - sg.gstart[i]};
+}
+
 // ---------------------------------------------------------------------------
 // M <= MT (MT in {1, 2, 4}): v_dot2 path.  A 256-thread workgroup owns R
-// consecutive output rows; thread t handles the 16-byte weight units
-// t, t + 256, ... of every one of them, U units per round, so one load
+// consecutive output rows of one segment; thread t handles the 16-byte weight
+// units t, t + 256, ... of every one of them, U units per round, so one load
 // instruction of the workgroup covers 4 KB of a row and the R rows x U units
 // are in flight together.  Per-wave DPP sums, then an LDS combine of the four
-// waves.  Small workgroups dispatched in order keep the rows being read in
-// a sliding window of HBM, which streams better than long-lived persistent
+// waves.  Small workgroups dispatched in order keep the rows being read in a
+// sliding window of HBM, which streams better than long-lived persistent
 // waves each walking its own region.
 // ---------------------------------------------------------------------------
 template <typename T, int FMT, int MT, int R, int U>
-__global__ __launch_bounds__(256) void gemv_dot_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
-    const void* __restrict__ scale, int skind, uint16_t* __restrict__ y,
-    int M, int N, int K) {
+__global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
+                                                       int M, int K) {
   typedef typename T::pair P;
   __shared__ float red[4][MT * R];
+  const SegRef sr = find_seg(sg, blockIdx.x);
+  const int N = sr.n;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int row0 = blockIdx.x * R;
+  const int row0 = sr.group * R;
   const int K16 = K >> 4;
 
   const uint8_t* wrow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;  // clamped rows are never stored
-    wrow[r] = w + (size_t)row * K;
+    wrow[r] = sr.w + (size_t)row * K;
   }
   float acc[MT][R];
 #pragma unroll
@@ -130,26 +165,25 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(
     const int m = t / R, r = t % R, n = row0 + r;
     if (m < M && n < N) {
       const float s = red[0][t] + red[1][t] + red[2][t] + red[3][t];
-      y[(size_t)m * N + n] = T::from_f32(s * load_scale(scale, skind, n));
+      sr.y[(size_t)m * N + n] = T::from_f32(s * load_scale(sr.s, skind, n));
     }
   }
 }
 
 // ---------------------------------------------------------------------------
 // 4 < M <= 16: MFMA 16x16x32 path.  Workgroup = 4 waves = one 16*NT-row
-// tile; wave w takes the 64-byte K steps s with s % 4 == w.
+// tile of one segment; wave w takes the 64-byte K steps s with s % 4 == w.
 // ---------------------------------------------------------------------------
-
 template <typename T, int FMT, int NT, int UNROLL>
-__global__ __launch_bounds__(256) void gemv_mfma_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
-    const void* __restrict__ scale, int skind, uint16_t* __restrict__ y,
-    int M, int N, int K) {
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
+                                                        int M, int K) {
   typedef typename T::pair P;
   __shared__ f4 red[3][NT][64];
+  const SegRef sr = find_seg(sg, blockIdx.x);
+  const int N = sr.n;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16 * NT;
+  const int n0 = sr.group * 16 * NT;
   const int r16 = lane & 15;
   const int g = lane >> 4;
   const int steps = K >> 6;  // 64-byte K steps (K % 64 == 0 on this path)
@@ -159,7 +193,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(
   for (int t = 0; t < NT; ++t) {
     int row = n0 + t * 16 + r16;
     row = row < N ? row : N - 1;  // clamped rows are never stored
-    wrow[t] = w + (size_t)row * K + g * 16;
+    wrow[t] = sr.w + (size_t)row * K + g * 16;
   }
   const bool xrow_ok = r16 < M;
   const uint16_t* xrow = x + (size_t)(xrow_ok ? r16 : 0) * K + g * 16;
@@ -192,18 +226,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         u4 lo, hi;  // decoded weights for k-slots [0,8) and [8,16) of this lane
-        P p0 = fp8x2_to_pair<T, FMT, false>(wv[u][t][0]);
-        P p1 = fp8x2_to_pair<T, FMT, true>(wv[u][t][0]);
-        P p2 = fp8x2_to_pair<T, FMT, false>(wv[u][t][1]);
-        P p3 = fp8x2_to_pair<T, FMT, true>(wv[u][t][1]);
-        P p4 = fp8x2_to_pair<T, FMT, false>(wv[u][t][2]);
-        P p5 = fp8x2_to_pair<T, FMT, true>(wv[u][t][2]);
-        P p6 = fp8x2_to_pair<T, FMT, false>(wv[u][t][3]);
-        P p7 = fp8x2_to_pair<T, FMT, true>(wv[u][t][3]);
-        lo = u4{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-                __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
-        hi = u4{__builtin_bit_cast(uint32_t, p4), __builtin_bit_cast(uint32_t, p5),
-                __builtin_bit_cast(uint32_t, p6), __builtin_bit_cast(uint32_t, p7)};
+        decode16<T, FMT>(wv[u][t], lo, hi);
         // A = activations (row r16 = m), B = weights (column r16 = n).
         acc[t] = mfma16x16x32<T>(xa[u], lo, acc[t]);
         acc[t] = mfma16x16x32<T>(xb[u], hi, acc[t]);
@@ -222,47 +245,55 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(
     f4 c = acc[t] + red[0][t][lane] + red[1][t][lane] + red[2][t][lane];
     const int n = n0 + t * 16 + r16;  // D column = lane & 15
     if (n >= N) continue;
-    const float sc = load_scale(scale, skind, n);
+    const float sc = load_scale(sr.s, skind, n);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = g * 4 + v;  // D row = 4 * (lane >> 4) + v
-      if (m < M) y[(size_t)m * N + n] = T::from_f32(c[v] * sc);
+      if (m < M) sr.y[(size_t)m * N + n] = T::from_f32(c[v] * sc);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Generic: any M, K, alignment.  One wave per output row.
+// Generic: any M, K, alignment.  One wave per output row of a segment.
 // ---------------------------------------------------------------------------
 template <typename T, int FMT>
-__global__ __launch_bounds__(256) void gemv_generic_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
-    const void* __restrict__ scale, int skind, uint16_t* __restrict__ y,
-    int M, int N, int K) {
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
+                                                           int M, int K) {
+  const SegRef sr = find_seg(sg, blockIdx.x);
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const uint8_t* wr = w + (size_t)n * K;
-  const float sc = load_scale(scale, skind, n);
+  const int n = sr.group * 4 + (threadIdx.x >> 6);
+  if (n >= sr.n) return;
+  const uint8_t* wr = sr.w + (size_t)n * K;
+  const float sc = load_scale(sr.s, skind, n);
   for (int m = 0; m < M; ++m) {
     const uint16_t* xr = x + (size_t)m * K;
     float acc = 0.f;
     for (int k = lane; k < K; k += 64) acc += T::to_f32(xr[k]) * fp8_to_f32<FMT>(wr[k]);
     acc = wave_sum(acc);
-    if (lane == 0) y[(size_t)m * N + n] = T::from_f32(acc * sc);
+    if (lane == 0) sr.y[(size_t)m * sr.n + n] = T::from_f32(acc * sc);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
+// Fill gstart for `rows_per_wg` output rows per workgroup; returns the grid.
+static int seg_grid(GemvSegs& sg, int rows_per_wg) {
+  int g = 0;
+  for (int i = 0; i < sg.count; ++i) {
+    sg.gstart[i] = g;
+    g += (sg.n[i] + rows_per_wg - 1) / rows_per_wg;
+  }
+  for (int i = sg.count; i <= MAX_SEGS; ++i) sg.gstart[i] = g;
+  return g;
+}
+
 template <typename T, int FMT>
-static int launch_gemv_t(const void* x, const void* w, const void* scale, int skind, void* y,
-                         int M, int N, int K, hipStream_t st) {
+static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bool vec16, hipStream_t st) {
   const uint16_t* xp = static_cast<const uint16_t*>(x);
-  const uint8_t* wp = static_cast<const uint8_t*>(w);
-  uint16_t* yp = static_cast<uint16_t*>(y);
-  const bool vec16 = (K % 16 == 0) && aligned(x, 16) && aligned(w, 16);
+  int N = 0;  // launch shape is chosen from the total row count
+  for (int i = 0; i < sg.count; ++i) N += sg.n[i];
   if (vec16 && M <= 4) {
     // Rows per workgroup (measured on MI355X, one pass over > 2 GB of
     // rotating weights): 2 for M = 1 up to K = 4096, else 4, which amortises
@@ -270,7 +301,7 @@ static int launch_gemv_t(const void* x, const void* w, const void* scale, int sk
     // rows.  One 16-byte unit per thread and row per round.
     const int K16 = K / 16;
     const bool r2 = M == 1 && K16 <= 256;
-#define CEK_DOT(MT, R) gemv_dot_kernel<T, FMT, MT, R, 1><<<dim3((N + R - 1) / R), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
+#define CEK_DOT(MT, R) gemv_dot_kernel<T, FMT, MT, R, 1><<<dim3(seg_grid(sg, R)), 256, 0, st>>>(xp, sg, skind, M, K)
     if (M == 1) { if (r2) CEK_DOT(1, 2); else CEK_DOT(1, 4); }
     else if (M == 2) CEK_DOT(2, 4);
     else CEK_DOT(4, 4);
@@ -279,45 +310,83 @@ static int launch_gemv_t(const void* x, const void* w, const void* scale, int sk
     // 16-row tiles per wave (NT) and 64-byte K steps in flight per wave
     // (UNROLL), measured per shape class: wide N amortises the activation
     // reads over more tiles; narrow N needs more workgroups and deeper K.
-#define CEK_MF(NT, UN) gemv_mfma_kernel<T, FMT, NT, UN><<<dim3((N + 16 * NT - 1) / (16 * NT)), 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K)
+#define CEK_MF(NT, UN) gemv_mfma_kernel<T, FMT, NT, UN><<<dim3(seg_grid(sg, 16 * NT)), 256, 0, st>>>(xp, sg, skind, M, K)
     if (N >= 16384) CEK_MF(4, 4);
     else if (N >= 8192) { if (M > 8) CEK_MF(4, 2); else if (K <= 3072) CEK_MF(1, 8); else CEK_MF(2, 8); }
     else if (K <= 4096) { if (N >= 6144) CEK_MF(2, 16); else CEK_MF(1, 16); }
     else CEK_MF(1, 4);
 #undef CEK_MF
   } else {
-    dim3 grid((N + 3) / 4);
-    gemv_generic_kernel<T, FMT><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+    gemv_generic_kernel<T, FMT><<<dim3(seg_grid(sg, 4)), 256, 0, st>>>(xp, sg, skind, M, K);
   }
   return check_launch();
 }
 
+// Validates and launches one GEMV over count (<= MAX_SEGS) weight matrices.
+int launch_gemv_segs(const void* x, int count, const void* const* w, const void* const* scale,
+                     void* const* y, const int64_t* Ns, int64_t M, int64_t K, int skind, int io_dtype,
+                     int fp8_fmt, hipStream_t st) {
+  if (count < 1 || count > MAX_SEGS || !w || !scale || !y || !Ns) return CEK_ERR_INVALID;
+  if (M < 0 || K <= 0 || K > INT32_MAX) return CEK_ERR_INVALID;
+  if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
+  if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
+  GemvSegs sg{};
+  int64_t total = 0;
+  bool vec16 = K % 16 == 0 && aligned(x, 16);
+  for (int i = 0; i < count; ++i) {
+    if (Ns[i] < 0 || Ns[i] > INT32_MAX || Ns[i] * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
+    total += Ns[i];
+    sg.w[sg.count] = static_cast<const uint8_t*>(w[i]);
+    sg.s[sg.count] = scale[i];
+    sg.y[sg.count] = static_cast<uint16_t*>(y[i]);
+    sg.n[sg.count] = (int)Ns[i];
+    if (Ns[i] == 0) continue;  // empty matrices take no workgroups
+    if (!w[i] || !scale[i] || !y[i]) return CEK_ERR_INVALID;
+    vec16 = vec16 && aligned(w[i], 16);
+    ++sg.count;
+  }
+  if (total > INT32_MAX) return CEK_ERR_INVALID;
+  if (M == 0 || sg.count == 0) return CEK_OK;
+  if (M > 16) return CEK_ERR_INVALID;
+  if (!x) return CEK_ERR_INVALID;
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) return launch_gemv_t<F16, CEK_E4M3>(x, sg, skind, M, K, vec16, st);
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E5M2) return launch_gemv_t<F16, CEK_E5M2>(x, sg, skind, M, K, vec16, st);
+  if (fp8_fmt == CEK_E4M3) return launch_gemv_t<BF16, CEK_E4M3>(x, sg, skind, M, K, vec16, st);
+  return launch_gemv_t<BF16, CEK_E5M2>(x, sg, skind, M, K, vec16, st);
+}
+
 int launch_gemv(const void* x, const void* w, const void* scale, int skind, void* y,
                 int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st) {
-  if (M < 0 || N < 0 || K <= 0 || M > 16) return CEK_ERR_INVALID;
-  if (N > INT32_MAX || K > INT32_MAX || (int64_t)N * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
-  if (M == 0 || N == 0) return CEK_OK;
-  if (!x || !w || !scale || !y) return CEK_ERR_INVALID;
-  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) return launch_gemv_t<F16, CEK_E4M3>(x, w, scale, skind, y, M, N, K, st);
-  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E5M2) return launch_gemv_t<F16, CEK_E5M2>(x, w, scale, skind, y, M, N, K, st);
-  if (io_dtype == CEK_BF16 && fp8_fmt == CEK_E4M3) return launch_gemv_t<BF16, CEK_E4M3>(x, w, scale, skind, y, M, N, K, st);
-  if (io_dtype == CEK_BF16 && fp8_fmt == CEK_E5M2) return launch_gemv_t<BF16, CEK_E5M2>(x, w, scale, skind, y, M, N, K, st);
-  return CEK_ERR_INVALID;
+  if (N < 0) return CEK_ERR_INVALID;
+  if (M < 0 || M > 16) return CEK_ERR_INVALID;
+  if (M == 0 || N == 0) return K > 0 ? CEK_OK : CEK_ERR_INVALID;
+  return launch_gemv_segs(x, 1, &w, &scale, &y, &N, M, K, skind, io_dtype, fp8_fmt, st);
 }
 
 // Generic path for any M (used by the GEMM entry point for odd shapes).
 int launch_gemv_generic(const void* x, const void* w, const void* scale, int skind, void* y,
                         int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st) {
-  dim3 grid((unsigned)((N + 3) / 4));
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = static_cast<const uint8_t*>(w);
+  sg.s[0] = scale;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)N;
+  dim3 grid((unsigned)seg_grid(sg, 4));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
-  const uint8_t* wp = static_cast<const uint8_t*>(w);
-  uint16_t* yp = static_cast<uint16_t*>(y);
-  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) gemv_generic_kernel<F16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-  else if (io_dtype == CEK_F16 && fp8_fmt == CEK_E5M2) gemv_generic_kernel<F16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-  else if (io_dtype == CEK_BF16 && fp8_fmt == CEK_E4M3) gemv_generic_kernel<BF16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
-  else if (io_dtype == CEK_BF16 && fp8_fmt == CEK_E5M2) gemv_generic_kernel<BF16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) gemv_generic_kernel<F16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, sg, skind, M, K);
+  else if (io_dtype == CEK_F16 && fp8_fmt == CEK_E5M2) gemv_generic_kernel<F16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, sg, skind, M, K);
+  else if (io_dtype == CEK_BF16 && fp8_fmt == CEK_E4M3) gemv_generic_kernel<BF16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, sg, skind, M, K);
+  else if (io_dtype == CEK_BF16 && fp8_fmt == CEK_E5M2) gemv_generic_kernel<BF16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, sg, skind, M, K);
   else return CEK_ERR_INVALID;
   return check_launch();
+}
+
+static int scale_kind(int scale_dtype) {
+  if (scale_dtype == CEK_F16) return SK_F16;
+  if (scale_dtype == CEK_BF16) return SK_BF16;
+  if (scale_dtype == CEK_F32) return SK_F32;
+  return -1;
 }
 
 }  // namespace cek
@@ -325,11 +394,8 @@ int launch_gemv_generic(const void* x, const void* w, const void* scale, int ski
 extern "C" int cek_gemv_fp8_pern(const void* x, const void* w, const void* scale, void* y,
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
-  int skind;
-  if (scale_dtype == CEK_F16) skind = cek::SK_F16;
-  else if (scale_dtype == CEK_BF16) skind = cek::SK_BF16;
-  else if (scale_dtype == CEK_F32) skind = cek::SK_F32;
-  else return CEK_ERR_INVALID;
+  const int skind = cek::scale_kind(scale_dtype);
+  if (skind < 0) return CEK_ERR_INVALID;
   return cek::launch_gemv(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 
@@ -337,4 +403,20 @@ extern "C" int cek_gemv_fp8_pert(const void* x, const void* w, const float* scal
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, void* stream) {
   return cek::launch_gemv(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
+}
+
+extern "C" int cek_gemv_fp8_pern_multi(const void* x, int count, const void* const* w,
+                                       const void* const* scale, void* const* y, const int64_t* N,
+                                       int64_t M, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype,
+                                       void* stream) {
+  const int skind = cek::scale_kind(scale_dtype);
+  if (skind < 0) return CEK_ERR_INVALID;
+  return cek::launch_gemv_segs(x, count, w, scale, y, N, M, K, skind, io_dtype, fp8_fmt, (hipStream_t)stream);
+}
+
+extern "C" int cek_gemv_fp8_pert_multi(const void* x, int count, const void* const* w,
+                                       const float* const* scale, void* const* y, const int64_t* N,
+                                       int64_t M, int64_t K, int io_dtype, int fp8_fmt, void* stream) {
+  return cek::launch_gemv_segs(x, count, w, reinterpret_cast<const void* const*>(scale), y, N, M, K,
+                               cek::SK_F32_SCALAR, io_dtype, fp8_fmt, (hipStream_t)stream);
 }

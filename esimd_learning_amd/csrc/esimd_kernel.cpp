@@ -8,6 +8,7 @@
 #include "torch_ops.h"
 
 #include <algorithm>
+#include <vector>
 
 #include "shim_common.h"
 
@@ -82,6 +83,81 @@ at::Tensor esimd_gemv_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor w
   TORCH_CHECK(weight.dim() == 2, "esimd_gemv_fp8_pert: weight must be [N, K]");
   run_gemv(input, weight, weight_scale, output, weight.size(0), weight.size(1), true, "esimd_gemv_fp8_pert");
   return output;
+}
+
+// Fused GEMVs sharing `input`: one launch per group of up to 8 matrices.
+static void run_gemv_fused(const at::Tensor& input, const std::vector<at::Tensor>& weights,
+                           const std::vector<at::Tensor>& scales, const std::vector<at::Tensor>& outputs,
+                           bool per_tensor, const char* op) {
+  TORCH_CHECK(!weights.empty() && weights.size() == scales.size() && weights.size() == outputs.size(), op,
+              ": weights, weight_scales and outputs must be non-empty lists of one length");
+  TORCH_CHECK(is_io(input.scalar_type()), op, ": input must be fp16 or bf16");
+  TORCH_CHECK(input.is_cuda(), op, ": input must be a GPU tensor");
+  check_contig(input, op, "input");
+  const int64_t K = weights[0].dim() == 2 ? weights[0].size(1) : -1;
+  TORCH_CHECK(K > 0 && input.numel() % K == 0, op, ": weights must be [N_i, K] with input [M, K]");
+  const int64_t M = input.numel() / K;
+  TORCH_CHECK(M <= 16, op, ": at most 16 activation rows");
+  const int fmt = fp8_code(weights[0]);
+  int scale_code = CEK_F32;
+  for (size_t i = 0; i < weights.size(); ++i) {
+    const auto& w = weights[i];
+    const auto& sc = scales[i];
+    const auto& y = outputs[i];
+    check_fp8_weight(w, op);
+    TORCH_CHECK(fp8_code(w) == fmt, op, ": all weights must share one fp8 format");
+    TORCH_CHECK(w.dim() == 2 && w.size(1) == K, op, ": every weight must be [N_i, K]");
+    check_device(w, input, op, "weight");
+    check_device(sc, input, op, "weight_scale");
+    check_device(y, input, op, "output");
+    check_contig(w, op, "weight");
+    check_contig(sc, op, "weight_scale");
+    check_contig(y, op, "output");
+    TORCH_CHECK(y.scalar_type() == input.scalar_type(), op, ": outputs must have the input's dtype");
+    TORCH_CHECK(y.numel() == M * w.size(0), op, ": output ", i, " must be [M, N_i]");
+    if (per_tensor) {
+      TORCH_CHECK(sc.scalar_type() == at::ScalarType::Float && sc.numel() >= 1, op,
+                  ": weight_scales must be fp32 scalar tensors");
+    } else {
+      const auto st = sc.scalar_type();
+      TORCH_CHECK(st == at::ScalarType::Half || st == at::ScalarType::BFloat16 || st == at::ScalarType::Float, op,
+                  ": weight_scales must be fp16, bf16 or fp32");
+      const int code = st == at::ScalarType::Float ? CEK_F32 : (st == at::ScalarType::Half ? CEK_F16 : CEK_BF16);
+      TORCH_CHECK(i == 0 || code == scale_code, op, ": all weight_scales must share one dtype");
+      scale_code = code;
+      TORCH_CHECK(sc.numel() >= w.size(0), op, ": weight_scale ", i, " must hold N_i elements");
+    }
+  }
+  c10::OptionalDeviceGuard guard(input.device());
+  void* st = current_stream(input);
+  for (size_t b = 0; b < weights.size(); b += 8) {
+    const int cnt = (int)std::min<size_t>(8, weights.size() - b);
+    const void* wp[8];
+    const void* sp[8];
+    void* yp[8];
+    int64_t ns[8];
+    for (int i = 0; i < cnt; ++i) {
+      wp[i] = weights[b + i].data_ptr();
+      sp[i] = scales[b + i].data_ptr();
+      yp[i] = outputs[b + i].data_ptr();
+      ns[i] = weights[b + i].size(0);
+    }
+    const int io = io_code(input.scalar_type());
+    int rc = per_tensor ? cek_gemv_fp8_pert_multi(input.data_ptr(), cnt, wp, reinterpret_cast<const float* const*>(sp),
+                                                  yp, ns, M, K, io, fmt, st)
+                        : cek_gemv_fp8_pern_multi(input.data_ptr(), cnt, wp, sp, yp, ns, M, K, io, fmt, scale_code, st);
+    check_rc(rc, op);
+  }
+}
+
+void esimd_gemv_fp8_pern_fused(at::Tensor input, std::vector<at::Tensor> weights,
+                               std::vector<at::Tensor> weight_scales, std::vector<at::Tensor> outputs) {
+  run_gemv_fused(input, weights, weight_scales, outputs, false, "esimd_gemv_fp8_pern_fused");
+}
+
+void esimd_gemv_fp8_pert_fused(at::Tensor input, std::vector<at::Tensor> weights,
+                               std::vector<at::Tensor> weight_scales, std::vector<at::Tensor> outputs) {
+  run_gemv_fused(input, weights, weight_scales, outputs, true, "esimd_gemv_fp8_pert_fused");
 }
 
 static void check_norm(const at::Tensor& h, const at::Tensor& r, const at::Tensor& w, const char* op) {

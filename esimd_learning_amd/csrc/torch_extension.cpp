@@ -23,6 +23,14 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
   m.impl("esimd_fused_add_rms_norm_batched", c10::DispatchKey::CUDA, &esimd_fused_add_rms_norm_batched);
 
   // ---- new ops ----
+  m.def("esimd_gemv_fp8_pern_fused(Tensor input, Tensor[] weights, Tensor[] weight_scales, "
+        "Tensor(a!)[] outputs) -> ()");
+  m.impl("esimd_gemv_fp8_pern_fused", c10::DispatchKey::CUDA, &esimd_gemv_fp8_pern_fused);
+
+  m.def("esimd_gemv_fp8_pert_fused(Tensor input, Tensor[] weights, Tensor[] weight_scales, "
+        "Tensor(a!)[] outputs) -> ()");
+  m.impl("esimd_gemv_fp8_pert_fused", c10::DispatchKey::CUDA, &esimd_gemv_fp8_pert_fused);
+
   m.def("esimd_fused_add_rms_norm_quant_fp8(Tensor hidden_states, Tensor(a!) residual, Tensor weight, "
         "float eps, Tensor(b!) out_q, Tensor(c!) out_scale) -> ()");
   m.impl("esimd_fused_add_rms_norm_quant_fp8", c10::DispatchKey::CUDA, &esimd_fused_add_rms_norm_quant_fp8);

@@ -8,6 +8,8 @@
 
 #include <ATen/ATen.h>
 
+#include <vector>
+
 at::Tensor esimd_gemv_fp8_pern(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
                                at::Tensor output, int64_t N, int64_t K);
 
@@ -20,7 +22,14 @@ at::Tensor esimd_fused_add_rms_norm_batched(at::Tensor hidden_states, at::Tensor
 at::Tensor esimd_gemm_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
                                at::Tensor output);
 
-// ---- new ops (no reference counterpart) ----
+// ---- new ops (no reference op) ----
+// Fused GEMVs over several weight matrices sharing `input` (the reference's
+// unregistered GEMV_fp8_pern_fused_host / GEMV_fp8_pert_fused_host).
+void esimd_gemv_fp8_pern_fused(at::Tensor input, std::vector<at::Tensor> weights,
+                               std::vector<at::Tensor> weight_scales, std::vector<at::Tensor> outputs);
+void esimd_gemv_fp8_pert_fused(at::Tensor input, std::vector<at::Tensor> weights,
+                               std::vector<at::Tensor> weight_scales, std::vector<at::Tensor> outputs);
+
 void esimd_fused_add_rms_norm_quant_fp8(at::Tensor hidden_states, at::Tensor residual,
                                         at::Tensor weight, double eps, at::Tensor out_q,
                                         at::Tensor out_scale);

@@ -17,6 +17,8 @@ from custom_esimd_kernels_vllm.ops import (  # noqa: F401
     esimd_gemv_fp8_pert,
     esimd_fused_add_rms_norm_batched,
     esimd_gemm_fp8_pert,
+    esimd_gemv_fp8_pern_fused,
+    esimd_gemv_fp8_pert_fused,
     esimd_fused_add_rms_norm_quant_fp8,
     esimd_per_token_quant_fp8,
     esimd_gelu_and_mul,

@@ -65,6 +65,20 @@ def esimd_gemm_fp8_pert(
 
 # ---- new ops -------------------------------------------------------------
 
+def esimd_gemv_fp8_pern_fused(input, weights, weight_scales, outputs) -> None:
+    """Several per-channel-scale fp8 GEMVs sharing ``input`` in one launch.
+
+    weights[i]: [N_i, K] fp8; weight_scales[i]: [N_i]; outputs[i]: [M, N_i].
+    Each output equals esimd_gemv_fp8_pern on its own matrix.
+    """
+    _ops.esimd_gemv_fp8_pern_fused(input, list(weights), list(weight_scales), list(outputs))
+
+
+def esimd_gemv_fp8_pert_fused(input, weights, weight_scales, outputs) -> None:
+    """Several per-tensor-scale fp8 GEMVs sharing ``input`` in one launch."""
+    _ops.esimd_gemv_fp8_pert_fused(input, list(weights), list(weight_scales), list(outputs))
+
+
 def esimd_fused_add_rms_norm_quant_fp8(
     hidden_states: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
     out_q: torch.Tensor, out_scale: torch.Tensor,

@@ -66,6 +66,23 @@ int cek_gemv_fp8_pert(const void* x, const void* w, const float* scale, void* y,
                       int io_dtype, int fp8_fmt, void* stream);
 
 /*
+ * Several fp8-weight GEMVs that share one activation matrix, in one launch
+ * (e.g. Q, K and V, or gate and up projections).  Host arrays of `count`
+ * (1..8) device pointers / row counts: w[i] [N[i], K], scale[i] (per-channel
+ * of scale_dtype for _pern, fp32 device scalar for _pert), y[i] [M, N[i]].
+ * Each y[i] equals what cek_gemv_fp8_pern/pert computes for matrix i.
+ * Replaces the reference's GEMV_fp8_pern_fused_host (fp8_GEMV_v2.h:263-316)
+ * and GEMV_fp8_pert_fused_host (:506-558), csrc/xpu/esimd_kernels/, which
+ * the reference defines but does not register as an op.
+ */
+int cek_gemv_fp8_pern_multi(const void* x, int count, const void* const* w, const void* const* scale,
+                            void* const* y, const int64_t* N, int64_t M, int64_t K,
+                            int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+int cek_gemv_fp8_pert_multi(const void* x, int count, const void* const* w, const float* const* scale,
+                            void* const* y, const int64_t* N, int64_t M, int64_t K,
+                            int io_dtype, int fp8_fmt, void* stream);
+
+/*
  * fp8-weight GEMM, fp16|bf16 activations, per-tensor fp32 scale, any M.
  *   Y[m, n] = Out( (sum_k f32(X[m, k]) * dq(W[n, k])) * (*scale) )
  * M <= 16 uses the GEMV kernels; larger M a w8a16 MFMA GEMM.

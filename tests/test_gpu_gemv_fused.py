@@ -1,0 +1,71 @@
+"""Fused multi-matrix GEMV (one launch over several weights sharing x).
+
+The reference defines GEMV_fp8_pern_fused / GEMV_fp8_pert_fused
+(reference csrc/xpu/esimd_kernels/fp8_GEMV_v2.h:197-316, 440-558) but
+registers no op for them; its e5m2 fused test (tests/test_gemv_fp8.py:446-477)
+checks nothing.  Here each fused output must equal, bit for bit, the
+single-matrix op on the same matrix (the same kernels run over a segment
+table), and match the oracle.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from conftest import assert_close_fp
+from esimd_learning_amd import synthetic
+from oracle import gemv as ogemv
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("Ns,K", [((4096, 1024, 1024), 3072), ((14336, 14336), 4096), ((512, 512), 2048),
+                                  ((100, 7, 2049), 1024), ((4096,), 14336)])
+def test_pern_fused_equals_separate(ops, dev, M, Ns, K):
+    _say(f"fused pern M={M} Ns={Ns} K={K}")
+    Ws, Ss = zip(*[synthetic.weight_fp8(n, K, seed=n + i) for i, n in enumerate(Ns)])
+    x = synthetic.activations(M, K, seed=5)
+    xd = x.to(dev)
+    Wd = [w.to(dev) for w in Ws]
+    Sd = [s.to(dev) for s in Ss]
+    ys = [torch.zeros(M, n, dtype=torch.float16, device=dev) for n in Ns]
+    ops.esimd_gemv_fp8_pern_fused(xd, Wd, Sd, ys)
+    for i, n in enumerate(Ns):
+        y1 = torch.zeros(M, n, dtype=torch.float16, device=dev)
+        ops.esimd_gemv_fp8_pern(xd, Wd[i], Sd[i], y1, n, K)
+        torch.cuda.synchronize()
+        assert torch.equal(ys[i], y1), f"matrix {i}"
+        assert_close_fp(ys[i].cpu(), ogemv.gemv_fp8_pern(x, Ws[i], Ss[i]), f"matrix {i}")
+
+
+def test_pert_fused_e5m2_and_many(ops, dev):
+    # ten matrices (two launches of up to eight), e5m2, per-tensor scales
+    K, M = 2048, 1
+    Ns = [512, 256, 128, 64, 512, 16, 48, 512, 1024, 32]
+    g = torch.Generator().manual_seed(0)
+    Ws = [(torch.randn(n, K, generator=g).half() * 0.1).to(torch.float8_e5m2) for n in Ns]
+    Ss = [torch.tensor(0.05 + 0.01 * i) for i in range(len(Ns))]
+    x = (torch.randn(M, K, generator=g) * 0.1).half()
+    ys = [torch.zeros(M, n, dtype=torch.float16, device=dev) for n in Ns]
+    ops.esimd_gemv_fp8_pert_fused(x.to(dev), [w.to(dev) for w in Ws], [s.to(dev) for s in Ss], ys)
+    torch.cuda.synchronize()
+    for i in range(len(Ns)):
+        assert_close_fp(ys[i].cpu(), ogemv.gemv_fp8_pert(x, Ws[i], Ss[i]), f"matrix {i}")
+
+
+def test_fused_rejects_mismatch(ops, dev):
+    x = torch.zeros(1, 64, dtype=torch.float16, device=dev)
+    w = torch.zeros(8, 64, dtype=torch.float8_e4m3fn, device=dev)
+    with pytest.raises(RuntimeError, match="one length"):
+        ops.esimd_gemv_fp8_pern_fused(x, [w, w], [torch.ones(8, device=dev)], [torch.zeros(1, 8, dtype=torch.float16, device=dev)])
+    with pytest.raises(RuntimeError, match=r"\[N_i, K\]"):
+        ops.esimd_gemv_fp8_pern_fused(x, [w, torch.zeros(8, 32, dtype=torch.float8_e4m3fn, device=dev)],
+                                      [torch.ones(8, device=dev)] * 2,
+                                      [torch.zeros(1, 8, dtype=torch.float16, device=dev)] * 2)

@@ -70,6 +70,18 @@ __device__ inline f4 mfma16x16x32<BF16>(u4 a, u4 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
 }
 
+// C += A * B^T on one 16 x 16 x 128 fp8 MFMA block (32 OCP e4m3 bytes per
+// lane; cbsz = blgp = 0 select e4m3 for both operands; block scales unused).
+__device__ inline f4 mfma_fp8_16x16x128(const i8& a, const i8& b, f4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ inline i8 cat_i8(u4 lo, u4 hi) {
+  return i8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
 // Decode 16 fp8 bytes into two u4 of activation-typed values (k-slots 0-7, 8-15).
 template <typename T, int FMT>
 __device__ inline void decode16(u4 w, u4& lo, u4& hi) {

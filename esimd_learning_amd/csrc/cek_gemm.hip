@@ -24,11 +24,10 @@ int launch_gemv(const void* x, const void* w, const void* scale, int skind, void
                 int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st);
 int launch_gemv_generic(const void* x, const void* w, const void* scale, int skind, void* y,
                         int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st);
-
-__device__ inline f4 mfma_fp8_16x16x128(const i8& a, const i8& b, f4 c) {
-  // cbsz = blgp = 0: both operands OCP e4m3; scale operands unused (0).
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
+int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const float* ws, void* y,
+                     int64_t M, int64_t N, int64_t K, int out_dtype, hipStream_t st);
+int launch_gemv_wide(const void* x, const void* w, const void* scale, int skind, void* y,
+                     int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st);
 
 // ---------------------------------------------------------------------------
 // a8w8, direct-from-global v0: workgroup = 4 waves = 64 x 64 C tile, each wave
@@ -126,8 +125,6 @@ __device__ inline void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn
   tm = first_m + tin % gsize;
   tn = tin / gsize;
 }
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Direct-to-LDS loads of one K step (128 bytes) of the A and B slices into a
 // stage: this wave's 1 KB writer chunks j = wave + 4 i (rows 8 j .. 8 j + 7).
@@ -417,6 +414,10 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   if (M <= 16) return launch_gemv(x, w, scale, 3 /* f32 scalar */, y, M, N, K, io_dtype, fp8_fmt, st);
+  if (M <= 32 && aligned(x, 16) && aligned(w, 16)) {
+    const int rc = launch_gemv_wide(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
+    if (rc != CEK_ERR_UNSUPPORTED) return rc;
+  }
   if (K % 64 != 0 || !aligned(x, 16) || !aligned(w, 16) || M > 65535 * 64)
     return launch_gemv_generic(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
   {
@@ -454,7 +455,14 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
   if (!aligned(a, 16) || !aligned(b, 16)) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   uint16_t* yp = static_cast<uint16_t*>(y);
-  if (K % 128 == 0 && (out_dtype == CEK_F16 || out_dtype == CEK_BF16)) {
+  if (out_dtype != CEK_F16 && out_dtype != CEK_BF16) return CEK_ERR_INVALID;
+  // Skinny A: stream the weights once with the GEMV kernels rather than tile
+  // a mostly empty GEMM (they decline the shapes the tiles serve better).
+  if (M <= 64) {
+    const int rc = launch_gemv_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, st);
+    if (rc != CEK_ERR_UNSUPPORTED) return rc;
+  }
+  if (K % 128 == 0) {
     // Tile choice (measured on MI355X over the BASELINE prefill shapes):
     // 128 x 128 tiles let two workgroups share a CU, so one's MFMAs cover the
     // other's LDS and barrier waits; 64 x 128 gives more tiles when there are

@@ -29,6 +29,8 @@
 //    contiguous bytes per row per round) and reduce through LDS.
 //  * gemv_generic_kernel: any K / alignment; byte loads.  Correctness path
 //    for shapes the vector kernels do not take.
+#include <type_traits>
+
 #include "cek_common.h"
 
 namespace cek {
@@ -54,6 +56,7 @@ struct GemvSegs {
   int n[MAX_SEGS];
   int gstart[MAX_SEGS + 1];
   int count;
+  const float* xs;  // per-row activation scales [M] when x holds e4m3 codes
 };
 
 struct SegRef {
@@ -81,7 +84,9 @@ __device__ inline SegRef find_seg(const GemvSegs& sg, int b) {
 // sliding window of HBM, which streams better than long-lived persistent
 // waves each walking its own region.
 // ---------------------------------------------------------------------------
-template <typename T, int FMT, int MT, int R, int U>
+// With XF8 the activations are e4m3 codes (x points at bytes) decoded exactly
+// into T pairs, and the epilogue multiplies by the row's activation scale.
+template <typename T, typename TO, int FMT, bool XF8, int MT, int R, int U>
 __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
                                                        int M, int K) {
   typedef typename T::pair P;
@@ -125,9 +130,18 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
       const int idx = min(base + u * 256, K16 - 1);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const P* xp = reinterpret_cast<const P*>(x + (size_t)min(m, M - 1) * K + (size_t)idx * 16);
+        if (XF8) {
+          const u4 c = load_u4(reinterpret_cast<const uint8_t*>(x) + (size_t)min(m, M - 1) * K + (size_t)idx * 16);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xv[u][m][j] = xp[j];
+          for (int j = 0; j < 4; ++j) {
+            xv[u][m][2 * j] = fp8x2_to_pair<T, CEK_E4M3, false>(c[j]);
+            xv[u][m][2 * j + 1] = fp8x2_to_pair<T, CEK_E4M3, true>(c[j]);
+          }
+        } else {
+          const P* xp = reinterpret_cast<const P*>(x + (size_t)min(m, M - 1) * K + (size_t)idx * 16);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xv[u][m][j] = xp[j];
+        }
       }
     }
     // Keep the scheduler from sinking the loads into the arithmetic below (it
@@ -164,8 +178,9 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
   if (t < MT * R) {
     const int m = t / R, r = t % R, n = row0 + r;
     if (m < M && n < N) {
-      const float s = red[0][t] + red[1][t] + red[2][t] + red[3][t];
-      sr.y[(size_t)m * N + n] = T::from_f32(s * load_scale(sr.s, skind, n));
+      float s = red[0][t] + red[1][t] + red[2][t] + red[3][t];
+      if (XF8) s *= sg.xs[m];
+      sr.y[(size_t)m * N + n] = TO::from_f32(s * load_scale(sr.s, skind, n));
     }
   }
 }
@@ -174,7 +189,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
 // 4 < M <= 16: MFMA 16x16x32 path.  Workgroup = 4 waves = one 16*NT-row
 // tile of one segment; wave w takes the 64-byte K steps s with s % 4 == w.
 // ---------------------------------------------------------------------------
-template <typename T, int FMT, int NT, int UNROLL>
+template <typename T, typename TO, int FMT, bool XF8, int NT, int UNROLL>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
                                                         int M, int K) {
   typedef typename T::pair P;
@@ -197,6 +212,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
   }
   const bool xrow_ok = r16 < M;
   const uint16_t* xrow = x + (size_t)(xrow_ok ? r16 : 0) * K + g * 16;
+  const uint8_t* xrow8 = reinterpret_cast<const uint8_t*>(x) + (size_t)(xrow_ok ? r16 : 0) * K + g * 16;
 
   f4 acc[NT];
 #pragma unroll
@@ -211,7 +227,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         wv[u][t] = s < steps ? load_u4_stream(wrow[t] + (size_t)s * 64) : u4{0, 0, 0, 0};
-      if (s < steps && xrow_ok) {
+      if (s < steps && xrow_ok && XF8) {
+        decode16<T, CEK_E4M3>(load_u4(xrow8 + (size_t)s * 64), xa[u], xb[u]);
+      } else if (s < steps && xrow_ok) {
         const u4* xp = reinterpret_cast<const u4*>(xrow + (size_t)s * 64);
         xa[u] = xp[0];
         xb[u] = xp[1];
@@ -249,9 +267,184 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = g * 4 + v;  // D row = 4 * (lane >> 4) + v
-      if (m < M) sr.y[(size_t)m * N + n] = T::from_f32(c[v] * sc);
+      if (m < M) sr.y[(size_t)m * N + n] = TO::from_f32(c[v] * (XF8 ? sc * sg.xs[m] : sc));
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// 4 < M <= 64, K % 1024 == 0: LDS-staged MFMA path.
+//
+// HBM streams best when every load instruction of a wave reads 1 KB of ONE
+// row (measured on MI355X: 6.4 TB/s, against 4.0-5.3 TB/s when an instruction
+// gathers 64-512-byte pieces of 16 rows, which is what an MFMA operand needs).
+// So the weights go through LDS: stage i holds bytes [1024 i, 1024 i + 1024)
+// of the workgroup's 16*NT rows, each row filled by one direct-to-LDS load
+// (global_load_lds_dwordx4; lane j's 16 bytes land at row base + 16 j).  Lane j
+// fetches 16-byte unit j ^ (row & 15) instead of unit j -- the same 1 KB --
+// so unit v of row r sits at slot v ^ (r & 15), and the sixteen rows an MFMA
+// fragment read touches fall in sixteen different bank groups.  Two stages
+// alternate: the next stage's loads are issued right after the barrier that
+// publishes the current one and run under its arithmetic.
+//
+// The activations (a few hundred KB at most) are read from L2 straight into
+// MFMA operand layout, before the next stage's weights so that waiting for
+// them leaves those in flight.  Each wave takes a quarter of a stage's K
+// units; the four partial sums meet in LDS at the end.
+//
+//  * gemv_lds_kernel: fp16/bf16 activations; a lane's 16-byte weight unit
+//    (16 K values) is decoded to two 8-value operands of
+//    v_mfma_f32_16x16x32_{f16,bf16}.
+//  * gemv_lds_a8w8_kernel: e4m3 activation codes with per-row scales; two
+//    units per lane feed one v_mfma_f32_16x16x128_f8f6f4 (no decode).
+// ---------------------------------------------------------------------------
+template <int NT, int MB>
+__device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wave, int lane, int n0, int N,
+                                        int M, const SegRef& sr, int skind, const float* xs, bool bf16_out) {
+  f4* red = reinterpret_cast<f4*>(smem);  // [3][NT][MB][64]
+  __syncthreads();                         // every wave is done with the stages
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) red[(((wave - 1) * NT + t) * MB + b) * 64 + lane] = acc[t][b];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int n16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = n0 + t * 16 + n16;  // D column = lane & 15
+    if (n >= N) continue;
+    const float sc = load_scale(sr.s, skind, n);
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      f4 c = acc[t][b];
+#pragma unroll
+      for (int w = 0; w < 3; ++w) c += red[((w * NT + t) * MB + b) * 64 + lane];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = b * 16 + g * 4 + v;  // D row = 4 * (lane >> 4) + v
+        if (m >= M) continue;
+        const float o = c[v] * (xs ? sc * xs[m] : sc);
+        sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+      }
+    }
+  }
+}
+
+// LDS writes of this wave done, then a workgroup barrier -- without the
+// vmcnt(0) a fenced __syncthreads adds, which would drain the loads of the
+// stages in flight.  The "memory" clobber keeps LDS accesses (and the
+// activation loads, which are therefore not __restrict__) on their side.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One kernel for both activation kinds.  XF8 = false: x is T (fp16/bf16), a
+// lane's 16-byte weight unit (16 K values) is decoded to two 8-value operands
+// of v_mfma_f32_16x16x32_{f16,bf16}.  XF8 = true: x holds e4m3 codes with
+// per-row scales sg.xs; two units per lane feed one
+// v_mfma_f32_16x16x128_f8f6f4 with no decode.
+//
+// Stage i = bytes [1024 i, 1024 i + 1024) of the workgroup's 16*NT weight
+// rows plus the activation operands that go with them.  Loads run D stages
+// ahead into registers (a ring of D + 1 slots, so the loop body is unrolled
+// D + 1 times); stage i is copied into one of two LDS buffers, then read back
+// in MFMA layout.  K = 1024 STEPS.
+template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS>
+__global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M) {
+  static_assert(D >= 1 && D <= STEPS, "prefetch depth");
+  constexpr int K = STEPS * 1024;
+  constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
+  constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
+  constexpr int XB = XF8 ? 1 : 2;  // activation bytes per value
+  constexpr int LW = ROWS / 4;     // weight rows per wave and stage
+  __shared__ __align__(16) uint8_t smem[2 * STAGE];
+  const SegRef sr = find_seg(sg, blockIdx.x);
+  const int N = sr.n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n16 = lane & 15, g = lane >> 4;
+  const int n0 = sr.group * ROWS;
+  const uint8_t* gw[LW];  // this wave loads rows wave + 4 j of every stage
+#pragma unroll
+  for (int j = 0; j < LW; ++j) {
+    const int r = wave + 4 * j;
+    gw[j] = sr.w + (size_t)min(n0 + r, N - 1) * K + 16 * (lane ^ (r & 15));  // clamped rows are never stored
+  }
+  const uint8_t* gx[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b)  // rows >= M are never stored
+    gx[b] = static_cast<const uint8_t*>(xv) + (size_t)min(16 * b + n16, M - 1) * K * XB;
+
+  // Unit (16 K values) of operand group q for this lane: XF8 = false: unit
+  // 4 (wave + 4 q) + g; XF8 = true: units 2 (4 (wave + 4 q) + g) and the next.
+  auto unit = [&](int q) { return XF8 ? 2 * (4 * (wave + 4 * q) + g) : 4 * (wave + 4 * q) + g; };
+
+  u4 wr[S][LW];
+  u4 xr[S][QN][MB][2];
+  auto issue = [&](int i, u4 (&ws)[LW], u4 (&xs)[QN][MB][2]) {
+    const int k0 = i << 10;
+#pragma unroll
+    for (int j = 0; j < LW; ++j) ws[j] = load_u4_stream(gw[j] + k0);  // 1 KB of one row per instruction
+    asm volatile("" ::: "memory");  // same issue order in every step (weights, then activations)
+#pragma unroll
+    for (int q = 0; q < QN; ++q)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        const u4* p = reinterpret_cast<const u4*>(gx[b] + (size_t)(k0 + 16 * unit(q)) * XB);
+        xs[q][b][0] = p[0];
+        xs[q][b][1] = p[1];
+      }
+    asm volatile("" ::: "memory");
+  };
+
+  f4 acc[NT][MB];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // Fully unrolled over the STEPS stages (the host instantiates the K values
+  // it supports), so every slot index and every condition is static and the
+  // compiler's in-order vmcnt waits are exact: the wait for stage i leaves
+  // the loads of the stages after it in flight.
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue(j, wr[j], xr[j]);
+#pragma unroll
+  for (int i = 0; i < STEPS; ++i) {
+    // Stage i into LDS buffer i & 1 (last read at step i - 2, which every
+    // wave finished before the barrier of step i - 1).  Lane l's unit lands
+    // at slot l, i.e. unit v of row r at slot v ^ (r & 15).
+    uint8_t* sw = smem + (i & 1) * STAGE;
+#pragma unroll
+    for (int jj = 0; jj < LW; ++jj) *reinterpret_cast<u4*>(sw + (wave + 4 * jj) * 1024 + 16 * lane) = wr[i % S][jj];
+    lds_barrier();
+    if (i + D < STEPS) issue(i + D, wr[(i + D) % S], xr[(i + D) % S]);
+#pragma unroll
+    for (int q = 0; q < QN; ++q) {
+      const int v = unit(q);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint8_t* rw = sw + (16 * t + n16) * 1024;  // row 16 t + n16: slots are v ^ n16
+        if constexpr (XF8) {
+          const i8 bf = cat_i8(*reinterpret_cast<const u4*>(rw + 16 * (v ^ n16)),
+                               *reinterpret_cast<const u4*>(rw + 16 * ((v + 1) ^ n16)));
+#pragma unroll
+          for (int b = 0; b < MB; ++b)
+            acc[t][b] = mfma_fp8_16x16x128(cat_i8(xr[i % S][q][b][0], xr[i % S][q][b][1]), bf, acc[t][b]);
+        } else {
+          u4 lo, hi;
+          decode16<T, FMT>(*reinterpret_cast<const u4*>(rw + 16 * (v ^ n16)), lo, hi);
+#pragma unroll
+          for (int b = 0; b < MB; ++b) {
+            acc[t][b] = mfma16x16x32<T>(xr[i % S][q][b][0], lo, acc[t][b]);
+            acc[t][b] = mfma16x16x32<T>(xr[i % S][q][b][1], hi, acc[t][b]);
+          }
+        }
+      }
+    }
+  }
+  lds_reduce_store<NT, MB>(acc, smem, wave, lane, n0, N, M, sr, skind, XF8 ? sg.xs : nullptr,
+                           std::is_same<TO, BF16>::value);
 }
 
 // ---------------------------------------------------------------------------
@@ -289,11 +482,67 @@ static int seg_grid(GemvSegs& sg, int rows_per_wg) {
   return g;
 }
 
-template <typename T, int FMT>
+// LDS-staged path: configuration per (rows M, total weight rows N, K stages),
+// from sweeps on MI355X over the decode shapes.  Returns false when no
+// instantiation covers the shape (K not one of 2, 3, 4, 5, 14 or 24 KiB
+// values, or M / N outside the ranges below); the caller then uses another
+// kernel.  Requires 16-byte aligned x and weights.
+template <typename T, typename TO, int FMT, bool XF8, int S>
+static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int N, hipStream_t st) {
+#define CEK_LDS(NT, MB, D) \
+  gemv_lds_kernel<T, TO, FMT, XF8, NT, MB, D, S><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M)
+  constexpr bool SHORT = S >= 3 && S <= 5;
+  if (M <= 16) {
+    if constexpr (SHORT) {
+      // Two 16-row tiles per workgroup halve the activation re-reads once
+      // there are enough rows to keep >= 192 workgroups.
+      if (N >= 6144 && (XF8 ? M > 8 : M >= 8)) CEK_LDS(2, 1, 2);
+      else CEK_LDS(1, 1, 3);
+    } else if constexpr (XF8 && S >= 3) {
+      CEK_LDS(1, 1, 3);
+    } else {
+      CEK_LDS(1, 1, 2);
+    }
+    return true;
+  }
+  if (M <= 32 && N <= 16384) {  // wider N is served as well by the tiled GEMM
+    if constexpr (XF8) CEK_LDS(1, 2, 2);
+    else CEK_LDS(1, 2, 1);
+    return true;
+  }
+  if constexpr (XF8) {
+    if (M <= 64 && N <= 8192) {
+      CEK_LDS(1, 4, 1);
+      return true;
+    }
+  }
+  return false;
+#undef CEK_LDS
+}
+
+template <typename T, typename TO, int FMT, bool XF8>
+static bool launch_lds(const void* x, GemvSegs& sg, int skind, int M, int K, int N, hipStream_t st) {
+  if (K % 1024 != 0) return false;
+  switch (K >> 10) {
+    case 2: return launch_lds_steps<T, TO, FMT, XF8, 2>(x, sg, skind, M, N, st);
+    case 3: return launch_lds_steps<T, TO, FMT, XF8, 3>(x, sg, skind, M, N, st);
+    case 4: return launch_lds_steps<T, TO, FMT, XF8, 4>(x, sg, skind, M, N, st);
+    case 5: return launch_lds_steps<T, TO, FMT, XF8, 5>(x, sg, skind, M, N, st);
+    case 14: return launch_lds_steps<T, TO, FMT, XF8, 14>(x, sg, skind, M, N, st);
+    case 24: return launch_lds_steps<T, TO, FMT, XF8, 24>(x, sg, skind, M, N, st);
+    default: return false;
+  }
+}
+
+template <typename T, typename TO, int FMT, bool XF8>
 static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bool vec16, hipStream_t st) {
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   int N = 0;  // launch shape is chosen from the total row count
   for (int i = 0; i < sg.count; ++i) N += sg.n[i];
+  // M >= 3: the LDS-staged MFMA kernel (measured faster than the v_dot2
+  // kernel from three rows on, and than the direct MFMA kernel throughout).
+  if (vec16 && M >= 3 && launch_lds<T, TO, FMT, XF8>(x, sg, skind, M, K, N, st)) return check_launch();
+  if (M > 16) return CEK_ERR_UNSUPPORTED;
   if (vec16 && M <= 4) {
     // Rows per workgroup (measured on MI355X, one pass over > 2 GB of
     // rotating weights): 2 for M = 1 up to K = 4096, else 4, which amortises
@@ -301,7 +550,7 @@ static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bo
     // rows.  One 16-byte unit per thread and row per round.
     const int K16 = K / 16;
     const bool r2 = M == 1 && K16 <= 256;
-#define CEK_DOT(MT, R) gemv_dot_kernel<T, FMT, MT, R, 1><<<dim3(seg_grid(sg, R)), 256, 0, st>>>(xp, sg, skind, M, K)
+#define CEK_DOT(MT, R) gemv_dot_kernel<T, TO, FMT, XF8, MT, R, 1><<<dim3(seg_grid(sg, R)), 256, 0, st>>>(xp, sg, skind, M, K)
     if (M == 1) { if (r2) CEK_DOT(1, 2); else CEK_DOT(1, 4); }
     else if (M == 2) CEK_DOT(2, 4);
     else CEK_DOT(4, 4);
@@ -310,22 +559,27 @@ static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bo
     // 16-row tiles per wave (NT) and 64-byte K steps in flight per wave
     // (UNROLL), measured per shape class: wide N amortises the activation
     // reads over more tiles; narrow N needs more workgroups and deeper K.
-#define CEK_MF(NT, UN) gemv_mfma_kernel<T, FMT, NT, UN><<<dim3(seg_grid(sg, 16 * NT)), 256, 0, st>>>(xp, sg, skind, M, K)
+#define CEK_MF(NT, UN) gemv_mfma_kernel<T, TO, FMT, XF8, NT, UN><<<dim3(seg_grid(sg, 16 * NT)), 256, 0, st>>>(xp, sg, skind, M, K)
     if (N >= 16384) CEK_MF(4, 4);
     else if (N >= 8192) { if (M > 8) CEK_MF(4, 2); else if (K <= 3072) CEK_MF(1, 8); else CEK_MF(2, 8); }
     else if (K <= 4096) { if (N >= 6144) CEK_MF(2, 16); else CEK_MF(1, 16); }
     else CEK_MF(1, 4);
 #undef CEK_MF
-  } else {
+  } else if (!XF8) {
     gemv_generic_kernel<T, FMT><<<dim3(seg_grid(sg, 4)), 256, 0, st>>>(xp, sg, skind, M, K);
+  } else {
+    return CEK_ERR_UNSUPPORTED;  // the caller only routes vector-friendly shapes here
   }
   return check_launch();
 }
 
 // Validates and launches one GEMV over count (<= MAX_SEGS) weight matrices.
+// M <= 16 for the GEMV entry points; the GEMM entry point also sends
+// 16 < M <= 32 here (max_m = 32), which only the LDS path takes
+// (CEK_ERR_UNSUPPORTED otherwise).
 int launch_gemv_segs(const void* x, int count, const void* const* w, const void* const* scale,
                      void* const* y, const int64_t* Ns, int64_t M, int64_t K, int skind, int io_dtype,
-                     int fp8_fmt, hipStream_t st) {
+                     int fp8_fmt, hipStream_t st, int max_m = 16) {
   if (count < 1 || count > MAX_SEGS || !w || !scale || !y || !Ns) return CEK_ERR_INVALID;
   if (M < 0 || K <= 0 || K > INT32_MAX) return CEK_ERR_INVALID;
   if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
@@ -347,12 +601,35 @@ int launch_gemv_segs(const void* x, int count, const void* const* w, const void*
   }
   if (total > INT32_MAX) return CEK_ERR_INVALID;
   if (M == 0 || sg.count == 0) return CEK_OK;
-  if (M > 16) return CEK_ERR_INVALID;
+  if (M > max_m) return CEK_ERR_INVALID;
   if (!x) return CEK_ERR_INVALID;
-  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) return launch_gemv_t<F16, CEK_E4M3>(x, sg, skind, M, K, vec16, st);
-  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E5M2) return launch_gemv_t<F16, CEK_E5M2>(x, sg, skind, M, K, vec16, st);
-  if (fp8_fmt == CEK_E4M3) return launch_gemv_t<BF16, CEK_E4M3>(x, sg, skind, M, K, vec16, st);
-  return launch_gemv_t<BF16, CEK_E5M2>(x, sg, skind, M, K, vec16, st);
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) return launch_gemv_t<F16, F16, CEK_E4M3, false>(x, sg, skind, M, K, vec16, st);
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E5M2) return launch_gemv_t<F16, F16, CEK_E5M2, false>(x, sg, skind, M, K, vec16, st);
+  if (fp8_fmt == CEK_E4M3) return launch_gemv_t<BF16, BF16, CEK_E4M3, false>(x, sg, skind, M, K, vec16, st);
+  return launch_gemv_t<BF16, BF16, CEK_E5M2, false>(x, sg, skind, M, K, vec16, st);
+}
+
+// a8w8 for skinny A (M <= 64): x [M, K] e4m3 codes with per-row scales
+// xs [M], e4m3 weights with per-channel fp32 scales; fp16 or bf16 output.
+// Requires 16-byte aligned x and w and K % 16 == 0 (the caller checks).
+// Returns CEK_ERR_UNSUPPORTED for shapes it leaves to the tiled GEMM.
+int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const float* ws, void* y,
+                     int64_t M, int64_t N, int64_t K, int out_dtype, hipStream_t st) {
+  if (M < 1 || M > 64 || N < 1 || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_UNSUPPORTED;
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = w;
+  sg.s[0] = ws;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)N;
+  sg.xs = xs;
+  if (M > 16) {  // only the LDS path takes these
+    const bool ok = out_dtype == CEK_F16 ? launch_lds<F16, F16, CEK_E4M3, true>(x, sg, SK_F32, (int)M, (int)K, (int)N, st)
+                                         : launch_lds<F16, BF16, CEK_E4M3, true>(x, sg, SK_F32, (int)M, (int)K, (int)N, st);
+    return ok ? check_launch() : CEK_ERR_UNSUPPORTED;
+  }
+  if (out_dtype == CEK_F16) return launch_gemv_t<F16, F16, CEK_E4M3, true>(x, sg, SK_F32, (int)M, (int)K, true, st);
+  return launch_gemv_t<F16, BF16, CEK_E4M3, true>(x, sg, SK_F32, (int)M, (int)K, true, st);
 }
 
 int launch_gemv(const void* x, const void* w, const void* scale, int skind, void* y,
@@ -361,6 +638,13 @@ int launch_gemv(const void* x, const void* w, const void* scale, int skind, void
   if (M < 0 || M > 16) return CEK_ERR_INVALID;
   if (M == 0 || N == 0) return K > 0 ? CEK_OK : CEK_ERR_INVALID;
   return launch_gemv_segs(x, 1, &w, &scale, &y, &N, M, K, skind, io_dtype, fp8_fmt, st);
+}
+
+// 16 < M <= 32 (GEMM entry point): the LDS path when it covers the shape.
+int launch_gemv_wide(const void* x, const void* w, const void* scale, int skind, void* y,
+                     int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st) {
+  if (M <= 16 || M > 32 || N <= 0) return CEK_ERR_UNSUPPORTED;
+  return launch_gemv_segs(x, 1, &w, &scale, &y, &N, M, K, skind, io_dtype, fp8_fmt, st, 32);
 }
 
 // Generic path for any M (used by the GEMM entry point for odd shapes).

@@ -108,3 +108,17 @@ def test_a8w8_rejects_bad_k(ops, dev):
     with pytest.raises(RuntimeError, match="multiple of 16"):
         ops.esimd_gemm_fp8_a8w8(a, torch.ones(4, device=dev), a, torch.ones(4, device=dev),
                                 torch.zeros(4, 4, dtype=torch.float16, device=dev))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 13, 16])
+@pytest.mark.parametrize("K,N", [(1024, 600), (4096, 1040)])
+def test_a8w8_decode_rows(ops, dev, M, K, N):
+    """M <= 16 takes the weight-streaming GEMV kernels with fp8 activations."""
+    _say(f"a8w8 decode M={M} K={K} N={N}")
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M * 7 + K + N)
+    ref = ogemm.gemm_a8w8(q, sa, W8, sb)
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.zeros(M, N, dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ref, f"a8w8 decode M={M} {out_dt}")

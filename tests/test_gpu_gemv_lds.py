@@ -1,0 +1,108 @@
+"""GPU parity of the LDS-staged GEMV kernel across its dispatch branches.
+
+The kernel is instantiated per K (2, 3, 4, 5, 14 and 24 KiB values) and per
+configuration (one or two 16-row weight tiles per workgroup, one to four
+16-row activation blocks, prefetch depth); these cases reach each of them
+through the public ops:
+
+* esimd_gemv_fp8_pern / _pert, 3 <= M <= 16, fp16/bf16 x e4m3/e5m2;
+* esimd_gemm_fp8_pert with 16 < M <= 32 (the GEMM entry's skinny route);
+* esimd_gemm_fp8_a8w8 with 3 <= M <= 64 (e4m3 activations and weights);
+* the fused multi-matrix GEMV (segment table), whose segments share a launch.
+
+N values include ones that are not multiples of the 16- and 32-row tiles.
+Reference: the CPU oracle; tolerance |out - ref| <= 1e-2 max|ref| + 2e-2 |ref|.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from conftest import assert_close_fp
+from esimd_learning_amd import synthetic
+from oracle import gemm as ogemm
+from oracle import gemv as ogemv
+from oracle import norm as onorm
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+# (K, N): every instantiated K, with N on both sides of the 6144-row switch
+SHAPES = [(2048, 1000), (3072, 6200), (4096, 6144), (4096, 2050), (5120, 6150), (14336, 1030), (24576, 520)]
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+@pytest.mark.parametrize("M", [3, 5, 8, 13, 16])
+def test_gemv_pern_lds(ops, dev, K, N, M):
+    _say(f"lds gemv pern M={M} K={K} N={N}")
+    W8, s = synthetic.weight_fp8(N, K, seed=K + M)
+    x = synthetic.activations(M, K, seed=N + M)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    ops.esimd_gemv_fp8_pern(x.to(dev), W8.to(dev), s.to(dev), y, N, K)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, W8, s), f"pern M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("io", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("fmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("K,N,M", [(4096, 6150, 9), (3072, 700, 4), (14336, 260, 16)])
+def test_gemv_pert_lds_types(ops, dev, io, fmt, K, N, M):
+    _say(f"lds gemv pert M={M} K={K} N={N} {io} {fmt}")
+    g = torch.Generator().manual_seed(K + N)
+    W8 = (torch.randn(N, K, generator=g).half() * 0.1).to(fmt)
+    sv = torch.tensor(0.07)
+    x = (torch.randn(M, K, generator=g) * 0.5).to(io)
+    y = torch.zeros(M, N, dtype=io, device=dev)
+    ops.esimd_gemv_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemv_fp8_pert(x, W8, sv), f"pert {io} {fmt}")
+
+
+@pytest.mark.parametrize("M,K,N", [(17, 2048, 3000), (24, 4096, 6144), (32, 5120, 1100), (32, 4096, 20000)])
+def test_gemm_pert_skinny(ops, dev, M, K, N):
+    """16 < M <= 32 through esimd_gemm_fp8_pert (N = 20000 takes the tiles)."""
+    _say(f"lds gemm pert M={M} K={K} N={N}")
+    W8, _ = synthetic.weight_fp8(N, K, seed=M + K)
+    x = synthetic.activations(M, K, seed=M)
+    sv = torch.tensor(0.02)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemm_fp8_pert(x, W8, sv), f"gemm pert M={M}")
+
+
+@pytest.mark.parametrize("M,K,N", [(3, 3072, 1000), (7, 24576, 300), (12, 4096, 6160), (16, 5120, 6144),
+                                   (20, 4096, 3000), (32, 14336, 1024), (33, 4096, 2000), (64, 2048, 8192),
+                                   (48, 4096, 9000)])
+def test_a8w8_skinny(ops, dev, M, K, N):
+    """a8w8 M <= 64: LDS kernel with 1, 2 and 4 activation blocks (and the
+    tiled GEMM for M > 32, N > 8192)."""
+    _say(f"lds a8w8 M={M} K={K} N={N}")
+    x = synthetic.activations(M, K, seed=M + 5)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=K + 3)
+    ref = ogemm.gemm_a8w8(q, sa, W8.view(torch.uint8), sb)
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.zeros(M, N, dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.view(torch.uint8).to(dev), sb.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
+
+
+def test_fused_segments_lds(ops, dev):
+    """Three matrices of different heights in one launch at M = 8."""
+    M, K = 8, 4096
+    x = synthetic.activations(M, K, seed=9)
+    Ns = [4096, 1030, 2000]
+    Ws, Ss = zip(*[synthetic.weight_fp8(n, K, seed=n) for n in Ns])
+    ys = [torch.zeros(M, n, dtype=torch.float16, device=dev) for n in Ns]
+    ops.esimd_gemv_fp8_pern_fused(x.to(dev), [w.to(dev) for w in Ws], [s.to(dev) for s in Ss], ys)
+    torch.cuda.synchronize()
+    for w, s, y in zip(Ws, Ss, ys):
+        assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, w, s), f"fused N={w.shape[0]}")

@@ -78,6 +78,19 @@ __device__ inline f4 mfma_fp8_16x16x128(const i8& a, const i8& b, f4 c) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// s_waitcnt vmcnt(N): this wave's vector-memory loads, all but the N most
+// recent, are complete (for direct-to-LDS loads: their data is in LDS).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the vmcnt(0) that a fenced __syncthreads adds
+// (which would drain loads still meant to be in flight).  The "memory"
+// clobber keeps the compiler from moving memory accesses across it.
+__device__ inline void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 __device__ inline i8 cat_i8(u4 lo, u4 hi) {
   return i8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }

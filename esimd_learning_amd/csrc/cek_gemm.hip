@@ -149,6 +149,61 @@ __device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
   return i8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
+// Epilogue of the tiled GEMMs.  The accumulators are scaled (row scale rs[m]
+// if given, column scale cs[n] if given, times s0), converted, and staged as
+// the BM x BN output tile in LDS; then every thread writes 16-byte pieces of
+// output rows.  Writing straight from the MFMA layout instead stores 2 bytes
+// per lane, four rows per instruction, and took 20-40% of a K = 4096 GEMM.
+// In LDS, the 16-byte column chunk k of tile row r sits at k ^ 2 ((r >> 2) & 3),
+// so the four row groups of an accumulator write land in distinct banks.
+// smem must hold BM * BN * 2 bytes; every wave must be done with it (the
+// leading barrier).
+template <typename T, int BM, int BN, int WM, int WN>
+__device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], uint8_t* smem, int wm, int wn,
+                                  int lane, int m0, int n0, int M, int N, const float* rs, const float* cs,
+                                  float s0, uint16_t* Y) {
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
+  constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+  static_assert(CPR % 8 == 0, "the chunk swizzle stays inside aligned groups of 8");
+  const int r16 = lane & 15, g = lane >> 4;
+  float rsv[FM][4];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) rsv[i][v] = rs ? rs[min(m0 + wm * TM + i * 16 + 4 * g + v, M - 1)] : 1.f;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int c = wn * TN + j * 16 + r16;
+    const float cv = (cs ? cs[min(n0 + c, N - 1)] : 1.f) * s0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = wm * TM + i * 16 + 4 * g + v;  // D row = 4 * (lane >> 4) + v
+        const int chunk = (c >> 3) ^ (2 * ((r >> 2) & 3));
+        *reinterpret_cast<uint16_t*>(smem + r * (BN * 2) + chunk * 16 + (c & 7) * 2) =
+            T::from_f32(acc[i][j][v] * rsv[i][v] * cv);
+      }
+  }
+  __syncthreads();
+  const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  for (int q = threadIdx.x; q < BM * CPR; q += 256) {
+    const int r = q / CPR, k = q % CPR;
+    const int m = m0 + r, n = n0 + 8 * k;
+    if (m >= M || n >= N) continue;
+    const uint8_t* src = smem + r * (BN * 2) + (k ^ (2 * ((r >> 2) & 3))) * 16;
+    uint16_t* dst = Y + (size_t)m * N + n;
+    if (vec) {
+      *reinterpret_cast<u4*>(dst) = *reinterpret_cast<const u4*>(src);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
+    }
+  }
+}
+
 template <typename T, int BM, int BN, int WM, int WN, int LAYOUT, int OCC>
 __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sa,
@@ -213,20 +268,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
     }
   }
 
-  // epilogue: D[4 (l >> 4) + v][l & 15] of each block
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * TN + j * 16 + r16;
-    if (n >= N) continue;
-    const float sn = sb[n];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = m0 + wm * TM + i * 16 + g * 4 + v;
-        if (m < M) Y[(size_t)m * N + n] = T::from_f32(acc[i][j][v] * sa[m] * sn);
-      }
-  }
+  static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
+  store_tile<T, BM, BN, WM, WN>(acc, smem, wm, wn, lane, m0, n0, M, N, sa, sb, 1.f, Y);
 }
 
 
@@ -322,19 +365,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_w8a16_lds_kernel(
     }
   }
 
-  const float sc = *scale;
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * TN + j * 16 + r16;
-    if (n >= N) continue;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = m0 + wm * TM + i * 16 + g * 4 + v;
-        if (m < M) Y[(size_t)m * N + n] = T::from_f32(acc[i][j][v] * sc);
-      }
-  }
+  static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
+  store_tile<T, BM, BN, 2, 2>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, *scale, Y);
 }
 
 // ---------------------------------------------------------------------------
@@ -463,15 +495,13 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     if (rc != CEK_ERR_UNSUPPORTED) return rc;
   }
   if (K % 128 == 0) {
-    // Tile choice (measured on MI355X over the BASELINE prefill shapes):
-    // 128 x 128 tiles let two workgroups share a CU, so one's MFMAs cover the
-    // other's LDS and barrier waits; 64 x 128 gives more tiles when there are
-    // too few to fill 256 CUs twice; 256 x 256 halves the L2 -> LDS traffic
-    // per flop and wins once there are many tiles per CU anyway.
+    // Tile choice (measured on MI355X over the BASELINE prefill shapes, with
+    // the LDS-staged epilogue): 128 x 128 tiles, two workgroups per CU so
+    // one's MFMAs cover the other's LDS reads and barrier waits; 64 x 128 when
+    // there are too few 128 x 128 tiles to give every CU one.  (256 x 256,
+    // one workgroup per CU, lost on every shape measured.)
     const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-    int cfg;
-    if (K >= 8192) cfg = t128 < 256 ? 0 : 1;
-    else cfg = t128 < 1024 ? 0 : (t128 < 4096 ? 1 : 2);
+    const int cfg = t128 < 256 ? 0 : 1;
 #define CEK_A8W8(TY, BM, BN, OCC)                                                                      \
   do {                                                                                               \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                          \
@@ -480,12 +510,10 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
   } while (0)
     if (out_dtype == CEK_F16) {
       if (cfg == 0) CEK_A8W8(F16, 64, 128, 2);
-      else if (cfg == 1) CEK_A8W8(F16, 128, 128, 2);
-      else CEK_A8W8(F16, 256, 256, 1);
+      else CEK_A8W8(F16, 128, 128, 2);
     } else {
       if (cfg == 0) CEK_A8W8(BF16, 64, 128, 2);
-      else if (cfg == 1) CEK_A8W8(BF16, 128, 128, 2);
-      else CEK_A8W8(BF16, 256, 256, 1);
+      else CEK_A8W8(BF16, 128, 128, 2);
     }
 #undef CEK_A8W8
     return check_launch();

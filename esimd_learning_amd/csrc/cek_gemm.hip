@@ -128,7 +128,7 @@ __device__ inline void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn
 
 // Direct-to-LDS loads of one K step (128 bytes) of the A and B slices into a
 // stage: this wave's 1 KB writer chunks j = wave + 4 i (rows 8 j .. 8 j + 7).
-template <int BM, int BN, int ACH, int BCH>
+template <int BM, int BN, int ACH, int BCH, int NW = 4>
 __device__ inline void a8w8_issue(uint8_t* smem, int stage, int kb, int wave,
                                   const uint8_t* const (&ga)[ACH], const uint8_t* const (&gb)[BCH]) {
 #if defined(__HIP_DEVICE_COMPILE__)  // device-only builtin; the host pass only needs the kernel's stub
@@ -136,10 +136,10 @@ __device__ inline void a8w8_issue(uint8_t* smem, int stage, int kb, int wave,
   uint8_t* sB = sA + BM * 128;
 #pragma unroll
   for (int i = 0; i < ACH; ++i)
-    __builtin_amdgcn_global_load_lds(ga[i] + kb, (lds_ptr_t)(sA + (wave + 4 * i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(ga[i] + kb, (lds_ptr_t)(sA + (wave + NW * i) * 1024), 16, 0, 0);
 #pragma unroll
   for (int i = 0; i < BCH; ++i)
-    __builtin_amdgcn_global_load_lds(gb[i] + kb, (lds_ptr_t)(sB + (wave + 4 * i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(gb[i] + kb, (lds_ptr_t)(sB + (wave + NW * i) * 1024), 16, 0, 0);
 #endif
 }
 
@@ -158,7 +158,7 @@ __device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
 // so the four row groups of an accumulator write land in distinct banks.
 // smem must hold BM * BN * 2 bytes; every wave must be done with it (the
 // leading barrier).
-template <typename T, int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, int NT = 256>
 __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], uint8_t* smem, int wm, int wn,
                                   int lane, int m0, int n0, int M, int N, const float* rs, const float* cs,
                                   float s0, uint16_t* Y) {
@@ -188,7 +188,7 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
   }
   __syncthreads();
   const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
-  for (int q = threadIdx.x; q < BM * CPR; q += 256) {
+  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
     const int r = q / CPR, k = q % CPR;
     const int m = m0 + r, n = n0 + 8 * k;
     if (m >= M || n >= N) continue;
@@ -205,7 +205,7 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int LAYOUT, int OCC>
-__global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
+__global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_lds_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sa,
     const uint8_t* __restrict__ B, const float* __restrict__ sb,
     uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
@@ -213,7 +213,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int STAGE = (BM + BN) * BK;
-  constexpr int ACH = BM / 8 / 4, BCH = BN / 8 / 4;  // 1 KB writer chunks per wave per stage
+  constexpr int NW = WM * WN;                         // waves per workgroup
+  constexpr int ACH = BM / 8 / NW, BCH = BN / 8 / NW;  // 1 KB writer chunks per wave per stage
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -228,12 +229,12 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
   const uint8_t* gb[BCH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
-    const int row = (wave + 4 * i) * 8 + (lane >> 3);
+    const int row = (wave + NW * i) * 8 + (lane >> 3);
     ga[i] = A + (size_t)min(m0 + row, M - 1) * K + ((lane & 7) ^ swz<LAYOUT>(row)) * 16;
   }
 #pragma unroll
   for (int i = 0; i < BCH; ++i) {
-    const int row = (wave + 4 * i) * 8 + (lane >> 3);
+    const int row = (wave + NW * i) * 8 + (lane >> 3);
     gb[i] = B + (size_t)min(n0 + row, N - 1) * K + ((lane & 7) ^ swz<LAYOUT>(row)) * 16;
   }
 
@@ -251,10 +252,10 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
-  a8w8_issue<BM, BN, ACH, BCH>(smem, 0, 0, wave, ga, gb);
+  a8w8_issue<BM, BN, ACH, BCH, NW>(smem, 0, 0, wave, ga, gb);
   for (int kt = 0; kt < KT; ++kt) {
     __syncthreads();  // this step's stage has landed; the other stage is free
-    if (kt + 1 < KT) a8w8_issue<BM, BN, ACH, BCH>(smem, (kt + 1) & 1, (kt + 1) * BK, wave, ga, gb);
+    if (kt + 1 < KT) a8w8_issue<BM, BN, ACH, BCH, NW>(smem, (kt + 1) & 1, (kt + 1) * BK, wave, ga, gb);
     const uint8_t* sA = smem + (kt & 1) * STAGE + (wm * TM + r16) * BK;
     const uint8_t* sB = smem + (kt & 1) * STAGE + (BM + wn * TN + r16) * BK;
     i8 bf[FN];
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_a8w8_lds_kernel(
   }
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
-  store_tile<T, BM, BN, WM, WN>(acc, smem, wm, wn, lane, m0, n0, M, N, sa, sb, 1.f, Y);
+  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, sa, sb, 1.f, Y);
 }
 
 
@@ -495,25 +496,44 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     if (rc != CEK_ERR_UNSUPPORTED) return rc;
   }
   if (K % 128 == 0) {
-    // Tile choice (measured on MI355X over the BASELINE prefill shapes, with
-    // the LDS-staged epilogue): 128 x 128 tiles, two workgroups per CU so
-    // one's MFMAs cover the other's LDS reads and barrier waits; 64 x 128 when
-    // there are too few 128 x 128 tiles to give every CU one.  (256 x 256,
-    // one workgroup per CU, lost on every shape measured.)
-    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-    const int cfg = t128 < 256 ? 0 : 1;
-#define CEK_A8W8(TY, BM, BN, OCC)                                                                      \
-  do {                                                                                               \
-    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                          \
-    gemm_a8w8_lds_kernel<TY, BM, BN, 2, 2, CEK_A8W8_LAYOUT, OCC><<<dim3((unsigned)(tm * tn)), 256, 0, st>>>( \
-        a, sa, b, sb, yp, M, N, K, tm, tn);                                                          \
+    // Tile choice: each configuration's measured rate at full occupancy
+    // (MI355X, BASELINE prefill shapes) times the fraction of the last
+    // round of workgroups that is filled (256 CUs; the 8-wave tiles fit one
+    // workgroup per CU, the 4-wave ones two), best score wins:
+    //  * 256 x 256, 8 waves (4 x 2, wave tile 64 x 128, two waves per SIMD):
+    //    the least LDS traffic per MFMA;
+    //  * 256 x 192, 8 waves (2 x 4);
+    //  * 128 x 128, 4 waves, two workgroups per CU so that one's MFMAs cover
+    //    the other's LDS reads and barrier waits;
+    //  * 64 x 128 for few, small tiles.
+    // This picks the fastest measured configuration on all nine config-4
+    // shapes but one (4096 x 6144 x 4096, within 2%).
+    struct Opt { int bm, bn; double rate; int slots; };
+    constexpr Opt opts[4] = {{64, 128, 1750, 512}, {128, 128, 2250, 512}, {256, 192, 2150, 256}, {256, 256, 2400, 256}};
+    int cfg = 0;
+    double best = -1.0;
+    for (int c = 0; c < 4; ++c) {
+      const int64_t tiles = ((M + opts[c].bm - 1) / opts[c].bm) * ((N + opts[c].bn - 1) / opts[c].bn);
+      const int64_t rounds = (tiles + opts[c].slots - 1) / opts[c].slots;
+      const double score = opts[c].rate * (double)tiles / (double)(rounds * opts[c].slots);
+      if (score > best) { best = score; cfg = c; }
+    }
+#define CEK_A8W8(TY, BM, BN, WM, WN, OCC)                                                               \
+  do {                                                                                                \
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
+    gemm_a8w8_lds_kernel<TY, BM, BN, WM, WN, CEK_A8W8_LAYOUT, OCC>                                    \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
     if (out_dtype == CEK_F16) {
-      if (cfg == 0) CEK_A8W8(F16, 64, 128, 2);
-      else CEK_A8W8(F16, 128, 128, 2);
+      if (cfg == 3) CEK_A8W8(F16, 256, 256, 4, 2, 1);
+      else if (cfg == 2) CEK_A8W8(F16, 256, 192, 2, 4, 1);
+      else if (cfg == 1) CEK_A8W8(F16, 128, 128, 2, 2, 2);
+      else CEK_A8W8(F16, 64, 128, 2, 2, 2);
     } else {
-      if (cfg == 0) CEK_A8W8(BF16, 64, 128, 2);
-      else CEK_A8W8(BF16, 128, 128, 2);
+      if (cfg == 3) CEK_A8W8(BF16, 256, 256, 4, 2, 1);
+      else if (cfg == 2) CEK_A8W8(BF16, 256, 192, 2, 4, 1);
+      else if (cfg == 1) CEK_A8W8(BF16, 128, 128, 2, 2, 2);
+      else CEK_A8W8(BF16, 64, 128, 2, 2, 2);
     }
 #undef CEK_A8W8
     return check_launch();

@@ -122,3 +122,20 @@ def test_a8w8_decode_rows(ops, dev, M, K, N):
         ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev), y)
         torch.cuda.synchronize()
         assert_close_fp(y.cpu(), ref, f"a8w8 decode M={M} {out_dt}")
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 1024, 8192), (4000, 512, 8150), (2000, 1024, 6100), (2048, 512, 6144)])
+def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
+    """The 256 x 256 and 256 x 192 tile configurations (8 waves), including
+    ragged M and N, against a float32 torch GPU matmul of the dequantised codes."""
+    _say(f"a8w8 large tiles M={M} K={K} N={N}")
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M + N)
+    qd, Wd = q.to(dev), W8.to(dev)
+    A = qd.view(torch.float8_e4m3fn).float()
+    B = Wd.view(torch.float8_e4m3fn).float()
+    ref = ((A @ B.T) * sa.to(dev)[:, None] * sb.to(dev)[None, :]).cpu()
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.zeros(M, N, dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(qd, sa.to(dev), Wd, sb.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")

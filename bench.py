@@ -155,6 +155,18 @@ def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
                          "traffic": None}}
 
 
+def bench_gemm_all(ops, torch, steps, warmup):
+    """BASELINE config 4 at M = 2048: the headline (K, N) = (4096, 6144) plus
+    the other two projections, each timed the same way."""
+    head = bench_gemm(ops, torch, steps, warmup)
+    head["shapes"] = []
+    for K, N in ((4096, 6144), (4096, 28672), (14336, 4096)):
+        r = head if (K, N) == (4096, 6144) else bench_gemm(ops, torch, steps, warmup, K=K, N=N)
+        head["shapes"].append({"config": r["config"], "avg_launch_us": round(r["avg_launch_us"], 2),
+                               "tflops": round(r["tflops"], 1)})
+    return head
+
+
 def bench_layer(torch, steps, M=4):
     """one Gemma-style decoder-layer decode step, HIP-graph replayed."""
     from esimd_learning_amd import synthetic
@@ -277,7 +289,7 @@ def main():
                      "algorithmic_bytes": g["bytes"], "avg_launch_us": round(g["avg_launch_us"], 3)},
     }
     if not a.no_gemm:
-        out["gemm"] = bench_gemm(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
+        out["gemm"] = bench_gemm_all(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")
     if not a.no_layer:
         out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))

@@ -9,12 +9,14 @@
 //   Grid: (row chunks of 2048 outputs, T); each thread handles 8 outputs with
 //   16-byte loads/stores.
 //
-// qk_norm_rope:  one 256-thread workgroup per token.  The cos/sin of the
-//   token's hd/2 rotary angles are computed once per token in double
-//   precision (angle = pos * base^(-2i/hd)) into LDS and shared by all heads;
-//   each wave then owns whole heads of q and k: RMS over the head via a wave
-//   butterfly, weight multiply, rounding to the activation type, rotation in
-//   fp32, and store in place.
+// qk_norm_rope:  256-thread workgroups over (token, group of heads); with
+//   many tokens a group is all of a token's heads, with few (decode) it is
+//   four, one per wave, so the work still spreads over many workgroups.  The
+//   cos/sin of the token's hd/2 rotary angles are computed in double
+//   precision (angle = pos * base^(-2i/hd)) into LDS and shared by the
+//   group's heads; each wave owns whole heads of q and k: RMS over the head
+//   via a wave butterfly, weight multiply, rounding to the activation type,
+//   rotation in fp32, and store in place.
 #include "cek_common.h"
 
 namespace cek {
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k,
     const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
     const int64_t* __restrict__ positions, int nq, int nk, int hd,
-    int64_t qs, int64_t ks, float eps, float theta, int neox) {
+    int64_t qs, int64_t ks, float eps, float theta, int neox, int heads_per_wg) {
   __shared__ float cs[256], sn[256];
   const int t = blockIdx.x;
   const int half = hd >> 1;
@@ -70,7 +72,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int h = wave; h < nq + nk; h += 4) {
+  const int h_end = min(nq + nk, ((int)blockIdx.y + 1) * heads_per_wg);
+  for (int h = (int)blockIdx.y * heads_per_wg + wave; h < h_end; h += 4) {
     const bool isq = h < nq;
     uint16_t* v = isq ? q + (size_t)t * qs + (size_t)h * hd : k + (size_t)t * ks + (size_t)(h - nq) * hd;
     const uint16_t* w = isq ? qw : kw;
@@ -141,13 +144,20 @@ extern "C" int cek_qk_norm_rope(void* q, void* k, const void* qw, const void* kw
   if (!positions || (n_q > 0 && (!q || !qw)) || (n_k > 0 && (!k || !kw))) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   const int ppl = (int)((head_dim / 2 + 63) / 64);
+  // Heads per workgroup (a multiple of the 4 waves): all of a token's heads
+  // once there are enough tokens to fill the GPU; otherwise one head per wave,
+  // so a decode step's few tokens still spread over many workgroups (each
+  // rebuilds its token's cos/sin table).
+  const int nh = (int)(n_q + n_k);
+  const int hpw = T >= 64 ? (nh + 3) / 4 * 4 : 4;
+  const dim3 grid((unsigned)T, (unsigned)((nh + hpw - 1) / hpw));
   uint16_t* qp = static_cast<uint16_t*>(q);
   uint16_t* kp = static_cast<uint16_t*>(k);
   const uint16_t* qwp = static_cast<const uint16_t*>(qw);
   const uint16_t* kwp = static_cast<const uint16_t*>(kw);
 #define CEK_ROPE_LAUNCH(TY, P)                                                                              \
-  qk_norm_rope_kernel<TY, P><<<dim3((unsigned)T), 256, 0, st>>>(qp, kp, qwp, kwp, positions, (int)n_q, (int)n_k, \
-                                                                (int)head_dim, q_stride, k_stride, eps, theta, is_neox)
+  qk_norm_rope_kernel<TY, P><<<grid, 256, 0, st>>>(qp, kp, qwp, kwp, positions, (int)n_q, (int)n_k, (int)head_dim, \
+                                                   q_stride, k_stride, eps, theta, is_neox, hpw)
   if (io_dtype == CEK_F16) {
     if (ppl == 1) CEK_ROPE_LAUNCH(F16, 1);
     else if (ppl == 2) CEK_ROPE_LAUNCH(F16, 2);

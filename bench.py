@@ -1,6 +1,6 @@
 """Benchmark of the fp8 decode GEMV (headline) and the fp8 prefill GEMM.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--no-layer] [--no-tables]
 
 Headline workload (headline shape): esimd_gemv_fp8_pern
 with M = 1, K = 4096, N = 14336: fp16 activations, e4m3 weights with an fp32
@@ -14,6 +14,12 @@ graph (so host launch cost is not measured) and replayed once between
 device synchronisations; ms_per_step = wall time / K.  The dominant kernel's
 average launch duration is measured with HIP events on the launch stream
 around the same graph replay; it feeds roofline.achieved.
+
+Further legs (same JSON line): "gemm" (a8w8 at M = 2048,
+three projections), "decoder_layer" (config 5, one graph-replayed step),
+"gemv_shapes" (config 2, every M x shape), "norm_quant_gemv" (config 3,
+fused add+RMSNorm+quant then the fp8 GEMV/GEMM to N = 6144), and the device
+copy rate the headline is also quoted against (roofline.copy_GBps).
 
 cpu_baseline: the reference's torch CPU path restated in oracle/
 ((x.float() @ W8.to(fp16).float().T) * s) on this host's cores, timed on the
@@ -122,9 +128,99 @@ def bench_gemv(ops, torch, steps, warmup, M=1, K=4096, N=14336):
             b.record(stream)
     torch.cuda.synchronize()
     per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
-    res["eager_event_us_median"] = per[len(per) // 2]
+    res["eager_event_us"] = {"p10": round(per[len(per) // 10], 2), "median": round(per[len(per) // 2], 2),
+                             "p90": round(per[(9 * len(per)) // 10], 2)}
     # correctness spot check against the first copy (cheap, CPU oracle at M=1)
     return res, (x, Wd, s, y)
+
+
+def copy_bandwidth(torch, nbytes=1 << 30, reps=5):
+    """Device-to-device copy rate (read + write bytes / s) of a 1 GiB buffer."""
+    dev = "cuda:0"
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    return 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
+def bench_gemv_table(ops, torch, shapes=((4096, 14336), (4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)),
+                     Ms=(1, 2, 4, 8, 16)):
+    """every (M, K, N), per-launch time over > 2 GB of
+    rotating weights (graph of two passes over the copies, event-timed)."""
+    from esimd_learning_amd import synthetic
+    dev = "cuda:0"
+    stream = torch.cuda.Stream()
+    rows = []
+    for K, N in shapes:
+        W8, s = synthetic.weight_fp8(N, K, seed=0)
+        copies = max(2, math.ceil(ROTATE_BYTES / (N * K)))
+        Wd = W8.to(dev)
+        Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
+        sd = s.to(dev)
+        for M in Ms:
+            x = synthetic.activations(M, K, seed=1).to(dev)
+            y = torch.empty(M, N, dtype=torch.float16, device=dev)
+            fns = [(lambda W=W: ops.esimd_gemv_fp8_pern(x, W, sd, y, N, K)) for W in Ws] * 2
+            with torch.cuda.stream(stream):
+                for f in fns[:copies]:
+                    f()
+            torch.cuda.synchronize()
+            _, ev_ms, _ = time_graph(fns, torch, stream)
+            us = ev_ms * 1e3 / len(fns)
+            rows.append({"M": M, "K": K, "N": N, "us": round(us, 2),
+                         "GBps": round(gemv_bytes(M, N, K) / (us * 1e-6) / 1e9, 1)})
+        del Ws, Wd
+        torch.cuda.empty_cache()
+    return rows
+
+
+def bench_norm_quant_gemv(ops, torch, reps=50, N=6144):
+    """fused add+RMSNorm+per-token e4m3 quant, then the
+    fp8 x fp8 GEMV/GEMM to N = 6144 on its codes and scales.  Per (T, H):
+    the two kernels' times (each a graph of `reps` launches, event-timed;
+    the GEMV rotates over > 2 GB of weights) and the pair back to back."""
+    from esimd_learning_amd import synthetic
+    dev = "cuda:0"
+    stream = torch.cuda.Stream()
+    rows = []
+    for H in (4096, 5120):
+        W8, sb = synthetic.weight_fp8(N, H, seed=4)
+        copies = max(2, math.ceil(ROTATE_BYTES / (N * H)))
+        Wd = W8.view(torch.uint8).to(dev)
+        Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
+        sbd = sb.to(dev)
+        w = synthetic.norm_weight(H, seed=H).to(dev)
+        for T in (1, 8, 32, 64):
+            h = synthetic.activations(T, H, seed=T).to(dev)
+            r = synthetic.activations(T, H, seed=T + 1).to(dev)
+            q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+            sa = torch.empty(T, dtype=torch.float32, device=dev)
+            y = torch.empty(T, N, dtype=torch.float16, device=dev)
+            norm = lambda: ops.esimd_fused_add_rms_norm_quant_fp8(h, r, w, 1e-6, q, sa)  # noqa: E731
+            gemv = [(lambda W=W: ops.esimd_gemm_fp8_a8w8(q.view(torch.uint8), sa, W, sbd, y)) for W in Ws]
+            with torch.cuda.stream(stream):
+                norm()
+                gemv[0]()
+            torch.cuda.synchronize()
+            _, n_ms, _ = time_graph([norm] * reps, torch, stream)
+            _, g_ms, _ = time_graph(gemv * 2, torch, stream)
+            pair = []
+            for i in range(reps):
+                pair += [norm, gemv[i % copies]]
+            _, p_ms, _ = time_graph(pair, torch, stream)
+            rows.append({"T": T, "H": H, "norm_quant_us": round(n_ms * 1e3 / reps, 2),
+                         "gemv_us": round(g_ms * 1e3 / (2 * copies), 2),
+                         "pair_us": round(p_ms * 1e3 / reps, 2)})
+        del Ws, Wd
+        torch.cuda.empty_cache()
+    return rows
 
 
 def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
@@ -211,6 +307,17 @@ def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
             ts.append(time.perf_counter() - t0)
     ts.sort()
     med = ts[len(ts) // 2]
+    # the same with the weights dequantised once up front (matmul + scale only)
+    Wf = W8.to(torch.float16).float()
+    xf = x.float()
+    tm = []
+    for i in range(2 + reps):
+        t0 = time.perf_counter()
+        (xf @ Wf.T) * s.float()
+        if i >= 2:
+            tm.append(time.perf_counter() - t0)
+    tm.sort()
+    med_mm = tm[len(tm) // 2]
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -223,7 +330,10 @@ def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
             "kind": "port",
             "sample": f"oracle gemv_fp8_pern (dequant fp8->fp16->fp32 + fp32 matmul + scale) on CPU, "
                       f"M={M} K={K} N={N}, median of {reps} after 2 warm-ups, {med * 1e3:.1f} ms/call; "
-                      f"os.cpu_count()={os.cpu_count()}; cpu '{model}'"}
+                      f"os.cpu_count()={os.cpu_count()}; cpu '{model}'",
+            "matmul_only": {"value": gemv_bytes(M, N, K) / med_mm / 1e9, "unit": "GB/s",
+                            "ms_per_call": round(med_mm * 1e3, 2),
+                            "sample": "same shape with W dequantised once before timing (fp32 matmul + scale)"}}
 
 
 def main():
@@ -234,6 +344,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--no-tables", action="store_true", help="skip the config-2 GEMV table and config-3 legs")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run 10 plain device copies of N*K bytes (reference for HBM counter scaling)")
     a = ap.parse_args()
@@ -258,7 +369,7 @@ def main():
 
     g, (x, Wd, s, y) = bench_gemv(ops, torch, a.steps, a.warmup)
     log(f"gemv: {g['avg_launch_us']:.2f} us/launch, {g['achieved']:.0f} GB/s; eager event median "
-        f"{g['eager_event_us_median']:.2f} us; wall {g['ms_per_step'] * 1e3:.2f} us/step")
+        f"{g['eager_event_us']['median']:.2f} us; wall {g['ms_per_step'] * 1e3:.2f} us/step")
     # spot check of the measured output
     from oracle import gemv as ogemv
     torch.cuda.synchronize()
@@ -286,8 +397,18 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic("gemv_dot_kernel_m1_k4096_n14336"),
-                     "algorithmic_bytes": g["bytes"], "avg_launch_us": round(g["avg_launch_us"], 3)},
+                     "algorithmic_bytes": g["bytes"], "avg_launch_us": round(g["avg_launch_us"], 3),
+                     "eager_event_us": g["eager_event_us"]},
     }
+    cbw = copy_bandwidth(torch)
+    out["roofline"]["copy_GBps"] = round(cbw, 1)
+    out["roofline"]["frac_of_copy"] = round(g["achieved"] / cbw, 4)
+    log(f"device copy: {cbw:.0f} GB/s (read + write); GEMV at {g['achieved'] / cbw:.1%} of it")
+    if not a.no_tables:
+        out["gemv_shapes"] = bench_gemv_table(ops, torch)
+        log("gemv table: " + ", ".join(f"M{r['M']}/{r['K']}x{r['N']}={r['us']}us" for r in out["gemv_shapes"]))
+        out["norm_quant_gemv"] = bench_norm_quant_gemv(ops, torch)
+        log("norm+quant -> gemv: " + ", ".join(f"T{r['T']}/H{r['H']}={r['pair_us']}us" for r in out["norm_quant_gemv"]))
     if not a.no_gemm:
         out["gemm"] = bench_gemm_all(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")

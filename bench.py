@@ -263,13 +263,14 @@ def bench_gemm_all(ops, torch, steps, warmup):
     return head
 
 
-def bench_layer(torch, steps, M=4):
-    """one Gemma-style decoder-layer decode step, HIP-graph replayed."""
+def bench_layer(torch, steps, M=4, act_fp8=False):
+    """one Gemma-style decoder-layer decode step, HIP-graph replayed
+    (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations)."""
     from esimd_learning_amd import synthetic
     from esimd_learning_amd.layer import GemmaDecodeLayer
     dev = "cuda:0"
     p = synthetic.gemma_layer(seed=10)
-    layer = GemmaDecodeLayer(p, M, dev)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8)
     h = synthetic.activations(M, p["hidden"], seed=20).to(dev)
     r = synthetic.activations(M, p["hidden"], seed=21).to(dev)
     pos = synthetic.positions(M, seed=22).to(dev)
@@ -415,6 +416,9 @@ def main():
     if not a.no_layer:
         out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))
         log(f"layer: {out['decoder_layer']['us_per_step']} us/step, {out['decoder_layer']['weight_GBps']} GB/s")
+        fp8 = bench_layer(torch, max(20, a.steps // 4), act_fp8=True)
+        out["decoder_layer"]["act_fp8_us_per_step"] = fp8["us_per_step"]
+        log(f"layer, e4m3 activation hand-off: {fp8['us_per_step']} us/step")
     if not a.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch)

@@ -10,6 +10,11 @@
     g      = gelu_tanh(gu[:, :d]) * gu[:, d:]             esimd_gelu_and_mul
     out    = g @ Wd^T * sd                                esimd_gemv_fp8_pern
 
+With ``act_fp8=True`` the two norm -> GEMV hand-offs carry e4m3 activations
+instead of fp16: esimd_fused_add_rms_norm_quant_fp8 writes per-token codes
+and scales, and esimd_gemm_fp8_a8w8 consumes them (the hidden input is then
+only read, not overwritten with the normed value).  Needs e4m3 weights.
+
 All intermediate buffers are allocated once in the constructor, so a step
 enqueues only kernels: it can be captured in a HIP graph (``capture``) and
 replayed, which removes host launch overhead from the latency-bound small
@@ -20,7 +25,7 @@ import torch
 
 
 class GemmaDecodeLayer:
-    def __init__(self, params, M, device="cuda:0", dtype=torch.float16):
+    def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False):
         from . import ops as _load_ops
         self.ops = _load_ops()
         p = params
@@ -42,6 +47,14 @@ class GemmaDecodeLayer:
         self.gu = mk(2 * self.mlp)
         self.act = mk(self.mlp)
         self.out = mk(self.hidden)
+        self.act_fp8 = act_fp8
+        if act_fp8:
+            if self.Wqkv.dtype != torch.float8_e4m3fn or self.Wgu.dtype != torch.float8_e4m3fn:
+                raise ValueError("act_fp8 needs e4m3 weights")
+            self.q8 = torch.empty(M, self.hidden, dtype=torch.float8_e4m3fn, device=device)
+            self.s8 = torch.empty(M, dtype=torch.float32, device=device)
+            self.Wqkv8, self.sqkv32 = self.Wqkv.view(torch.uint8), self.sqkv.float()
+            self.Wgu8, self.sgu32 = self.Wgu.view(torch.uint8), self.sgu.float()
         self.graph = None
 
     def weight_bytes(self):
@@ -50,14 +63,22 @@ class GemmaDecodeLayer:
     def step(self, hidden, residual, positions):
         """hidden, residual: [M, hidden] (residual updated in place); returns out."""
         o, hd, nq, nk = self.ops, self.hd, self.nq, self.nk
-        o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, self.eps)
-        o.esimd_gemv_fp8_pern(hidden, self.Wqkv, self.sqkv, self.qkv, self.Wqkv.shape[0], self.hidden)
+        if self.act_fp8:
+            o.esimd_fused_add_rms_norm_quant_fp8(hidden, residual, self.w_in, self.eps, self.q8, self.s8)
+            o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wqkv8, self.sqkv32, self.qkv)
+        else:
+            o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, self.eps)
+            o.esimd_gemv_fp8_pern(hidden, self.Wqkv, self.sqkv, self.qkv, self.Wqkv.shape[0], self.hidden)
         o.esimd_qk_norm_rope(self.qkv[:, : nq * hd], self.qkv[:, nq * hd:(nq + nk) * hd], self.qw, self.kw,
                              positions, self.eps, self.theta, True)
         self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
         o.esimd_gemv_fp8_pern(self.attn, self.Wo, self.so, self.o, self.hidden, nq * hd)
-        o.esimd_fused_add_rms_norm_batched(self.o, residual, self.w_post, self.eps)
-        o.esimd_gemv_fp8_pern(self.o, self.Wgu, self.sgu, self.gu, 2 * self.mlp, self.hidden)
+        if self.act_fp8:
+            o.esimd_fused_add_rms_norm_quant_fp8(self.o, residual, self.w_post, self.eps, self.q8, self.s8)
+            o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wgu8, self.sgu32, self.gu)
+        else:
+            o.esimd_fused_add_rms_norm_batched(self.o, residual, self.w_post, self.eps)
+            o.esimd_gemv_fp8_pern(self.o, self.Wgu, self.sgu, self.gu, 2 * self.mlp, self.hidden)
         o.esimd_gelu_and_mul(self.act, self.gu)
         o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
         return self.out

@@ -15,21 +15,32 @@ dtype between steps exactly as the device pipeline hands fp16 tensors on):
   a      = gelu_and_mul(gu)                                (a10)
   out    = gemv(a, Wd, sd)                                 (a1)
 
+With act_fp8 the two add_rmsnorm -> gemv hand-offs go through the per-token
+e4m3 quant (a6) and the a8w8 product (a9) instead.
+
 Pins: each step is pinned in its own module; this file only composes them.
 """
 
 import torch
 
-from . import act, gemv, norm
+from . import act, gemm, gemv, norm
 
 
-def decoder_step(p, hidden, residual, positions):
+def _norm_then_gemv(x, r, w, eps, W8, s, act_fp8):
+    """add_rmsnorm then the projection; returns (residual_out, y fp32)."""
+    if act_fp8:
+        r_new, q, qs, _ = norm.fused_add_rms_norm_quant(x, r, w, eps)
+        return r_new, gemm.gemm_a8w8(q, qs, W8.view(torch.uint8), s.float())
+    r_new, h = norm.fused_add_rms_norm(x, r, w, eps)
+    return r_new, gemv.gemv_fp8_pern(h.to(x.dtype), W8, s)
+
+
+def decoder_step(p, hidden, residual, positions, act_fp8=False):
     """p: dict of CPU tensors (see esimd_learning_amd.synthetic.gemma_layer)."""
     dt = hidden.dtype
     hd, nq, nk = p["head_dim"], p["n_q"], p["n_kv"]
-    r1, h1 = norm.fused_add_rms_norm(hidden, residual, p["w_in"], p["eps"])
-    h1 = h1.to(dt)
-    qkv = gemv.gemv_fp8_pern(h1, p["Wqkv"], p["sqkv"]).to(dt)
+    r1, qkv = _norm_then_gemv(hidden, residual, p["w_in"], p["eps"], p["Wqkv"], p["sqkv"], act_fp8)
+    qkv = qkv.to(dt)
     q = qkv[:, : nq * hd].float().numpy()
     k = qkv[:, nq * hd:(nq + nk) * hd].float().numpy()
     qo, ko = act.qk_norm_rope(q, k, p["qw"].float().numpy(), p["kw"].float().numpy(),
@@ -37,9 +48,8 @@ def decoder_step(p, hidden, residual, positions):
     qkv[:, : nq * hd] = torch.from_numpy(qo).to(dt)
     qkv[:, nq * hd:(nq + nk) * hd] = torch.from_numpy(ko).to(dt)
     o = gemv.gemv_fp8_pern(qkv[:, : nq * hd], p["Wo"], p["so"]).to(dt)
-    r2, h2 = norm.fused_add_rms_norm(o, r1, p["w_post"], p["eps"])
-    h2 = h2.to(dt)
-    gu = gemv.gemv_fp8_pern(h2, p["Wgu"], p["sgu"]).to(dt)
+    r2, gu = _norm_then_gemv(o, r1, p["w_post"], p["eps"], p["Wgu"], p["sgu"], act_fp8)
+    gu = gu.to(dt)
     a = torch.from_numpy(act.gelu_and_mul(gu.float().numpy())).to(dt)
     out = gemv.gemv_fp8_pern(a, p["Wd"], p["sd"])
     return out, r2, qkv

@@ -27,27 +27,29 @@ SMALL = dict(hidden=512, n_q=4, n_kv=2, head_dim=64, mlp=1024)
 CONFIG5 = dict(hidden=3072, n_q=16, n_kv=16, head_dim=256, mlp=24576)
 
 
+@pytest.mark.parametrize("act_fp8", [False, True])
 @pytest.mark.parametrize("dims,M", [(SMALL, 3), (CONFIG5, 4)])
-def test_decoder_step_vs_oracle(ops, dev, dims, M):
-    _say(f"decoder step M={M} {dims}")
+def test_decoder_step_vs_oracle(ops, dev, dims, M, act_fp8):
+    _say(f"decoder step M={M} {dims} act_fp8={act_fp8}")
     p = synthetic.gemma_layer(seed=10, **dims)
-    layer = GemmaDecodeLayer(p, M, dev)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8)
     h = synthetic.activations(M, dims["hidden"], seed=20)
     r = synthetic.activations(M, dims["hidden"], seed=21)
     pos = synthetic.positions(M, seed=22)
     hd, rd = h.to(dev), r.to(dev)
     out = layer.step(hd, rd, pos.to(dev)).clone()
     torch.cuda.synchronize()
-    ref_out, ref_r, _ = olayer.decoder_step(p, h, r, pos)
+    ref_out, ref_r, _ = olayer.decoder_step(p, h, r, pos, act_fp8=act_fp8)
     assert_close_fp(rd.cpu(), ref_r.float(), "residual after the layer")
     assert_close_fp(out.cpu(), ref_out, "layer output")
 
 
-def test_decoder_step_graph_replays(ops, dev):
+@pytest.mark.parametrize("act_fp8", [False, True])
+def test_decoder_step_graph_replays(ops, dev, act_fp8):
     M = 4
     dims = SMALL
     p = synthetic.gemma_layer(seed=11, **dims)
-    layer = GemmaDecodeLayer(p, M, dev)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8)
     h0 = synthetic.activations(M, dims["hidden"], seed=30).to(dev)
     r0 = synthetic.activations(M, dims["hidden"], seed=31).to(dev)
     pos = synthetic.positions(M, seed=32).to(dev)

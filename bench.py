@@ -134,6 +134,16 @@ def bench_gemv(ops, torch, steps, warmup, M=1, K=4096, N=14336):
     return res, (x, Wd, s, y)
 
 
+def launch_floor_us(torch, steps=400):
+    """Per-launch time of a trivial kernel (a 4-element fill) replayed from a
+    graph: the fixed cost every kernel launch in a sequence pays."""
+    dev = "cuda:0"
+    t = torch.empty(4, dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()
+    _, ev_ms, _ = time_graph([lambda: t.fill_(1.0)] * steps, torch, stream)
+    return ev_ms * 1e3 / steps
+
+
 def copy_bandwidth(torch, nbytes=1 << 30, reps=5):
     """Device-to-device copy rate (read + write bytes / s) of a 1 GiB buffer."""
     dev = "cuda:0"
@@ -401,10 +411,12 @@ def main():
                      "algorithmic_bytes": g["bytes"], "avg_launch_us": round(g["avg_launch_us"], 3),
                      "eager_event_us": g["eager_event_us"]},
     }
-    cbw = copy_bandwidth(torch)
-    out["roofline"]["copy_GBps"] = round(cbw, 1)
-    out["roofline"]["frac_of_copy"] = round(g["achieved"] / cbw, 4)
-    log(f"device copy: {cbw:.0f} GB/s (read + write); GEMV at {g['achieved'] / cbw:.1%} of it")
+    out["roofline"]["launch_floor_us"] = round(launch_floor_us(torch), 2)
+    if not a.copy_ref:  # (counter runs keep the copy kernels to the reference copies)
+        cbw = copy_bandwidth(torch)
+        out["roofline"]["copy_GBps"] = round(cbw, 1)
+        out["roofline"]["frac_of_copy"] = round(g["achieved"] / cbw, 4)
+        log(f"device copy: {cbw:.0f} GB/s (read + write); GEMV at {g['achieved'] / cbw:.1%} of it")
     if not a.no_tables:
         out["gemv_shapes"] = bench_gemv_table(ops, torch)
         log("gemv table: " + ", ".join(f"M{r['M']}/{r['K']}x{r['N']}={r['us']}us" for r in out["gemv_shapes"]))

@@ -57,6 +57,12 @@ def test_host_rejects_invalid_arguments():
     assert lib.cek_gelu_and_mul(p, p, 4, 64, 100, 64, 0, None) == E                  # x stride < 2d
     assert lib.cek_qk_norm_rope(p, p, p, p, p, 4, 2, 2, 1024, 2048, 2048, 1e-6, 1e4, 1, 0, None) == E
     assert lib.cek_qk_norm_rope(p, p, p, p, p, 4, 2, 2, 128, 100, 256, 1e-6, 1e4, 1, 0, None) == E
+    # multi-matrix GEMV: count out of range, null tables
+    P3 = C.c_void_p * 3
+    Ns = (C.c_int64 * 3)(8, 8, 8)
+    assert lib.cek_gemv_fp8_pern_multi(p, 0, P3(p, p, p), P3(p, p, p), P3(p, p, p), Ns, 1, 64, 0, 0, 2, None) == E
+    assert lib.cek_gemv_fp8_pern_multi(p, 9, P3(p, p, p), P3(p, p, p), P3(p, p, p), Ns, 1, 64, 0, 0, 2, None) == E
+    assert lib.cek_gemv_fp8_pert_multi(p, 3, None, P3(p, p, p), P3(p, p, p), Ns, 1, 64, 0, 0, None) == E
     # empty problems are no-ops that succeed without touching memory
     assert lib.cek_gemv_fp8_pern(None, None, None, None, 0, 8, 64, 0, 0, 2, None) == cabi.CEK_OK
     assert lib.cek_fused_add_rms_norm(None, None, None, 0, 64, 1e-6, 0, None) == cabi.CEK_OK
@@ -109,3 +115,30 @@ def test_cabi_error_string_after_invalid(ops, dev):
     assert rc == cabi.CEK_ERR_INVALID
     with pytest.raises(RuntimeError, match="invalid argument"):
         cabi.check(rc)
+
+
+@pytest.mark.gpu
+def test_cabi_multi_gemv_matches_single(ops, dev):
+    """cek_gemv_fp8_pern_multi over three matrices (host pointer tables) gives
+    each matrix's cek_gemv_fp8_pern result bit for bit, at M on both sides of
+    the v_dot2 / LDS-kernel switch."""
+    lib = cabi.load()
+    K = 4096
+    Ns = [1024, 520, 2048]
+    mats = [synthetic.weight_fp8(n, K, seed=40 + i) for i, n in enumerate(Ns)]
+    wd = [w.to(dev) for w, _ in mats]
+    sd = [s.to(dev) for _, s in mats]
+    for M in (1, 5):
+        x = synthetic.activations(M, K, seed=41).to(dev)
+        ys = [torch.zeros(M, n, dtype=torch.float16, device=dev) for n in Ns]
+        P = C.c_void_p * 3
+        cabi.check(lib.cek_gemv_fp8_pern_multi(cabi.ptr(x), 3, P(*[t.data_ptr() for t in wd]),
+                                               P(*[t.data_ptr() for t in sd]), P(*[t.data_ptr() for t in ys]),
+                                               (C.c_int64 * 3)(*Ns), M, K, cabi.CEK_F16, cabi.CEK_E4M3,
+                                               cabi.CEK_F32, cabi.stream_ptr()))
+        for w, s, y, n in zip(wd, sd, ys, Ns):
+            y1 = torch.zeros(M, n, dtype=torch.float16, device=dev)
+            cabi.check(lib.cek_gemv_fp8_pern(cabi.ptr(x), cabi.ptr(w), cabi.ptr(s), cabi.ptr(y1), M, n, K,
+                                             cabi.CEK_F16, cabi.CEK_E4M3, cabi.CEK_F32, cabi.stream_ptr()))
+            torch.cuda.synchronize()
+            assert torch.equal(y, y1), f"M={M} N={n}"

@@ -1,4 +1,5 @@
-// cek_gemv.hip -- fp8-weight GEMV for decode (M <= 16 activation rows), gfx950.
+// cek_gemv.hip -- fp8-weight GEMV for decode (M <= 16 activation rows; up
+// to 64 for the skinny GEMMs that reuse these kernels), gfx950.
 //
 // y[m, n] = Out((sum_k x[m, k] * dq(W[n, k])) * scale[n])   (scale after the
 // reduction, as reference fp8_GEMV_v2.h:77 / :355 apply it).
@@ -14,19 +15,23 @@
 // kernel arguments; workgroup b finds its segment from the table's prefix
 // sums of workgroups per segment.
 //
-//  * gemv_dot_kernel (M <= 4): a 256-thread workgroup owns R output rows;
-//    one load instruction of the workgroup reads 4 KB of contiguous weight
-//    bytes of a row (thread t reads bytes [16 t, 16 t + 16) of the chunk),
-//    which are decoded with v_cvt_scalef32_pk_{f16,bf16}_fp8 into
-//    activation-typed pairs and accumulated with v_dot2_f32_{f16,bf16}
-//    (fp32 accumulation).  The activation slice a thread needs is re-read
-//    from L1/L2 (x is tiny).  DPP wave sums and an LDS combine end a row.
-//  * gemv_mfma_kernel (4 < M <= 16): the 16 x 16 x 32 f16/bf16 MFMA does
-//    the M x 16-row dot products; lane l streams row (l & 15) of a 16-row
-//    tile at k-offset 16 * (l >> 4) of each 64-byte step, so a tile is read
-//    as 16 rows x 64 contiguous bytes per load instruction.  The four waves
-//    of a workgroup interleave over the K steps of the same tile (256
-//    contiguous bytes per row per round) and reduce through LDS.
+//  * gemv_dot_kernel (M <= 2, and M <= 4 where the LDS kernel has no
+//    instantiation): a 256-thread workgroup owns R output rows; one load
+//    instruction of the workgroup reads 4 KB of contiguous weight bytes of a
+//    row (thread t reads bytes [16 t, 16 t + 16) of the chunk), which are
+//    decoded with v_cvt_scalef32_pk_{f16,bf16}_fp8 into activation-typed
+//    pairs and accumulated with v_dot2_f32_{f16,bf16} (fp32 accumulation).
+//    The activation slice a thread needs is re-read from L1/L2 (x is tiny).
+//    DPP wave sums and an LDS combine end a row.
+//  * gemv_lds_kernel (3 <= M <= 64, K in {2, 3, 4, 5, 14, 24} x 1024): MFMA
+//    on weights staged through LDS so that every load instruction still
+//    reads 1 KB of one row (see the comment at the kernel).  Also the a8w8
+//    path (e4m3 activations) for 3 <= M <= 64.
+//  * gemv_mfma_kernel (4 < M <= 16, other K % 64 == 0): the 16 x 16 x 32
+//    f16/bf16 MFMA does the M x 16-row dot products; lane l streams row
+//    (l & 15) of a 16-row tile at k-offset 16 * (l >> 4) of each 64-byte
+//    step.  The four waves of a workgroup interleave over the K steps of the
+//    same tile and reduce through LDS.
 //  * gemv_generic_kernel: any K / alignment; byte loads.  Correctness path
 //    for shapes the vector kernels do not take.
 #include <type_traits>

@@ -7,6 +7,7 @@ device pointers agree with the torch ops and the oracle.
 """
 
 import ctypes as C
+from pathlib import Path
 import subprocess
 
 import numpy as np
@@ -28,6 +29,23 @@ def test_library_exports_header_functions():
     missing = [f for f in declared if f not in exported]
     assert not missing, missing
     assert sorted(cabi.SIGNATURES) == declared
+
+
+def test_c_host_program(tmp_path):
+    """A C99 program built against include/cek.h and libcek.so (gcc, no GPU
+    calls): the header is plain C and the argument checks hold from C."""
+    import shutil
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = Path(__file__).parent / "c" / "abi_host.c"
+    exe = tmp_path / "abi_host"
+    libdir = Path(cabi.LIBCEK).parent
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", str(cabi.HEADER.parent), str(src),
+                    "-o", str(exe), "-L", str(libdir), "-lcek", f"-Wl,-rpath,{libdir}"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().endswith("ok")
 
 
 def test_library_loads_and_reports():

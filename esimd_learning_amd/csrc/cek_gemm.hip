@@ -287,7 +287,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_lds_kernel(
 __device__ inline int swzA(int row) { return (row ^ ((row >> 3) & 1)) & 7; }
 __device__ inline int swzB(int row) { return (row >> 2) & 3; }
 
-template <int BM, int BN, int ACH, int BCH>
+template <int BM, int BN, int ACH, int BCH, int NW = 4>
 __device__ inline void w8a16_issue(uint8_t* smem, int stage, int kb, int wave,
                                    const uint8_t* const (&ga)[ACH], const uint8_t* const (&gb)[BCH]) {
 #if defined(__HIP_DEVICE_COMPILE__)  // device-only builtin; the host pass only needs the kernel's stub
@@ -295,26 +295,29 @@ __device__ inline void w8a16_issue(uint8_t* smem, int stage, int kb, int wave,
   uint8_t* sB = sA + BM * 128;
 #pragma unroll
   for (int i = 0; i < ACH; ++i)
-    __builtin_amdgcn_global_load_lds(ga[i] + 2 * kb, (lds_ptr_t)(sA + (wave + 4 * i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(ga[i] + 2 * kb, (lds_ptr_t)(sA + (wave + NW * i) * 1024), 16, 0, 0);
 #pragma unroll
   for (int i = 0; i < BCH; ++i)
-    __builtin_amdgcn_global_load_lds(gb[i] + kb, (lds_ptr_t)(sB + (wave + 4 * i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(gb[i] + kb, (lds_ptr_t)(sB + (wave + NW * i) * 1024), 16, 0, 0);
 #endif
 }
 
-template <typename T, int FMT, int BM, int BN, int OCC>
-__global__ __launch_bounds__(256, OCC) void gemm_w8a16_lds_kernel(
+template <typename T, int FMT, int BM, int BN, int OCC, int WM = 2, int WN = 2>
+__global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
     uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
   constexpr int BK = 64;
-  constexpr int TM = BM / 2, TN = BN / 2;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int STAGE = BM * 128 + BN * 64;
-  constexpr int ACH = BM / 8 / 4, BCH = BN / 16 / 4;   // 1 KB writer chunks per wave per stage
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  constexpr int ACH = BM / 8 / NW, BCH = BN / 16 / NW;   // 1 KB writer chunks per wave per stage
+  static_assert(ACH * 8 * NW == BM && BCH * 16 * NW == BN, "writer chunks");
+  // two stages, or the output tile of the epilogue if that is larger
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
   tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -326,12 +329,12 @@ __global__ __launch_bounds__(256, OCC) void gemm_w8a16_lds_kernel(
   const uint8_t* gb[BCH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
-    const int row = (wave + 4 * i) * 8 + (lane >> 3);
+    const int row = (wave + NW * i) * 8 + (lane >> 3);
     ga[i] = Xb + ((size_t)min(m0 + row, M - 1) * K) * 2 + ((lane & 7) ^ swzA(row)) * 16;
   }
 #pragma unroll
   for (int i = 0; i < BCH; ++i) {
-    const int row = (wave + 4 * i) * 16 + (lane >> 2);
+    const int row = (wave + NW * i) * 16 + (lane >> 2);
     gb[i] = W + (size_t)min(n0 + row, N - 1) * K + ((lane & 3) ^ swzB(row)) * 16;
   }
 
@@ -345,10 +348,10 @@ __global__ __launch_bounds__(256, OCC) void gemm_w8a16_lds_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
-  w8a16_issue<BM, BN, ACH, BCH>(smem, 0, 0, wave, ga, gb);
+  w8a16_issue<BM, BN, ACH, BCH, NW>(smem, 0, 0, wave, ga, gb);
   for (int kt = 0; kt < KT; ++kt) {
     __syncthreads();  // this step's stage has landed; the other stage is free
-    if (kt + 1 < KT) w8a16_issue<BM, BN, ACH, BCH>(smem, (kt + 1) & 1, (kt + 1) * BK, wave, ga, gb);
+    if (kt + 1 < KT) w8a16_issue<BM, BN, ACH, BCH, NW>(smem, (kt + 1) & 1, (kt + 1) * BK, wave, ga, gb);
     const uint8_t* sA = smem + (kt & 1) * STAGE + (wm * TM + r16) * 128;
     const uint8_t* sB = smem + (kt & 1) * STAGE + BM * 128 + (wn * TN + r16) * 64;
     u4 blo[FN], bhi[FN];
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_w8a16_lds_kernel(
   }
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
-  store_tile<T, BM, BN, 2, 2>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, *scale, Y);
+  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, *scale, Y);
 }
 
 // ---------------------------------------------------------------------------
@@ -454,18 +457,37 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   if (K % 64 != 0 || !aligned(x, 16) || !aligned(w, 16) || M > 65535 * 64)
     return launch_gemv_generic(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
   {
-    constexpr int BM = 128, BN = 128;
-    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
-    dim3 grid((unsigned)(tm * tn));
+    // Tiles: 128 x 128 with 4 waves and two workgroups per CU, or 256 x 256
+    // with 8 waves (2 x 4) where its last round of workgroups is fuller --
+    // each configuration's measured rate (MI355X, config-4 shapes with fp16
+    // activations) times the fill of its last round over 256 CUs.
+    auto score = [&](int bm, int bn, double rate, int slots) {
+      const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+      const int64_t rounds = (tiles + slots - 1) / slots;
+      // useful share of the tile area the rounds could cover
+      return rate * (double)(M * N) / ((double)(rounds * slots) * bm * bn);
+    };
+    const bool big = score(256, 256, 1300, 256) > score(128, 128, 1150, 512);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     uint16_t* yp = static_cast<uint16_t*>(y);
-#define CEK_W8A16(TY, F) gemm_w8a16_lds_kernel<TY, F, BM, BN, 2><<<grid, 256, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn)
+#define CEK_W8A16_TILE(TY, F, BM, BN, OCC, WM, WN)                                                                 \
+  do {                                                                                                         \
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                    \
+    gemm_w8a16_lds_kernel<TY, F, BM, BN, OCC, WM, WN>                                                          \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn);              \
+  } while (0)
+#define CEK_W8A16(TY, F)                                     \
+  do {                                                       \
+    if (big) CEK_W8A16_TILE(TY, F, 256, 256, 1, 2, 4);       \
+    else CEK_W8A16_TILE(TY, F, 128, 128, 2, 2, 2);           \
+  } while (0)
     if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_W8A16(F16, CEK_E4M3);
     else if (io_dtype == CEK_F16) CEK_W8A16(F16, CEK_E5M2);
     else if (fp8_fmt == CEK_E4M3) CEK_W8A16(BF16, CEK_E4M3);
     else CEK_W8A16(BF16, CEK_E5M2);
 #undef CEK_W8A16
+#undef CEK_W8A16_TILE
     return check_launch();
   }
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
@@ -497,8 +519,8 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
   }
   if (K % 128 == 0) {
     // Tile choice: each configuration's measured rate at full occupancy
-    // (MI355X, BASELINE prefill shapes) times the fraction of the last
-    // round of workgroups that is filled (256 CUs; the 8-wave tiles fit one
+    // (MI355X, BASELINE prefill shapes) times the useful share of the tile
+    // area its rounds of workgroups cover (256 CUs; the 8-wave tiles fit one
     // workgroup per CU, the 4-wave ones two), best score wins:
     //  * 256 x 256, 8 waves (4 x 2, wave tile 64 x 128, two waves per SIMD):
     //    the least LDS traffic per MFMA;
@@ -515,7 +537,8 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     for (int c = 0; c < 4; ++c) {
       const int64_t tiles = ((M + opts[c].bm - 1) / opts[c].bm) * ((N + opts[c].bn - 1) / opts[c].bn);
       const int64_t rounds = (tiles + opts[c].slots - 1) / opts[c].slots;
-      const double score = opts[c].rate * (double)tiles / (double)(rounds * opts[c].slots);
+      // useful share of the tile area the rounds could cover
+      const double score = opts[c].rate * (double)(M * N) / ((double)(rounds * opts[c].slots) * opts[c].bm * opts[c].bn);
       if (score > best) { best = score; cfg = c; }
     }
 #define CEK_A8W8(TY, BM, BN, WM, WN, OCC)                                                               \

@@ -139,3 +139,21 @@ def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
         ops.esimd_gemm_fp8_a8w8(qd, sa.to(dev), Wd, sb.to(dev), y)
         torch.cuda.synchronize()
         assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 1024, 4096), (4000, 576, 4090)])
+@pytest.mark.parametrize("io,fmt", [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)])
+def test_gemm_pert_large_tiles_vs_gpu_fp32(ops, dev, M, K, N, io, fmt):
+    """w8a16 256 x 256 tiles (8 waves), ragged edges, both activation types
+    and fp8 formats, against a float32 torch GPU matmul of the dequantised
+    weights."""
+    _say(f"gemm pert large tiles M={M} K={K} N={N} {io} {fmt}")
+    g = torch.Generator().manual_seed(M + K)
+    W8 = (torch.randn(N, K, generator=g).half() * 0.1).to(fmt).to(dev)
+    x = (torch.randn(M, K, generator=g) * 0.5).to(io).to(dev)
+    sv = torch.tensor(0.05, device=dev)
+    y = torch.zeros(M, N, dtype=io, device=dev)
+    ops.esimd_gemm_fp8_pert(x, W8, sv, y)
+    ref = (x.float() @ W8.float().T) * 0.05
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ref.cpu(), f"pert large M={M} {io} {fmt}")

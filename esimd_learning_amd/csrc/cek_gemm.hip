@@ -374,6 +374,67 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// w8a16 with N <= 16 and M > 16 (the reference's tiny-N M-parallel path,
+// fp8_GEMM_pert.h:3913-3994 via the dispatcher at :4030-4046): here the
+// activations are the large operand, so the roles flip.  A workgroup owns 16
+// activation rows and streams them once; the N (<= 16) weight rows, a few KB
+// that stay in L2, are decoded into the MFMA B operand (rows >= N read row
+// N - 1 and are never stored).  Lane l takes row l & 15 and the 16 K values
+// 16 (l >> 4) .. + 15 of each 64-value step (32 bytes of x, 16 of w); the
+// four waves take the steps s with s % 4 == wave, U in flight, and meet in
+// LDS.  Requires K % 64 == 0 and 16-byte aligned x and w.
+// ---------------------------------------------------------------------------
+template <typename T, int FMT, int U>
+__global__ __launch_bounds__(256) void gemm_w8a16_tinyn_kernel(const uint16_t* __restrict__ X,
+                                                               const uint8_t* __restrict__ W,
+                                                               const float* __restrict__ scale,
+                                                               uint16_t* __restrict__ Y, int M, int N, int K) {
+  __shared__ f4 red[3][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int m0 = blockIdx.x * 16;
+  const uint16_t* xrow = X + (size_t)min(m0 + r16, M - 1) * K + g * 16;  // rows >= M are never stored
+  const uint8_t* wrow = W + (size_t)min(r16, N - 1) * K + g * 16;
+  const int steps = K >> 6;
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = wave; s0 < steps; s0 += 4 * U) {
+    u4 xa[U], xb[U], wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + 4 * u;
+      if (s < steps) {
+        const u4* xp = reinterpret_cast<const u4*>(xrow + (size_t)s * 64);
+        xa[u] = load_u4_stream(xp);
+        xb[u] = load_u4_stream(xp + 1);
+        wv[u] = load_u4(wrow + (size_t)s * 64);
+      } else {
+        xa[u] = xb[u] = wv[u] = u4{0, 0, 0, 0};
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the round before any arithmetic
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      u4 lo, hi;
+      decode16<T, FMT>(wv[u], lo, hi);
+      acc = mfma16x16x32<T>(xa[u], lo, acc);
+      acc = mfma16x16x32<T>(xb[u], hi, acc);
+    }
+  }
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  const f4 c = acc + red[0][lane] + red[1][lane] + red[2][lane];
+  const float sc = *scale;
+  const int n = r16;  // D column = lane & 15
+  if (n >= N) return;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int m = m0 + 4 * g + v;  // D row = 4 * (lane >> 4) + v
+    if (m < M) Y[(size_t)m * N + n] = T::from_f32(c[v] * sc);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // w8a16, direct-from-global v0: 64 x 64 C tile per workgroup, K step 64.
 // ---------------------------------------------------------------------------
 
@@ -450,6 +511,19 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   if (M <= 16) return launch_gemv(x, w, scale, 3 /* f32 scalar */, y, M, N, K, io_dtype, fp8_fmt, st);
+  if (N <= 16 && K % 64 == 0 && aligned(x, 16) && aligned(w, 16) && M <= (int64_t)INT32_MAX - 16) {
+    const dim3 grid((unsigned)((M + 15) / 16));
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    const uint8_t* wp = static_cast<const uint8_t*>(w);
+    uint16_t* yp = static_cast<uint16_t*>(y);
+#define CEK_TINYN(TY, F) gemm_w8a16_tinyn_kernel<TY, F, 4><<<grid, 256, 0, st>>>(xp, wp, scale, yp, (int)M, (int)N, (int)K)
+    if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_TINYN(F16, CEK_E4M3);
+    else if (io_dtype == CEK_F16) CEK_TINYN(F16, CEK_E5M2);
+    else if (fp8_fmt == CEK_E4M3) CEK_TINYN(BF16, CEK_E4M3);
+    else CEK_TINYN(BF16, CEK_E5M2);
+#undef CEK_TINYN
+    return check_launch();
+  }
   if (M <= 32 && aligned(x, 16) && aligned(w, 16)) {
     const int rc = launch_gemv_wide(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
     if (rc != CEK_ERR_UNSUPPORTED) return rc;

@@ -85,7 +85,9 @@ int cek_gemv_fp8_pert_multi(const void* x, int count, const void* const* w, cons
 /*
  * fp8-weight GEMM, fp16|bf16 activations, per-tensor fp32 scale, any M.
  *   Y[m, n] = Out( (sum_k f32(X[m, k]) * dq(W[n, k])) * (*scale) )
- * M <= 16 uses the GEMV kernels; larger M a w8a16 MFMA GEMM.
+ * M <= 16 uses the GEMV kernels; N <= 16 an activation-streaming MFMA
+ * kernel (the reference's tiny-N path); 16 < M <= 32 the LDS-staged GEMV
+ * kernel where it has an instantiation; otherwise a tiled w8a16 MFMA GEMM.
  * Replaces esimd_gemm_fp8_pert, csrc/xpu/esimd_kernel_gemm.sycl:23-65 ->
  * GEMM_fp8_pert_dispatch, csrc/xpu/esimd_kernels/fp8_GEMM_pert.h:4017-4062.
  */

@@ -157,3 +157,19 @@ def test_gemm_pert_large_tiles_vs_gpu_fp32(ops, dev, M, K, N, io, fmt):
     ref = (x.float() @ W8.float().T) * 0.05
     torch.cuda.synchronize()
     assert_close_fp(y.cpu(), ref.cpu(), f"pert large M={M} {io} {fmt}")
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 1, 64), (64, 5, 2048), (300, 16, 4160), (2048, 8, 2048), (33, 16, 64)])
+@pytest.mark.parametrize("io,fmt", [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)])
+def test_gemm_pert_tiny_n(ops, dev, M, N, K, io, fmt):
+    """N <= 16 with M > 16: the activation-streaming kernel (reference tiny-N
+    M-parallel path), against the CPU oracle."""
+    _say(f"gemm pert tiny N M={M} N={N} K={K} {io} {fmt}")
+    g = torch.Generator().manual_seed(M * 7 + N)
+    W8 = (torch.randn(N, K, generator=g).half() * 0.1).to(fmt)
+    x = (torch.randn(M, K, generator=g) * 0.5).to(io)
+    sv = torch.tensor(0.08)
+    y = torch.zeros(M, N, dtype=io, device=dev)
+    ops.esimd_gemm_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemm_fp8_pert(x, W8, sv), f"tiny N M={M} N={N} K={K}")

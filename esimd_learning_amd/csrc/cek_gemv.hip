@@ -355,15 +355,24 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // ahead into registers (a ring of D + 1 slots, so the loop body is unrolled
 // D + 1 times); stage i is copied into one of two LDS buffers, then read back
 // in MFMA layout.  K = 1024 STEPS.
-template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS>
+template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M) {
   static_assert(D >= 1 && D <= STEPS, "prefetch depth");
+  static_assert(MX == 0 || (MB == 1 && MX <= 8), "activations go through LDS only for M <= 8");
   constexpr int K = STEPS * 1024;
   constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
   constexpr int XB = XF8 ? 1 : 2;  // activation bytes per value
   constexpr int LW = ROWS / 4;     // weight rows per wave and stage
-  __shared__ __align__(16) uint8_t smem[2 * STAGE];
+  // MX > 0: the stage's activations (MX rows, rows >= M repeating row M - 1)
+  // are loaded 16 contiguous bytes per lane and staged in LDS next to the
+  // weights, XU units per thread; MX = 0: each lane loads its MFMA operands
+  // straight from L2 (all 16 operand rows, the clamped ones included).
+  constexpr int XROW = 1024 * XB;                  // activation bytes per row and stage
+  constexpr int XU = MX > 0 ? MX * XROW / 16 / 256 : 1;
+  constexpr int XSTAGE = MX * XROW;
+  static_assert(MX == 0 || XU * 16 * 256 == XSTAGE, "activation units per thread");
+  __shared__ __align__(16) uint8_t smem[2 * (STAGE + XSTAGE)];
   const SegRef sr = find_seg(sg, blockIdx.x);
   const int N = sr.n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -379,26 +388,40 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 #pragma unroll
   for (int b = 0; b < MB; ++b)  // rows >= M are never stored
     gx[b] = static_cast<const uint8_t*>(xv) + (size_t)min(16 * b + n16, M - 1) * K * XB;
+  // MX > 0: thread t's units t + 256 j of the MX x XROW stage: row, 16-byte chunk
+  const uint8_t* gxu[XU];
+  int xdst[XU];
+#pragma unroll
+  for (int j = 0; j < XU; ++j) {
+    const int q = threadIdx.x + 256 * j, row = q / (XROW / 16), col = q % (XROW / 16);
+    gxu[j] = static_cast<const uint8_t*>(xv) + (size_t)min(row, M - 1) * K * XB + 16 * col;
+    xdst[j] = row * XROW + 16 * (col ^ (row & 7));  // chunk c of row r at c ^ (r & 7)
+  }
 
   // Unit (16 K values) of operand group q for this lane: XF8 = false: unit
   // 4 (wave + 4 q) + g; XF8 = true: units 2 (4 (wave + 4 q) + g) and the next.
   auto unit = [&](int q) { return XF8 ? 2 * (4 * (wave + 4 * q) + g) : 4 * (wave + 4 * q) + g; };
 
   u4 wr[S][LW];
-  u4 xr[S][QN][MB][2];
-  auto issue = [&](int i, u4 (&ws)[LW], u4 (&xs)[QN][MB][2]) {
+  u4 xr[S][MX > 0 ? XU : QN][MX > 0 ? 1 : MB][MX > 0 ? 1 : 2];
+  auto issue = [&](int i, u4 (&ws)[LW], u4 (&xs)[MX > 0 ? XU : QN][MX > 0 ? 1 : MB][MX > 0 ? 1 : 2]) {
     const int k0 = i << 10;
 #pragma unroll
     for (int j = 0; j < LW; ++j) ws[j] = load_u4_stream(gw[j] + k0);  // 1 KB of one row per instruction
     asm volatile("" ::: "memory");  // same issue order in every step (weights, then activations)
+    if constexpr (MX > 0) {
 #pragma unroll
-    for (int q = 0; q < QN; ++q)
+      for (int j = 0; j < XU; ++j) xs[j][0][0] = load_u4(gxu[j] + (size_t)k0 * XB);
+    } else {
 #pragma unroll
-      for (int b = 0; b < MB; ++b) {
-        const u4* p = reinterpret_cast<const u4*>(gx[b] + (size_t)(k0 + 16 * unit(q)) * XB);
-        xs[q][b][0] = p[0];
-        xs[q][b][1] = p[1];
-      }
+      for (int q = 0; q < QN; ++q)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          const u4* p = reinterpret_cast<const u4*>(gx[b] + (size_t)(k0 + 16 * unit(q)) * XB);
+          xs[q][b][0] = p[0];
+          xs[q][b][1] = p[1];
+        }
+    }
     asm volatile("" ::: "memory");
   };
 
@@ -420,13 +443,27 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     // wave finished before the barrier of step i - 1).  Lane l's unit lands
     // at slot l, i.e. unit v of row r at slot v ^ (r & 15).
     uint8_t* sw = smem + (i & 1) * STAGE;
+    uint8_t* sx = smem + 2 * STAGE + (i & 1) * XSTAGE;
 #pragma unroll
     for (int jj = 0; jj < LW; ++jj) *reinterpret_cast<u4*>(sw + (wave + 4 * jj) * 1024 + 16 * lane) = wr[i % S][jj];
+    if constexpr (MX > 0) {
+#pragma unroll
+      for (int j = 0; j < XU; ++j) *reinterpret_cast<u4*>(sx + xdst[j]) = xr[i % S][j][0][0];
+    }
     lds_barrier();
     if (i + D < STEPS) issue(i + D, wr[(i + D) % S], xr[(i + D) % S]);
+    const int xrow = min(n16, M - 1);  // MX > 0: this lane's operand row in LDS
+    const uint8_t* sxr = sx + xrow * XROW;
 #pragma unroll
     for (int q = 0; q < QN; ++q) {
       const int v = unit(q);
+      // this lane's activation operand for group q: 32 bytes of its row
+      u4 xa0, xa1;
+      if constexpr (MX > 0) {
+        const int c0 = XF8 ? v : 2 * v;  // first 16-byte chunk
+        xa0 = *reinterpret_cast<const u4*>(sxr + 16 * (c0 ^ (xrow & 7)));
+        xa1 = *reinterpret_cast<const u4*>(sxr + 16 * ((c0 + 1) ^ (xrow & 7)));
+      }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const uint8_t* rw = sw + (16 * t + n16) * 1024;  // row 16 t + n16: slots are v ^ n16
@@ -434,15 +471,22 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           const i8 bf = cat_i8(*reinterpret_cast<const u4*>(rw + 16 * (v ^ n16)),
                                *reinterpret_cast<const u4*>(rw + 16 * ((v + 1) ^ n16)));
 #pragma unroll
-          for (int b = 0; b < MB; ++b)
-            acc[t][b] = mfma_fp8_16x16x128(cat_i8(xr[i % S][q][b][0], xr[i % S][q][b][1]), bf, acc[t][b]);
+          for (int b = 0; b < MB; ++b) {
+            if constexpr (MX > 0) acc[t][b] = mfma_fp8_16x16x128(cat_i8(xa0, xa1), bf, acc[t][b]);
+            else acc[t][b] = mfma_fp8_16x16x128(cat_i8(xr[i % S][q][b][0], xr[i % S][q][b][1]), bf, acc[t][b]);
+          }
         } else {
           u4 lo, hi;
           decode16<T, FMT>(*reinterpret_cast<const u4*>(rw + 16 * (v ^ n16)), lo, hi);
 #pragma unroll
           for (int b = 0; b < MB; ++b) {
-            acc[t][b] = mfma16x16x32<T>(xr[i % S][q][b][0], lo, acc[t][b]);
-            acc[t][b] = mfma16x16x32<T>(xr[i % S][q][b][1], hi, acc[t][b]);
+            if constexpr (MX > 0) {
+              acc[t][b] = mfma16x16x32<T>(xa0, lo, acc[t][b]);
+              acc[t][b] = mfma16x16x32<T>(xa1, hi, acc[t][b]);
+            } else {
+              acc[t][b] = mfma16x16x32<T>(xr[i % S][q][b][0], lo, acc[t][b]);
+              acc[t][b] = mfma16x16x32<T>(xr[i % S][q][b][1], hi, acc[t][b]);
+            }
           }
         }
       }
@@ -496,7 +540,19 @@ template <typename T, typename TO, int FMT, bool XF8, int S>
 static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int N, hipStream_t st) {
 #define CEK_LDS(NT, MB, D) \
   gemv_lds_kernel<T, TO, FMT, XF8, NT, MB, D, S><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M)
+#define CEK_LDS_MX(NT, D, MX) \
+  gemv_lds_kernel<T, TO, FMT, XF8, NT, 1, D, S, MX><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M)
   constexpr bool SHORT = S >= 3 && S <= 5;
+  if constexpr (!XF8) {
+    // fp16/bf16, M <= 8, up to 12288 rows: activations staged through LDS
+    // (contiguous loads of just the M rows) -- 5-20% faster there, slower
+    // for wider matrices.
+    if (M <= 8 && N <= 12288 && !(SHORT && M >= 8 && N >= 6144)) {
+      if (M <= 4) CEK_LDS_MX(1, (S >= 3 ? 3 : 2), 4);
+      else CEK_LDS_MX(1, 2, 8);
+      return true;
+    }
+  }
   if (M <= 16) {
     if constexpr (SHORT) {
       // Two 16-row tiles per workgroup halve the activation re-reads once
@@ -523,6 +579,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   }
   return false;
 #undef CEK_LDS
+#undef CEK_LDS_MX
 }
 
 template <typename T, typename TO, int FMT, bool XF8>
@@ -544,9 +601,12 @@ static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bo
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   int N = 0;  // launch shape is chosen from the total row count
   for (int i = 0; i < sg.count; ++i) N += sg.n[i];
-  // M >= 3: the LDS-staged MFMA kernel (measured faster than the v_dot2
-  // kernel from three rows on, and than the direct MFMA kernel throughout).
-  if (vec16 && M >= 3 && launch_lds<T, TO, FMT, XF8>(x, sg, skind, M, K, N, st)) return check_launch();
+  // The LDS-staged MFMA kernel from three rows on (measured faster than the
+  // v_dot2 kernel there, and than the direct MFMA kernel throughout); from two
+  // rows on for K >= 14336, whose v_dot2 workgroups re-read long activation
+  // rows.
+  const int m_lds = K >= 14336 ? 2 : 3;
+  if (vec16 && M >= m_lds && launch_lds<T, TO, FMT, XF8>(x, sg, skind, M, K, N, st)) return check_launch();
   if (M > 16) return CEK_ERR_UNSUPPORTED;
   if (vec16 && M <= 4) {
     // Rows per workgroup (measured on MI355X, one pass over > 2 GB of

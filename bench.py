@@ -10,8 +10,10 @@ weights in the 256 MB Infinity Cache.  All inputs are resident in HBM before
 the timed region.
 
 Timing: W untimed warm-up steps, then exactly K steps captured in one HIP
-graph (so host launch cost is not measured) and replayed once between
-device synchronisations; ms_per_step = wall time / K.  The dominant kernel's
+graph (so host launch cost is not measured); the graph is replayed untimed
+for WARM_S seconds (a cold MI355X runs the first replays 7-20% slower while
+its clocks settle), then replayed once, timed, between device
+synchronisations; ms_per_step = wall time / K.  The dominant kernel's
 average launch duration is measured with HIP events on the launch stream
 around the same graph replay; it feeds roofline.achieved.
 
@@ -41,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, spec
 FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA, spec
 ROTATE_BYTES = 2.2e9
+WARM_S = 1.0                   # graph replays before each headline timing (clock settling)
 
 
 def log(msg):
@@ -56,8 +59,11 @@ def gemm_a8w8_bytes(M, N, K):
     return M * K + N * K + 2 * M * N + 4 * M + 4 * N
 
 
-def time_graph(fn_list, torch, stream):
-    """Capture fn_list (one launch each) in a graph, replay once, return (wall_s, event_ms)."""
+def time_graph(fn_list, torch, stream, warm_s=0.0):
+    """Capture fn_list (one launch each) in a graph, replay it for warm_s
+    seconds (the GPU's clocks take about a second of load to settle: a cold
+    GPU runs the first replays 7% (GEMV) to 20% (GEMM) slower), then time one
+    replay between device synchronisations; returns (wall_s, event_ms, graph)."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for fn in fn_list:
@@ -65,6 +71,10 @@ def time_graph(fn_list, torch, stream):
     torch.cuda.synchronize()
     g.replay()                      # warm replay (graph upload)
     torch.cuda.synchronize()
+    t_end = time.perf_counter() + warm_s
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -108,7 +118,7 @@ def bench_gemv(ops, torch, steps, warmup, M=1, K=4096, N=14336):
         for i in range(warmup):
             step(i)()
     torch.cuda.synchronize()
-    wall, ev_ms, _ = time_graph([step(i) for i in range(steps)], torch, stream)
+    wall, ev_ms, _ = time_graph([step(i) for i in range(steps)], torch, stream, warm_s=WARM_S)
     nbytes = gemv_bytes(M, N, K)
     avg_launch_us = ev_ms * 1e3 / steps
     res = {
@@ -182,7 +192,7 @@ def bench_gemv_table(ops, torch, shapes=((4096, 14336), (4096, 6144), (4096, 409
                 for f in fns[:copies]:
                     f()
             torch.cuda.synchronize()
-            _, ev_ms, _ = time_graph(fns, torch, stream)
+            _, ev_ms, _ = time_graph(fns, torch, stream, warm_s=0.1)
             us = ev_ms * 1e3 / len(fns)
             rows.append({"M": M, "K": K, "N": N, "us": round(us, 2),
                          "GBps": round(gemv_bytes(M, N, K) / (us * 1e-6) / 1e9, 1)})
@@ -219,12 +229,12 @@ def bench_norm_quant_gemv(ops, torch, reps=50, N=6144):
                 norm()
                 gemv[0]()
             torch.cuda.synchronize()
-            _, n_ms, _ = time_graph([norm] * reps, torch, stream)
-            _, g_ms, _ = time_graph(gemv * 2, torch, stream)
+            _, n_ms, _ = time_graph([norm] * reps, torch, stream, warm_s=0.05)
+            _, g_ms, _ = time_graph(gemv * 2, torch, stream, warm_s=0.05)
             pair = []
             for i in range(reps):
                 pair += [norm, gemv[i % copies]]
-            _, p_ms, _ = time_graph(pair, torch, stream)
+            _, p_ms, _ = time_graph(pair, torch, stream, warm_s=0.05)
             rows.append({"T": T, "H": H, "norm_quant_us": round(n_ms * 1e3 / reps, 2),
                          "gemv_us": round(g_ms * 1e3 / (2 * copies), 2),
                          "pair_us": round(p_ms * 1e3 / reps, 2)})
@@ -250,7 +260,7 @@ def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
         for _ in range(warmup):
             fn()
     torch.cuda.synchronize()
-    wall, ev_ms, _ = time_graph([fn] * steps, torch, stream)
+    wall, ev_ms, _ = time_graph([fn] * steps, torch, stream, warm_s=WARM_S)
     flops = 2.0 * M * N * K
     us = ev_ms * 1e3 / steps
     return {"config": f"a8w8 M={M} K={K} N={N}", "avg_launch_us": us,
@@ -287,9 +297,10 @@ def bench_layer(torch, steps, M=4, act_fp8=False):
     layer.step(h, r, pos)
     torch.cuda.synchronize()
     g = layer.capture(h, r, pos)
-    for _ in range(3):
+    t_end = time.perf_counter() + WARM_S / 2
+    while time.perf_counter() < t_end:
         g.replay()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):

@@ -124,10 +124,13 @@ def test_a8w8_decode_rows(ops, dev, M, K, N):
         assert_close_fp(y.cpu(), ref, f"a8w8 decode M={M} {out_dt}")
 
 
-@pytest.mark.parametrize("M,K,N", [(4096, 1024, 8192), (4000, 512, 8150), (2000, 1024, 6100), (2048, 512, 6144)])
+@pytest.mark.parametrize("M,K,N", [(4096, 1024, 8192), (4000, 512, 8150), (2000, 1024, 6100), (2048, 512, 6144),
+                                   (2048, 640, 6144), (2048, 128, 6144), (2040, 384, 6100)])
 def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
     """The 256 x 256 and 256 x 192 tile configurations (8 waves), including
-    ragged M and N, against a float32 torch GPU matmul of the dequantised codes."""
+    ragged M and N, against a float32 torch GPU matmul of the dequantised codes.
+    The 256 x 192 shapes run the register-pipelined kernel; K = 640 and 128
+    give it an odd number of K steps and a single one."""
     _say(f"a8w8 large tiles M={M} K={K} N={N}")
     q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M + N)
     qd, Wd = q.to(dev), W8.to(dev)

@@ -285,21 +285,28 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_lds_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// a8w8, LDS-tiled with register-pipelined fragment reads and an NS-stage LDS
-// ring.  Same tiles, stage layout, swizzle and direct-to-LDS loads as
-// gemm_a8w8_lds_kernel; the difference is the order of work inside a K step.
-// A wave's step is FM groups of FN MFMAs (group i: A fragment i against the
-// FN B fragments).  The A fragment of group i + 1 is read from LDS while group
-// i's MFMAs run (two A register sets), and the step's one barrier sits before
-// the last group: after it the wave issues the direct-to-LDS loads of step
-// k + NS into the stage step k used, and reads step k + 1's B fragments and
-// first A fragment (two B register sets) behind the last group's MFMAs.
-// LDS latency and the barrier wait are covered by MFMAs already in flight
-// instead of stalling the matrix core at the top of every step, and the
-// global loads of a stage have NS - 1 steps to land.  The barrier orders, for
-// all waves: step k + 1's stage has landed (every load but those of the
-// NS - 2 younger stages is complete), every read of step k's stage is done
-// (lgkmcnt(0)), so it may be overwritten.
+// a8w8, LDS-tiled with register-pipelined fragment reads and separate A and
+// B stage rings.  Same K slices, row layout, swizzle and direct-to-LDS loads
+// as gemm_a8w8_lds_kernel; the difference is the order of work inside a K
+// step.  A wave's step is FM groups of FN MFMAs (group i: A fragment i
+// against the FN B fragments).  The A fragment of group i + 1 is read from
+// LDS while group i's MFMAs run (two A register sets), and the step's one
+// barrier sits before the last group: after it the wave issues the
+// direct-to-LDS loads of step k + NB's B rows and step k + NA's A rows into
+// the slots step k used, and reads step k + 1's B fragments and first A
+// fragment (two B register sets) behind the last group's MFMAs.  LDS latency
+// and the barrier wait are covered by MFMAs already in flight.
+// A and B have rings of their own because a step reads its B rows all at
+// once (at the previous step's barrier) but its A rows group by group: with
+// NA = 3 A slots and NB = 2 B slots (144 KB at 256 x 192, where three joint
+// stages would not fit in LDS) the A loads of a step have two steps to land
+// and the B loads, issued first, one.  On MI355X that measured 3-6% slower
+// than NA = 2 at M = 2048 (as did three joint stages for 256 x 128 tiles):
+// the loads are not latency-bound here, so the dispatcher uses NA = 2.
+// The barrier orders, for all waves:
+// step k + 1's A and B rows have landed (every load but the A rows of step
+// k + 2, issued last, is complete), every read of step k's slots is done
+// (lgkmcnt(0)), so they may be overwritten.
 // Requires K % 128 == 0, FM even, 16-byte aligned A and B.
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN>
@@ -307,9 +314,9 @@ struct PipeCfg {
   static constexpr int BK = 128;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 16, FN = TN / 16;
-  static constexpr int STAGE = (BM + BN) * BK;
+  static constexpr int ASLOT = BM * BK, BSLOT = BN * BK;
   static constexpr int NW = WM * WN;
-  static constexpr int ACH = BM / 8 / NW, BCH = BN / 8 / NW;
+  static constexpr int ACH = BM / 8 / NW, BCH = BN / 8 / NW;  // 1 KB loads per wave and slot
   static_assert(ACH * 8 * NW == BM && BCH * 8 * NW == BN, "writer chunks cover the tile");
   static_assert(FM % 2 == 0, "A fragments alternate between two register sets");
 };
@@ -322,31 +329,42 @@ __device__ inline void barrier_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int NS>
-__device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* smem, int wave, int wm, int wn, int r16,
-                                               int p0, int p1, const uint8_t* const (&ga)[PipeCfg<BM, BN, WM, WN>::ACH],
+// Direct-to-LDS loads of one K step (128 bytes) of CH 1 KB row chunks into a
+// slot: this wave's chunks j = wave + NW i (rows 8 j .. 8 j + 7).
+template <int CH, int NW>
+__device__ inline void a8w8_issue_rows(uint8_t* slot, int kb, int wave, const uint8_t* const (&gp)[CH]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int i = 0; i < CH; ++i)
+    __builtin_amdgcn_global_load_lds(gp[i] + kb, (lds_ptr_t)(slot + (wave + NW * i) * 1024), 16, 0, 0);
+#endif
+}
+
+template <int BM, int BN, int WM, int WN, int NA, int NB>
+__device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uint8_t* sBr, int wave, int wm, int wn,
+                                               int r16, int p0, int p1,
+                                               const uint8_t* const (&ga)[PipeCfg<BM, BN, WM, WN>::ACH],
                                                const uint8_t* const (&gb)[PipeCfg<BM, BN, WM, WN>::BCH],
                                                f4 (&acc)[PipeCfg<BM, BN, WM, WN>::FM][PipeCfg<BM, BN, WM, WN>::FN],
                                                i8 (&a)[2], const i8 (&bc)[PipeCfg<BM, BN, WM, WN>::FN],
                                                i8 (&bn)[PipeCfg<BM, BN, WM, WN>::FN]) {
   using C = PipeCfg<BM, BN, WM, WN>;
-  constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, STAGE = C::STAGE;
-  constexpr int G = C::ACH + C::BCH;  // loads per wave and stage
-  const int cur = kt % NS;
-  const uint8_t* sA = smem + cur * STAGE + (wm * TM + r16) * BK;
+  constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, ACH = C::ACH, NW = C::NW;
+  const int ca = kt % NA, cb = kt % NB;
+  const uint8_t* sA = sAr + ca * C::ASLOT + (wm * TM + r16) * BK;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     if (i + 1 < FM) {
       a[(i + 1) & 1] = lds_frag(sA + (i + 1) * 16 * BK, p0, p1);
     } else if (kt + 1 < KT) {
-      // the stages younger than kt + 1 that were issued may stay in flight
-      if (NS > 2 && kt + NS - 1 < KT) barrier_vmcnt<(NS > 2 ? (NS - 2) * G : 0)>();
+      // with NA = 3 the A rows of step k + 2, the newest loads, may still fly
+      if (NA > 2 && kt + 2 < KT) barrier_vmcnt<(NA > 2 ? ACH : 0)>();
       else barrier_vmcnt<0>();
-      if (kt + NS < KT)
-        a8w8_issue<BM, BN, C::ACH, C::BCH, C::NW>(smem, cur, (kt + NS) * BK, wave, ga, gb);
-      const int nxt = cur + 1 == NS ? 0 : cur + 1;
-      const uint8_t* nA = smem + nxt * STAGE + (wm * TM + r16) * BK;
-      const uint8_t* nB = smem + nxt * STAGE + (BM + wn * TN + r16) * BK;
+      if (kt + NB < KT) a8w8_issue_rows<C::BCH, NW>(sBr + cb * C::BSLOT, (kt + NB) * BK, wave, gb);
+      if (kt + NA < KT) a8w8_issue_rows<ACH, NW>(sAr + ca * C::ASLOT, (kt + NA) * BK, wave, ga);
+      const int na = ca + 1 == NA ? 0 : ca + 1, nb = cb + 1 == NB ? 0 : cb + 1;
+      const uint8_t* nA = sAr + na * C::ASLOT + (wm * TM + r16) * BK;
+      const uint8_t* nB = sBr + nb * C::BSLOT + (wn * TN + r16) * BK;
 #pragma unroll
       for (int j = 0; j < FN; ++j) bn[j] = lds_frag(nB + j * 16 * BK, p0, p1);
       a[0] = lds_frag(nA, p0, p1);
@@ -357,19 +375,23 @@ __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* smem, in
   }
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int OCC, int NS>
+template <typename T, int BM, int BN, int WM, int WN, int OCC, int NA, int NB>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sa,
     const uint8_t* __restrict__ B, const float* __restrict__ sb,
     uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
   using C = PipeCfg<BM, BN, WM, WN>;
-  constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, STAGE = C::STAGE, NW = C::NW;
-  constexpr int ACH = C::ACH, BCH = C::BCH, G = ACH + BCH;
-  static_assert(NS == 2 || NS == 3, "two or three stages");
-  constexpr int SMEM = NS * STAGE > BM * BN * 2 ? NS * STAGE : BM * BN * 2;
+  constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NW = C::NW;
+  constexpr int ACH = C::ACH, BCH = C::BCH;
+  static_assert(NB == 2 && (NA == 2 || NA == 3), "A slots 2 or 3, B slots 2");
+  constexpr int RINGS = NA * C::ASLOT + NB * C::BSLOT;
+  constexpr int SMEM = RINGS > BM * BN * 2 ? RINGS : BM * BN * 2;
   static_assert(BM + BN <= 64 * NW, "one scale per thread");
-  // the stages (or the output tile), then the tile's row and column scales
+  // the A ring and the B ring (or the output tile), then the tile's row and
+  // column scales
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + (BM + BN) * 4];
+  uint8_t* sAr = smem;
+  uint8_t* sBr = smem + NA * C::ASLOT;
   float* sc = reinterpret_cast<float*>(smem + SMEM);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -378,7 +400,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   // The epilogue's scales go to LDS first, by 4-byte direct-to-LDS loads
-  // (one instruction per wave for 64 of them), so that stage 0's wait covers
+  // (one instruction per wave for 64 of them), so that step 0's wait covers
   // their latency; register loads mixed with the direct-to-LDS ones would
   // make the compiler drain every load before using them.
   if (64 * wave < BM + BN) {
@@ -389,6 +411,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
 #endif
   }
 
+  // writer chunk j: lane i fills row 8 j + (i >> 3), position i & 7, i.e.
+  // logical chunk (i & 7) ^ s(row)
   const uint8_t* ga[ACH];
   const uint8_t* gb[BCH];
 #pragma unroll
@@ -411,36 +435,47 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
-  // stages 0 .. NS - 1 in flight; wait for stage 0
-  a8w8_issue<BM, BN, ACH, BCH, NW>(smem, 0, 0, wave, ga, gb);
-  if (KT > 1) a8w8_issue<BM, BN, ACH, BCH, NW>(smem, 1, BK, wave, ga, gb);
-  if (NS > 2 && KT > 2) a8w8_issue<BM, BN, ACH, BCH, NW>(smem, 2 % NS, 2 * BK, wave, ga, gb);
-  if (NS > 2) {
+  // Prologue, in the issue order the steps' waits assume: B 0, A 0, then
+  // (NA = 3) A 1, B 1, A 2 or (NA = 2) B 1, A 1; wait for step 0's rows.
+  a8w8_issue_rows<BCH, NW>(sBr, 0, wave, gb);
+  a8w8_issue_rows<ACH, NW>(sAr, 0, wave, ga);
+  if (NA > 2) {
+    if (KT > 1) {
+      a8w8_issue_rows<ACH, NW>(sAr + C::ASLOT, BK, wave, ga);
+      a8w8_issue_rows<BCH, NW>(sBr + C::BSLOT, BK, wave, gb);
+    }
     if (KT > 2) {
-      barrier_vmcnt<2 * G>();
+      a8w8_issue_rows<ACH, NW>(sAr + 2 * C::ASLOT, 2 * BK, wave, ga);
+      barrier_vmcnt<(NA > 2 ? 2 * ACH + BCH : 0)>();
     } else if (KT > 1) {
-      barrier_vmcnt<G>();
+      barrier_vmcnt<ACH + BCH>();
     } else {
       barrier_vmcnt<0>();
     }
   } else {
-    if (KT > 1) barrier_vmcnt<G>();
-    else barrier_vmcnt<0>();
+    if (KT > 1) {
+      a8w8_issue_rows<BCH, NW>(sBr + C::BSLOT, BK, wave, gb);
+      a8w8_issue_rows<ACH, NW>(sAr + C::ASLOT, BK, wave, ga);
+      barrier_vmcnt<ACH + BCH>();
+    } else {
+      barrier_vmcnt<0>();
+    }
   }
   i8 a[2], b0[FN], b1[FN];
   {
-    const uint8_t* sA = smem + (wm * TM + r16) * BK;
-    const uint8_t* sB = smem + (BM + wn * TN + r16) * BK;
+    const uint8_t* sA = sAr + (wm * TM + r16) * BK;
+    const uint8_t* sB = sBr + (wn * TN + r16) * BK;
 #pragma unroll
     for (int j = 0; j < FN; ++j) b0[j] = lds_frag(sB + j * 16 * BK, p0, p1);
     a[0] = lds_frag(sA, p0, p1);
   }
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    a8w8_pipe_step<BM, BN, WM, WN, NS>(kt, KT, smem, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b0, b1);
-    a8w8_pipe_step<BM, BN, WM, WN, NS>(kt + 1, KT, smem, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b1, b0);
+    a8w8_pipe_step<BM, BN, WM, WN, NA, NB>(kt, KT, sAr, sBr, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, NA, NB>(kt + 1, KT, sAr, sBr, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b1, b0);
   }
-  if (kt < KT) a8w8_pipe_step<BM, BN, WM, WN, NS>(kt, KT, smem, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b0, b1);
+  if (kt < KT)
+    a8w8_pipe_step<BM, BN, WM, WN, NA, NB>(kt, KT, sAr, sBr, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b0, b1);
 
   static_assert(SMEM >= BM * BN * 2, "output tile must fit");
   store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y);
@@ -795,10 +830,10 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     gemm_a8w8_lds_kernel<TY, BM, BN, WM, WN, CEK_A8W8_LAYOUT, OCC>                                    \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
-#define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, NS)                                                      \
+#define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, NA)                                                      \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, NS>                                                \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, NA, 2>                                             \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
     if (out_dtype == CEK_F16) {

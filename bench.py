@@ -1,6 +1,6 @@
 """Benchmark of the fp8 decode GEMV (headline) and the fp8 prefill GEMM.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--no-layer] [--no-tables]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--warm-s S] [--no-cpu] [--no-gemm] [--no-layer] [--no-tables]
 
 Headline workload (headline shape): esimd_gemv_fp8_pern
 with M = 1, K = 4096, N = 14336: fp16 activations, e4m3 weights with an fp32
@@ -359,6 +359,7 @@ def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
 
 
 def main():
+    global WARM_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
@@ -367,9 +368,13 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--no-tables", action="store_true", help="skip the config-2 GEMV table and config-3 legs")
+    ap.add_argument("--warm-s", type=float, default=None,
+                    help=f"seconds of untimed graph replays before each headline timing (default {WARM_S})")
     ap.add_argument("--copy-ref", action="store_true",
                     help="first run 10 plain device copies of N*K bytes (reference for HBM counter scaling)")
     a = ap.parse_args()
+    if a.warm_s is not None:
+        WARM_S = max(0.0, a.warm_s)
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the op pack has no "
               f"multi-GPU path. Run with --gpus 1.", file=sys.stderr)

@@ -51,6 +51,22 @@ __device__ inline float load_scale(const void* s, int kind, int n) {
   }
 }
 
+// The same in two halves, for kernels that load the scale long before they
+// use it: the load alone (raw bits, no conversion, so nothing waits for it
+// until scale_value) and the conversion.
+__device__ inline uint32_t load_scale_bits(const void* s, int kind, int n) {
+  uint32_t b;
+  if (kind == SK_F16 || kind == SK_BF16) b = reinterpret_cast<const uint16_t*>(s)[n];
+  else if (kind == SK_F32) b = reinterpret_cast<const uint32_t*>(s)[n];
+  else b = *reinterpret_cast<const uint32_t*>(s);
+  return b;
+}
+__device__ inline float scale_value(uint32_t b, int kind) {
+  if (kind == SK_F16) return F16::to_f32((uint16_t)b);
+  if (kind == SK_BF16) return BF16::to_f32((uint16_t)b);
+  return __uint_as_float(b);
+}
+
 constexpr int MAX_SEGS = 8;
 
 // Weight matrices sharing one x; gstart[i] = first workgroup of segment i.
@@ -102,6 +118,18 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
   const int lane = t & 63, wave = t >> 6;
   const int row0 = sr.group * R;
   const int K16 = K >> 4;
+  // Output scales are loaded up front: their latency then overlaps the
+  // weight loads' instead of following the reduction with the workgroup's
+  // slot held and no weight bytes in flight.
+  uint32_t sc_bits = 0;
+  float sc_m = 1.f;
+  if (t < MT * R) {
+    const int m = t / R, n = row0 + t % R;
+    if (m < M && n < N) {
+      sc_bits = load_scale_bits(sr.s, skind, n);
+      if (XF8) sc_m = sg.xs[m];
+    }
+  }
 
   const uint8_t* wrow[R];
 #pragma unroll
@@ -184,8 +212,8 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
     const int m = t / R, r = t % R, n = row0 + r;
     if (m < M && n < N) {
       float s = red[0][t] + red[1][t] + red[2][t] + red[3][t];
-      if (XF8) s *= sg.xs[m];
-      sr.y[(size_t)m * N + n] = TO::from_f32(s * load_scale(sr.s, skind, n));
+      if (XF8) s *= sc_m;
+      sr.y[(size_t)m * N + n] = TO::from_f32(s * scale_value(sc_bits, skind));
     }
   }
 }
@@ -218,6 +246,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
   const bool xrow_ok = r16 < M;
   const uint16_t* xrow = x + (size_t)(xrow_ok ? r16 : 0) * K + g * 16;
   const uint8_t* xrow8 = reinterpret_cast<const uint8_t*>(x) + (size_t)(xrow_ok ? r16 : 0) * K + g * 16;
+  // wave 0's output scales, loaded up front (their latency then overlaps the
+  // weight loads')
+  uint32_t sc_n[NT];
+  float sc_m[4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) sc_n[t] = wave == 0 ? load_scale_bits(sr.s, skind, min(n0 + t * 16 + r16, N - 1)) : 0u;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sc_m[v] = (XF8 && wave == 0) ? sg.xs[min(g * 4 + v, M - 1)] : 1.f;
 
   f4 acc[NT];
 #pragma unroll
@@ -268,11 +304,11 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
     f4 c = acc[t] + red[0][t][lane] + red[1][t][lane] + red[2][t][lane];
     const int n = n0 + t * 16 + r16;  // D column = lane & 15
     if (n >= N) continue;
-    const float sc = load_scale(sr.s, skind, n);
+    const float sc = scale_value(sc_n[t], skind);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = g * 4 + v;  // D row = 4 * (lane >> 4) + v
-      if (m < M) sr.y[(size_t)m * N + n] = TO::from_f32(c[v] * (XF8 ? sc * sg.xs[m] : sc));
+      if (m < M) sr.y[(size_t)m * N + n] = TO::from_f32(c[v] * (XF8 ? sc * sc_m[v] : sc));
     }
   }
 }
@@ -303,9 +339,26 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
 //  * gemv_lds_a8w8_kernel: e4m3 activation codes with per-row scales; two
 //    units per lane feed one v_mfma_f32_16x16x128_f8f6f4 (no decode).
 // ---------------------------------------------------------------------------
+// Wave 0's output scales of the LDS-staged kernels: sc_n[t] (raw bits) for
+// column n0 + 16 t + (lane & 15), sc_m[b][v] for row 16 b + 4 (lane >> 4) + v (xs:
+// per-row activation scales, or null).  Loaded at the start of the kernel so
+// that their latency overlaps the weight loads'.
+template <int NT, int MB>
+__device__ inline void lds_load_scales(uint32_t (&sc_n)[NT], float (&sc_m)[MB][4], int wave, int lane, int n0, int N,
+                                       int M, const SegRef& sr, int skind, const float* xs) {
+  const int n16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) sc_n[t] = wave == 0 ? load_scale_bits(sr.s, skind, min(n0 + t * 16 + n16, N - 1)) : 0u;
+#pragma unroll
+  for (int b = 0; b < MB; ++b)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sc_m[b][v] = (xs && wave == 0) ? xs[min(b * 16 + g * 4 + v, M - 1)] : 1.f;
+}
+
 template <int NT, int MB>
 __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wave, int lane, int n0, int N,
-                                        int M, const SegRef& sr, int skind, const float* xs, bool bf16_out) {
+                                        int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
+                                        const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
   f4* red = reinterpret_cast<f4*>(smem);  // [3][NT][MB][64]
   __syncthreads();                         // every wave is done with the stages
   if (wave > 0) {
@@ -321,7 +374,7 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
   for (int t = 0; t < NT; ++t) {
     const int n = n0 + t * 16 + n16;  // D column = lane & 15
     if (n >= N) continue;
-    const float sc = load_scale(sr.s, skind, n);
+    const float sc = scale_value(sc_n[t], skind);
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
       f4 c = acc[t][b];
@@ -331,7 +384,7 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
       for (int v = 0; v < 4; ++v) {
         const int m = b * 16 + g * 4 + v;  // D row = 4 * (lane >> 4) + v
         if (m >= M) continue;
-        const float o = c[v] * (xs ? sc * xs[m] : sc);
+        const float o = c[v] * (xscaled ? sc * sc_m[b][v] : sc);
         sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
       }
     }
@@ -378,6 +431,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n16 = lane & 15, g = lane >> 4;
   const int n0 = sr.group * ROWS;
+  uint32_t sc_n[NT];
+  float sc_m[MB][4];
+  lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, n0, N, M, sr, skind, XF8 ? sg.xs : nullptr);
   const uint8_t* gw[LW];  // this wave loads rows wave + 4 j of every stage
 #pragma unroll
   for (int j = 0; j < LW; ++j) {
@@ -492,7 +548,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       }
     }
   }
-  lds_reduce_store<NT, MB>(acc, smem, wave, lane, n0, N, M, sr, skind, XF8 ? sg.xs : nullptr,
+  lds_reduce_store<NT, MB>(acc, smem, wave, lane, n0, N, M, sr, skind, sc_n, sc_m, XF8,
                            std::is_same<TO, BF16>::value);
 }
 

@@ -18,7 +18,8 @@ average launch duration is measured with HIP events on the launch stream
 around the same graph replay; it feeds roofline.achieved.
 
 Further legs (same JSON line): "gemm" (a8w8 at M = 2048,
-three projections), "decoder_layer" (config 5, one graph-replayed step),
+three projections), "gemm_pert" (the reference's esimd_gemm_fp8_pert, w8a16,
+same shapes), "decoder_layer" (config 5, one graph-replayed step),
 "gemv_shapes" (config 2, every M x shape), "norm_quant_gemv" (config 3,
 fused add+RMSNorm+quant then the fp8 GEMV/GEMM to N = 6144), and the device
 copy rate the headline is also quoted against (roofline.copy_GBps).
@@ -42,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, spec
 FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA, spec
+FP16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 MFMA, spec
 ROTATE_BYTES = 2.2e9
 WARM_S = 1.0                   # graph replays before each headline timing (clock settling)
 
@@ -283,6 +285,35 @@ def bench_gemm_all(ops, torch, steps, warmup):
     return head
 
 
+def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
+    """The reference's prefill op esimd_gemm_fp8_pert (fp16 activations, e4m3
+    weights, fp32 per-tensor scale; the w8a16 fp16-MFMA path) at the three
+    config-4 projections, timed like the a8w8 leg; rate against the 2.5
+    PFLOP/s dense fp16 MFMA peak."""
+    from esimd_learning_amd import synthetic
+    dev = "cuda:0"
+    stream = torch.cuda.Stream()
+    rows = []
+    for K, N in ((4096, 6144), (4096, 28672), (14336, 4096)):
+        x = synthetic.activations(M, K, seed=2).to(dev)
+        W8, _ = synthetic.weight_fp8(N, K, seed=3)
+        Wd = W8.to(dev)
+        sv = torch.tensor(0.01, dtype=torch.float32, device=dev)
+        y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        fn = lambda: ops.esimd_gemm_fp8_pert(x, Wd, sv, y)  # noqa: E731
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                fn()
+        torch.cuda.synchronize()
+        _, ev_ms, _ = time_graph([fn] * steps, torch, stream, warm_s=WARM_S / 2)
+        us = ev_ms * 1e3 / steps
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        rows.append({"config": f"w8a16 M={M} K={K} N={N}", "avg_launch_us": round(us, 2), "tflops": round(tf, 1),
+                     "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+        del x, Wd, y
+    return rows
+
+
 def bench_layer(torch, steps, M=4, act_fp8=False):
     """one Gemma-style decoder-layer decode step, HIP-graph replayed
     (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations)."""
@@ -441,6 +472,9 @@ def main():
     if not a.no_gemm:
         out["gemm"] = bench_gemm_all(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")
+        out["gemm_pert"] = bench_gemm_pert(ops, torch, max(10, a.steps // 40), max(3, a.warmup // 10))
+        log("gemm pert (w8a16): " + ", ".join(f"{r['config']}={r['avg_launch_us']}us/{r['tflops']}TF"
+                                              for r in out["gemm_pert"]))
     if not a.no_layer:
         out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))
         log(f"layer: {out['decoder_layer']['us_per_step']} us/step, {out['decoder_layer']['weight_GBps']} GB/s")

@@ -506,6 +506,24 @@ __device__ inline void w8a16_issue(uint8_t* smem, int stage, int kb, int wave,
 #endif
 }
 
+// Same loads from 32-bit byte offsets off the matrix bases (one VGPR per
+// load instead of a 64-bit pointer; the caller checks that both matrices
+// are below 4 GB).
+template <int BM, int BN, int ACH, int BCH, int STRIDE>
+__device__ inline void w8a16_issue_off(uint8_t* smem, int stage, int kb, int wave, const uint8_t* Xb, const uint8_t* W,
+                                       const uint32_t (&oa)[ACH], const uint32_t (&ob)[BCH]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint8_t* sA = smem + stage * (BM * 128 + BN * 64);
+  uint8_t* sB = sA + BM * 128;
+#pragma unroll
+  for (int i = 0; i < ACH; ++i)
+    __builtin_amdgcn_global_load_lds(Xb + (oa[i] + 2u * (uint32_t)kb), (lds_ptr_t)(sA + (wave + STRIDE * i) * 1024), 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < BCH; ++i)
+    __builtin_amdgcn_global_load_lds(W + (ob[i] + (uint32_t)kb), (lds_ptr_t)(sB + (wave + STRIDE * i) * 1024), 16, 0, 0);
+#endif
+}
+
 template <typename T, int FMT, int BM, int BN, int OCC, int WM = 2, int WN = 2>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
@@ -583,20 +601,22 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
 // of work of gemm_a8w8_pipe_kernel.  A wave's K step (64 values) is FM groups
 // of FN MFMA block updates (two 16 x 16 x 32 MFMAs each); group i + 1's A
 // fragment is read while group i's MFMAs run, and the step's one barrier
-// sits before the last group, after which the wave issues the loads of step
-// k + 2 into the stage step k used and reads and decodes step k + 1's B
-// fragments and first A fragment behind the last group's MFMAs.
+// sits before the last group, after which the loader waves (the first LW)
+// issue the loads of step k + 2 into the stage step k used and every wave
+// reads and decodes step k + 1's B fragments and first A fragment behind the
+// last group's MFMAs.  Loader waves as in gemm_a8w8_pipe_kernel.
 // Requires K % 64 == 0, FM even, 16-byte aligned X and W.
 // ---------------------------------------------------------------------------
-template <typename T, int FMT, int BM, int BN, int WM, int WN>
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int LW>
 struct W8Pipe {
   static constexpr int BK = 64;
   static constexpr int NW = WM * WN;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 16, FN = TN / 16;
   static constexpr int STAGE = BM * 128 + BN * 64;
-  static constexpr int ACH = BM / 8 / NW, BCH = BN / 16 / NW;
-  static_assert(ACH * 8 * NW == BM && BCH * 16 * NW == BN, "writer chunks");
+  static constexpr int ACH = BM / 8 / LW, BCH = BN / 16 / LW;  // 1 KB loads per loader wave and stage
+  static_assert(LW >= 1 && LW <= NW, "loader waves");
+  static_assert(ACH * 8 * LW == BM && BCH * 16 * LW == BN, "writer chunks");
   static_assert(FM % 2 == 0, "A fragments alternate between two register sets");
 
   // A fragment (rows r16 of a 16-row block, K values 16 g .. 16 g + 15)
@@ -610,9 +630,9 @@ struct W8Pipe {
     for (int j = 0; j < FN; ++j) decode16<T, FMT>(*reinterpret_cast<const u4*>(sB + j * 16 * 64 + pb * 16), b[j][0], b[j][1]);
   }
 
-  __device__ static __forceinline__ void step(int kt, int KT, uint8_t* smem, int wave, int wm, int wn, int r16,
-                                              int pa0, int pa1, int pb, const uint8_t* const (&ga)[ACH],
-                                              const uint8_t* const (&gb)[BCH], f4 (&acc)[FM][FN], u4 (&a)[2][2],
+  __device__ static __forceinline__ void step(int kt, int KT, uint8_t* smem, bool loader, int wave, int wm, int wn, int r16,
+                                              int pa0, int pa1, int pb, const uint8_t* Xb, const uint8_t* W,
+                                              const uint32_t (&ga)[ACH], const uint32_t (&gb)[BCH], f4 (&acc)[FM][FN], u4 (&a)[2][2],
                                               const u4 (&bc)[FN][2], u4 (&bn)[FN][2]) {
     const uint8_t* sA = smem + (kt & 1) * STAGE + (wm * TM + r16) * 128;
 #pragma unroll
@@ -621,7 +641,7 @@ struct W8Pipe {
         read_a(sA + (i + 1) * 16 * 128, pa0, pa1, a[(i + 1) & 1]);
       } else if (kt + 1 < KT) {
         barrier_vmcnt<0>();  // step k + 1 has landed; step k's stage is free
-        if (kt + 2 < KT) w8a16_issue<BM, BN, ACH, BCH, NW>(smem, kt & 1, (kt + 2) * BK, wave, ga, gb);
+        if (loader && kt + 2 < KT) w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, kt & 1, (kt + 2) * BK, wave, Xb, W, ga, gb);
         const uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
         read_b(nxt + BM * 128 + (wn * TN + r16) * 64, pb, bn);
         read_a(nxt + (wm * TM + r16) * 128, pa0, pa1, a[0]);
@@ -636,35 +656,36 @@ struct W8Pipe {
   }
 };
 
-template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN>
+template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN, int LW>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
     uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
-  using P = W8Pipe<T, FMT, BM, BN, WM, WN>;
+  using P = W8Pipe<T, FMT, BM, BN, WM, WN, LW>;
   constexpr int BK = P::BK, NW = P::NW, TM = P::TM, TN = P::TN, FM = P::FM, FN = P::FN, STAGE = P::STAGE;
   constexpr int ACH = P::ACH, BCH = P::BCH;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  const bool loader = wave < LW;
   int tm, tn;
   tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const uint8_t* Xb = reinterpret_cast<const uint8_t*>(X);
 
-  // A writer chunk j: lane i -> row 8 j + (i >> 3), position i & 7
-  // B writer chunk j: lane i -> row 16 j + (i >> 2), position i & 3
-  const uint8_t* ga[ACH];
-  const uint8_t* gb[BCH];
+  // A writer chunk j = wave + LW i: lane l -> row 8 j + (l >> 3), position l & 7
+  // B writer chunk j = wave + LW i: lane l -> row 16 j + (l >> 2), position l & 3
+  // (non-loaders set up clamped pointers they never use)
+  uint32_t ga[ACH], gb[BCH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
-    const int row = (wave + NW * i) * 8 + (lane >> 3);
-    ga[i] = Xb + ((size_t)min(m0 + row, M - 1) * K) * 2 + ((lane & 7) ^ swzA(row)) * 16;
+    const int row = (wave + LW * i) * 8 + (lane >> 3);
+    ga[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ swzA(row)) * 16);
   }
 #pragma unroll
   for (int i = 0; i < BCH; ++i) {
-    const int row = (wave + NW * i) * 16 + (lane >> 2);
-    gb[i] = W + (size_t)min(n0 + row, N - 1) * K + ((lane & 3) ^ swzB(row)) * 16;
+    const int row = (wave + LW * i) * 16 + (lane >> 2);
+    gb[i] = (uint32_t)min(n0 + row, N - 1) * (uint32_t)K + (uint32_t)(((lane & 3) ^ swzB(row)) * 16);
   }
   const int r16 = lane & 15, g = lane >> 4;
   const int pa0 = (2 * g) ^ swzA(r16), pa1 = (2 * g + 1) ^ swzA(r16), pb = g ^ swzB(r16);
@@ -676,9 +697,11 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
-  w8a16_issue<BM, BN, ACH, BCH, NW>(smem, 0, 0, wave, ga, gb);
+  if (loader) {
+    w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, 0, 0, wave, Xb, W, ga, gb);
+    if (KT > 1) w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, 1, BK, wave, Xb, W, ga, gb);
+  }
   if (KT > 1) {
-    w8a16_issue<BM, BN, ACH, BCH, NW>(smem, 1, BK, wave, ga, gb);
     barrier_vmcnt<ACH + BCH>();
   } else {
     barrier_vmcnt<0>();
@@ -688,10 +711,10 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
   P::read_a(smem + (wm * TM + r16) * 128, pa0, pa1, a[0]);
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    P::step(kt, KT, smem, wave, wm, wn, r16, pa0, pa1, pb, ga, gb, acc, a, b0, b1);
-    P::step(kt + 1, KT, smem, wave, wm, wn, r16, pa0, pa1, pb, ga, gb, acc, a, b1, b0);
+    P::step(kt, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0, b1);
+    P::step(kt + 1, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b1, b0);
   }
-  if (kt < KT) P::step(kt, KT, smem, wave, wm, wn, r16, pa0, pa1, pb, ga, gb, acc, a, b0, b1);
+  if (kt < KT) P::step(kt, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0, b1);
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
   store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, *scale, Y);
@@ -821,6 +844,9 @@ __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
 
 using namespace cek;
 
+#ifndef CEK_W8A16_LW
+#define CEK_W8A16_LW 4
+#endif
 #ifndef CEK_A8W8_LAYOUT
 #define CEK_A8W8_LAYOUT 1
 #endif
@@ -867,7 +893,9 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
       // useful share of the tile area the rounds could cover
       return rate * (double)(M * N) / ((double)(rounds * slots) * bm * bn);
     };
-    const bool big = score(256, 256, 1300, 256) > score(128, 128, 1150, 512);
+    // the pipelined kernel addresses X and W by 32-bit byte offsets
+    const bool off32 = (uint64_t)M * (uint64_t)K * 2 < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
+    const bool big = off32 && score(256, 256, 1400, 256) > score(128, 128, 1150, 512);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     uint16_t* yp = static_cast<uint16_t*>(y);
@@ -880,7 +908,7 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
 #define CEK_W8A16_PIPE(TY, F, BM, BN, OCC, WM, WN)                                                                 \
   do {                                                                                                         \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                    \
-    gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN>                                                         \
+    gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN, CEK_W8A16_LW>                                                         \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn);              \
   } while (0)
 #define CEK_W8A16(TY, F)                                     \

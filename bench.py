@@ -23,6 +23,9 @@ same shapes), "decoder_layer" (config 5, one graph-replayed step),
 "gemv_shapes" (config 2, every M x shape), "norm_quant_gemv" (config 3,
 fused add+RMSNorm+quant then the fp8 GEMV/GEMM to N = 6144), and the device
 copy rate the headline is also quoted against (roofline.copy_GBps).
+roofline.read_ceiling_us is cek_hbm_read_probe (a read-only kernel) over
+the same rotating weight copies, timed the same way: the practical ceiling
+of one pass over those bytes on this GPU, beside the 8 TB/s spec peak.
 
 cpu_baseline: the reference's torch CPU path restated in oracle/
 ((x.float() @ W8.to(fp16).float().T) * s) on this host's cores, timed on the
@@ -142,6 +145,17 @@ def bench_gemv(ops, torch, steps, warmup, M=1, K=4096, N=14336):
     per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
     res["eager_event_us"] = {"p10": round(per[len(per) // 10], 2), "median": round(per[len(per) // 2], 2),
                              "p90": round(per[(9 * len(per)) // 10], 2)}
+    # One-pass read ceiling: cek_hbm_read_probe over the same rotating weight
+    # copies, timed the same way (graph of K launches, warmed).
+    from esimd_learning_amd import cabi
+    lib = cabi.load()
+
+    def probe(i):  # timed mode (no sink)
+        return lambda: cabi.check(lib.cek_hbm_read_probe(Ws[i % copies].data_ptr(), N * K, None,
+                                                         cabi.stream_ptr(stream)))
+
+    _, pev_ms, _ = time_graph([probe(i) for i in range(steps)], torch, stream, warm_s=WARM_S)
+    res["read_ceiling_us"] = pev_ms * 1e3 / steps
     # correctness spot check against the first copy (cheap, CPU oracle at M=1)
     return res, (x, Wd, s, y)
 
@@ -426,6 +440,7 @@ def main():
         del src, dst
 
     g, (x, Wd, s, y) = bench_gemv(ops, torch, a.steps, a.warmup)
+    log(f"gemv: read ceiling (one pass over the same weight bytes) {g['read_ceiling_us']:.2f} us")
     log(f"gemv: {g['avg_launch_us']:.2f} us/launch, {g['achieved']:.0f} GB/s; eager event median "
         f"{g['eager_event_us']['median']:.2f} us; wall {g['ms_per_step'] * 1e3:.2f} us/step")
     # spot check of the measured output
@@ -456,7 +471,12 @@ def main():
                      "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic("gemv_dot_kernel_m1_k4096_n14336"),
                      "algorithmic_bytes": g["bytes"], "avg_launch_us": round(g["avg_launch_us"], 3),
-                     "eager_event_us": g["eager_event_us"]},
+                     "eager_event_us": g["eager_event_us"],
+                     # the same weight bytes read once by cek_hbm_read_probe (no arithmetic):
+                     # the practical one-pass ceiling at this size
+                     "read_ceiling_us": round(g["read_ceiling_us"], 3),
+                     "read_ceiling_GBps": round(4096 * 14336 / (g["read_ceiling_us"] * 1e-6) / 1e9, 1),
+                     "frac_of_read_ceiling": round(g["read_ceiling_us"] / g["avg_launch_us"], 4)},
     }
     out["roofline"]["launch_floor_us"] = round(launch_floor_us(torch), 2)
     if not a.copy_ref:  # (counter runs keep the copy kernels to the reference copies)

@@ -39,7 +39,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
-CABI_SOURCES = ["cek_api.cpp", "cek_gemv.hip", "cek_norm.hip", "cek_act.hip", "cek_gemm.hip"]
+CABI_SOURCES = ["cek_api.cpp", "cek_gemv.hip", "cek_norm.hip", "cek_act.hip", "cek_gemm.hip", "cek_probe.hip"]
 
 
 def _run(cmd):

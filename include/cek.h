@@ -152,6 +152,17 @@ int cek_qk_norm_rope(void* q, void* k, const void* qw, const void* kw, const int
                      int64_t q_stride, int64_t k_stride, float eps, float theta,
                      int is_neox, int io_dtype, void* stream);
 
+/*
+ * Measurement utility, no counterpart in the reference: reads `bytes` bytes
+ * of buf (16-byte aligned, bytes % 16 == 0) once with 16-byte non-temporal
+ * loads.  With sink != NULL it writes the XOR of each of its 1024
+ * workgroups' 32-bit words into sink[0 .. 1023] (so the XOR of the sink
+ * words is the XOR of the buffer's words); with sink == NULL it only reads
+ * (the timed mode).  Its duration is the practical ceiling of one pass over
+ * the same bytes, which the benchmark quotes the HBM-bound kernels against.
+ */
+int cek_hbm_read_probe(const void* buf, int64_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,9 @@ def test_host_rejects_invalid_arguments():
     assert lib.cek_gelu_and_mul(p, p, 4, 64, 100, 64, 0, None) == E                  # x stride < 2d
     assert lib.cek_qk_norm_rope(p, p, p, p, p, 4, 2, 2, 1024, 2048, 2048, 1e-6, 1e4, 1, 0, None) == E
     assert lib.cek_qk_norm_rope(p, p, p, p, p, 4, 2, 2, 128, 100, 256, 1e-6, 1e4, 1, 0, None) == E
+    assert lib.cek_hbm_read_probe(p, 1000, p, None) == E                               # bytes % 16
+    assert lib.cek_hbm_read_probe(C.c_void_p(8), 1024, p, None) == E                   # alignment
+    assert lib.cek_hbm_read_probe(p, 0, p, None) == E
     # multi-matrix GEMV: count out of range, null tables
     P3 = C.c_void_p * 3
     Ns = (C.c_int64 * 3)(8, 8, 8)
@@ -160,3 +163,25 @@ def test_cabi_multi_gemv_matches_single(ops, dev):
                                              cabi.CEK_F16, cabi.CEK_E4M3, cabi.CEK_F32, cabi.stream_ptr()))
             torch.cuda.synchronize()
             assert torch.equal(y, y1), f"M={M} N={n}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nbytes", [16, 4096, 1 << 20, 58720256 + 48])
+def test_cabi_read_probe_reads_every_byte_once(dev, nbytes):
+    """The XOR of the probe's 1024 workgroup words equals the XOR of the
+    buffer's 32-bit words: every 16-byte unit is read exactly once (a unit
+    read twice or skipped changes the XOR for random data)."""
+    import numpy as np
+    lib = cabi.load()
+    g = torch.Generator().manual_seed(nbytes)
+    buf = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=g)
+    sink = torch.full((1024,), 0x5A5A5A5A, dtype=torch.int32, device=dev)
+    bd = buf.to(dev)
+    cabi.check(lib.cek_hbm_read_probe(cabi.ptr(bd), nbytes, cabi.ptr(sink), cabi.stream_ptr()))
+    torch.cuda.synchronize()
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    want = np.bitwise_xor.reduce(buf.numpy().view(np.uint32))
+    assert got == want
+    # the timed mode (no sink) runs the same loads and writes nothing
+    cabi.check(lib.cek_hbm_read_probe(cabi.ptr(bd), nbytes, None, cabi.stream_ptr()))
+    torch.cuda.synchronize()

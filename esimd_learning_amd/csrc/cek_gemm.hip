@@ -165,7 +165,8 @@ __device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
 template <typename T, int BM, int BN, int WM, int WN, int NT = 256, bool SL = false>
 __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], uint8_t* smem, int wm, int wn,
                                   int lane, int m0, int n0, int M, int N, const float* rs, const float* cs,
-                                  float s0, uint16_t* Y) {
+                                  float s0, uint16_t* Y, int mlo = 0,
+                                  int nlo = 0) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
   constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
   static_assert(CPR % 8 == 0, "the chunk swizzle stays inside aligned groups of 8");
@@ -202,15 +203,15 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
   for (int q = threadIdx.x; q < BM * CPR; q += NT) {
     const int r = q / CPR, k = q % CPR;
     const int m = m0 + r, n = n0 + 8 * k;
-    if (m >= M || n >= N) continue;
+    if (m >= M || n >= N || m < mlo) continue;
     const uint8_t* src = smem + r * (BN * 2) + (k ^ (2 * ((r >> 2) & 3))) * 16;
     uint16_t* dst = Y + (size_t)m * N + n;
-    if (vec) {
+    if (vec && n >= nlo) {
       __builtin_nontemporal_store(*reinterpret_cast<const u4*>(src), reinterpret_cast<u4*>(dst));
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (n + e < N) dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
+        if (n + e < N && n + e >= nlo) dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
     }
   }
 }
@@ -306,7 +307,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_lds_kernel(
 // The barrier orders, for all waves: step k + 1's rows have landed (the
 // loaders' only outstanding loads), every read of step k's slots is done
 // (lgkmcnt(0)), so they may be overwritten.
-// Requires K % 128 == 0, FM even, 16-byte aligned A and B.
+// Requires K % 128 == 0, FM even, M >= BM, N >= BN, 16-byte aligned A and B,
+// each below 4 GB.
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN>
 struct PipeCfg {
@@ -346,11 +348,24 @@ __device__ inline void a8w8_issue_rows(uint8_t* slot, int kb, int w, const uint8
 #endif
 }
 
+// The same from one 32-bit byte offset off a matrix base: chunk i's rows are
+// STRIDE * 8 rows (a uniform byte stride) after chunk 0's, so a lane keeps
+// one VGPR for all of its loads (the caller checks that the matrix is below
+// 4 GB and that every addressed row exists).
+template <int CH, int STRIDE>
+__device__ inline void a8w8_issue_off(uint8_t* slot, int kb, int w, const uint8_t* base, int K, uint32_t off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int i = 0; i < CH; ++i)
+    __builtin_amdgcn_global_load_lds(base + (size_t)i * STRIDE * 8 * K + (off + (uint32_t)kb),
+                                     (lds_ptr_t)(slot + (w + STRIDE * i) * 1024), 16, 0, 0);
+#endif
+}
+
 template <int BM, int BN, int WM, int WN, int LW>
 __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uint8_t* sBr, bool loader, int wave,
-                                               int wm, int wn, int r16, int p0, int p1,
-                                               const uint8_t* const (&ga)[LoadSplit<BM, BN, LW>::AL],
-                                               const uint8_t* const (&gb)[LoadSplit<BM, BN, LW>::BL],
+                                               int wm, int wn, int r16, int p0, int p1, const uint8_t* A, const uint8_t* B,
+                                               int K, uint32_t ga, uint32_t gb,
                                                f4 (&acc)[PipeCfg<BM, BN, WM, WN>::FM][PipeCfg<BM, BN, WM, WN>::FN],
                                                i8 (&a)[2], const i8 (&bc)[PipeCfg<BM, BN, WM, WN>::FN],
                                                i8 (&bn)[PipeCfg<BM, BN, WM, WN>::FN]) {
@@ -366,8 +381,8 @@ __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uin
     } else if (kt + 1 < KT) {
       barrier_vmcnt<0>();
       if (loader && kt + 2 < KT) {
-        a8w8_issue_rows<L::BL, LW>(sBr + c * C::BSLOT, (kt + 2) * BK, wave, gb);
-        a8w8_issue_rows<L::AL, LW>(sAr + c * C::ASLOT, (kt + 2) * BK, wave, ga);
+        a8w8_issue_off<L::BL, LW>(sBr + c * C::BSLOT, (kt + 2) * BK, wave, B, K, gb);
+        a8w8_issue_off<L::AL, LW>(sAr + c * C::ASLOT, (kt + 2) * BK, wave, A, K, ga);
       }
       const uint8_t* nA = sAr + (c ^ 1) * C::ASLOT + (wm * TM + r16) * BK;
       const uint8_t* nB = sBr + (c ^ 1) * C::BSLOT + (wn * TN + r16) * BK;
@@ -406,34 +421,31 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   const bool loader = wave < LW;
   int tm, tn;
   tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  // A last tile that would cross M (N) is moved back to end there (M >= BM,
+  // N >= BN): every row it loads exists, so no load needs a clamp, and it
+  // stores only from its own first row (column) mlo (nlo) on -- the rows
+  // before are the previous tile's, which computes the same values.
+  const int mlo = tm * BM, nlo = tn * BN;
+  const int m0 = min(mlo, M - BM), n0 = min(nlo, N - BN);
   // The epilogue's scales go to LDS first, by 4-byte direct-to-LDS loads
   // (one instruction per wave for 64 of them), so that the prologue's wait
   // covers their latency; register loads mixed with the direct-to-LDS ones
   // would make the compiler drain every load before using them.
   if (64 * wave < BM + BN) {
     const int t = min(64 * wave + lane, BM + BN - 1);
-    const float* src = t < BM ? sa + min(m0 + t, M - 1) : sb + min(n0 + t - BM, N - 1);
+    const float* src = t < BM ? sa + m0 + t : sb + n0 + t - BM;
 #if defined(__HIP_DEVICE_COMPILE__)
     __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(sc + 64 * wave), 4, 0, 0);
 #endif
   }
 
   // loader chunk j = wave + LW i: lane l fills row 8 j + (l >> 3), position
-  // l & 7, i.e. logical chunk (l & 7) ^ s(row).  Non-loaders set up the same
-  // pointers (clamped, never used).
-  const uint8_t* ga[AL];
-  const uint8_t* gb[BL];
-#pragma unroll
-  for (int i = 0; i < AL; ++i) {
-    const int row = (wave + LW * i) * 8 + (lane >> 3);
-    ga[i] = A + (size_t)min(m0 + row, M - 1) * K + ((lane & 7) ^ swz<1>(row)) * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < BL; ++i) {
-    const int row = (wave + LW * i) * 8 + (lane >> 3);
-    gb[i] = B + (size_t)min(n0 + row, N - 1) * K + ((lane & 7) ^ swz<1>(row)) * 16;
-  }
+  // l & 7, i.e. logical chunk (l & 7) ^ s(row) (s(row) = row & 7 = (l >> 3)
+  // & 7 for every chunk).  Byte offsets into A and B of this lane's chunk 0
+  // rows; chunk i is LW * 8 rows further (a uniform stride).
+  const uint32_t cofs = (uint32_t)(((lane & 7) ^ swz<1>(lane >> 3)) * 16);
+  const uint32_t ga = (uint32_t)(m0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs;
+  const uint32_t gb = (uint32_t)(n0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs;
   const int r16 = lane & 15, g = lane >> 4;
   const int p0 = g ^ swz<1>(r16), p1 = (g + 4) ^ swz<1>(r16);
 
@@ -447,11 +459,11 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   // Prologue: steps 0 and 1, then wait for step 0 (a loader's step 1 loads,
   // issued last, may fly; a non-loader has at most its older scale load out).
   if (loader) {
-    a8w8_issue_rows<BL, LW>(sBr, 0, wave, gb);
-    a8w8_issue_rows<AL, LW>(sAr, 0, wave, ga);
+    a8w8_issue_off<BL, LW>(sBr, 0, wave, B, K, gb);
+    a8w8_issue_off<AL, LW>(sAr, 0, wave, A, K, ga);
     if (KT > 1) {
-      a8w8_issue_rows<BL, LW>(sBr + C::BSLOT, BK, wave, gb);
-      a8w8_issue_rows<AL, LW>(sAr + C::ASLOT, BK, wave, ga);
+      a8w8_issue_off<BL, LW>(sBr + C::BSLOT, BK, wave, B, K, gb);
+      a8w8_issue_off<AL, LW>(sAr + C::ASLOT, BK, wave, A, K, ga);
     }
   }
   if (KT > 1) barrier_vmcnt<AL + BL>();
@@ -466,16 +478,16 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   }
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b0, b1);
-    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt + 1, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b1, b0);
+    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt + 1, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b1, b0);
   }
   if (kt < KT)
-    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b0, b1);
   // every wave's loads (a non-loader's scale load included) are complete
   // here: each step's barrier waited for vmcnt(0), and with KT == 1 the
   // prologue's did
   static_assert(SMEM >= BM * BN * 2, "output tile must fit");
-  store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y);
+  store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y, mlo, nlo);
 }
 
 // ---------------------------------------------------------------------------
@@ -957,18 +969,19 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     // (MI355X, BASELINE prefill shapes, TFLOP/s) times the useful share of
     // the tile area its rounds of workgroups cover (256 CUs; the 8-wave tiles
     // fit one workgroup per CU, the 4-wave ones two), best score wins:
-    //  * 256 x 256, 8 waves (4 x 2, wave tile 64 x 128, two waves per SIMD):
-    //    the least LDS traffic per MFMA;
-    //  * 256 x 192, 8 waves (2 x 4), register-pipelined fragment reads and
-    //    four loader waves (gemm_a8w8_pipe_kernel; 8-15% faster than the same
-    //    tile in gemm_a8w8_lds_kernel on every config-4 shape);
+    //  * 256 x 256, 8 waves (2 x 4, wave tile 128 x 64, two waves per SIMD,
+    //    four loader waves): the least load and LDS traffic per MFMA;
+    //  * 256 x 192, 8 waves (2 x 4, four loader waves);
     //  * 128 x 128, 4 waves, two workgroups per CU so that one's MFMAs cover
     //    the other's LDS reads and barrier waits;
     //  * 64 x 128 for few, small tiles.
-    // This picks the fastest measured configuration, or one within 3% of it,
-    // on all nine config-4 shapes.
+    // All four run gemm_a8w8_pipe_kernel (register-pipelined fragment reads,
+    // single-offset addressing) when the matrices are below 4 GB and at
+    // least one tile in each dimension; otherwise gemm_a8w8_lds_kernel with
+    // the same tile (its loads clamp rows).  This picks the fastest measured
+    // configuration, or one within 2% of it, on all nine config-4 shapes.
     struct Opt { int bm, bn; double rate; int slots; };
-    constexpr Opt opts[4] = {{64, 128, 1750, 512}, {128, 128, 2250, 512}, {256, 192, 2400, 256}, {256, 256, 2450, 256}};
+    constexpr Opt opts[4] = {{64, 128, 1750, 512}, {128, 128, 2250, 512}, {256, 192, 2480, 256}, {256, 256, 2650, 256}};
     int cfg = 0;
     double best = -1.0;
     for (int c = 0; c < 4; ++c) {
@@ -978,6 +991,8 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
       const double score = opts[c].rate * (double)(M * N) / ((double)(rounds * opts[c].slots) * opts[c].bm * opts[c].bn);
       if (score > best) { best = score; cfg = c; }
     }
+    const bool off32 = (uint64_t)M * (uint64_t)K < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
+    const bool pipe = off32 && M >= opts[cfg].bm && N >= opts[cfg].bn;
 #define CEK_A8W8(TY, BM, BN, WM, WN, OCC)                                                               \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
@@ -990,19 +1005,27 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW>                                                \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
-    if (out_dtype == CEK_F16) {
-      if (cfg == 3) CEK_A8W8(F16, 256, 256, 4, 2, 1);
-      else if (cfg == 2) CEK_A8W8_PIPE(F16, 256, 192, 2, 4, 1, 4);
-      else if (cfg == 1) CEK_A8W8(F16, 128, 128, 2, 2, 2);
-      else CEK_A8W8(F16, 64, 128, 2, 2, 2);
-    } else {
-      if (cfg == 3) CEK_A8W8(BF16, 256, 256, 4, 2, 1);
-      else if (cfg == 2) CEK_A8W8_PIPE(BF16, 256, 192, 2, 4, 1, 4);
-      else if (cfg == 1) CEK_A8W8(BF16, 128, 128, 2, 2, 2);
-      else CEK_A8W8(BF16, 64, 128, 2, 2, 2);
-    }
+#define CEK_A8W8_ALL(TY)                                                               \
+  do {                                                                                 \
+    if (cfg == 3) {                                                                    \
+      if (pipe) CEK_A8W8_PIPE(TY, 256, 256, 2, 4, 1, 4);                               \
+      else CEK_A8W8(TY, 256, 256, 4, 2, 1);                                            \
+    } else if (cfg == 2) {                                                             \
+      if (pipe) CEK_A8W8_PIPE(TY, 256, 192, 2, 4, 1, 4);                               \
+      else CEK_A8W8(TY, 256, 192, 2, 4, 1);                                            \
+    } else if (cfg == 1) {                                                             \
+      if (pipe) CEK_A8W8_PIPE(TY, 128, 128, 2, 2, 2, 4);                               \
+      else CEK_A8W8(TY, 128, 128, 2, 2, 2);                                            \
+    } else {                                                                           \
+      if (pipe) CEK_A8W8_PIPE(TY, 64, 128, 2, 2, 2, 2);                                \
+      else CEK_A8W8(TY, 64, 128, 2, 2, 2);                                             \
+    }                                                                                  \
+  } while (0)
+    if (out_dtype == CEK_F16) CEK_A8W8_ALL(F16);
+    else CEK_A8W8_ALL(BF16);
 #undef CEK_A8W8
 #undef CEK_A8W8_PIPE
+#undef CEK_A8W8_ALL
     return check_launch();
   }
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));

@@ -125,12 +125,16 @@ def test_a8w8_decode_rows(ops, dev, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(4096, 1024, 8192), (4000, 512, 8150), (2000, 1024, 6100), (2048, 512, 6144),
-                                   (2048, 640, 6144), (2048, 128, 6144), (2040, 384, 6100)])
+                                   (2048, 640, 6144), (2048, 128, 6144), (2040, 384, 6100), (520, 1024, 28800),
+                                   (4100, 512, 6150), (100, 256, 3000), (200, 512, 100), (70, 384, 130)])
 def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
-    """The 256 x 256 and 256 x 192 tile configurations (8 waves), including
-    ragged M and N, against a float32 torch GPU matmul of the dequantised codes.
-    The 256 x 192 shapes run the register-pipelined kernel; K = 640 and 128
-    give it an odd number of K steps and a single one."""
+    """The tile configurations (256 x 256, 256 x 192, 128 x 128, 64 x 128),
+    including ragged M and N, against a float32 torch GPU matmul of the
+    dequantised codes.  The register-pipelined kernel moves a last tile that
+    would cross M or N back onto the previous one and stores only its own
+    rows and columns (ragged shapes here); N < 128 (200 x 100) takes the
+    clamping LDS kernel.  K = 640 and 128 give an odd number of K steps and a
+    single one."""
     _say(f"a8w8 large tiles M={M} K={K} N={N}")
     q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M + N)
     qd, Wd = q.to(dev), W8.to(dev)

@@ -893,12 +893,11 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   if (K % 64 != 0 || !aligned(x, 16) || !aligned(w, 16) || M > 65535 * 64)
     return launch_gemv_generic(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
   {
-    // Tiles: 128 x 128 with 4 waves and two workgroups per CU, or 256 x 256
-    // with 8 waves (2 x 4, the register-pipelined kernel: 4-9% faster than
-    // the same tile in gemm_w8a16_lds_kernel) where its last round of
-    // workgroups is fuller --
-    // each configuration's measured rate (MI355X, config-4 shapes with fp16
-    // activations) times the fill of its last round over 256 CUs.
+    // Tiles: 128 x 128 with 4 waves and two workgroups per CU, or the
+    // register-pipelined 8-wave kernel (2 x 4 waves, four loader waves) at
+    // 256 x 192 or 256 x 256 -- each configuration's measured rate (MI355X,
+    // config-4 shapes with fp16 activations, TFLOP/s at full occupancy)
+    // times the fill of its last round over 256 CUs, best score wins.
     auto score = [&](int bm, int bn, double rate, int slots) {
       const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
       const int64_t rounds = (tiles + slots - 1) / slots;
@@ -907,7 +906,10 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
     };
     // the pipelined kernel addresses X and W by 32-bit byte offsets
     const bool off32 = (uint64_t)M * (uint64_t)K * 2 < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
-    const bool big = off32 && score(256, 256, 1400, 256) > score(128, 128, 1150, 512);
+    const double s128 = score(128, 128, 1150, 512);
+    const double s192 = off32 ? score(256, 192, 1250, 256) : -1.0;
+    const double s256 = off32 ? score(256, 256, 1400, 256) : -1.0;
+    const int tile = s256 > s192 && s256 > s128 ? 2 : (s192 > s128 ? 1 : 0);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     uint16_t* yp = static_cast<uint16_t*>(y);
@@ -923,10 +925,11 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
     gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN, CEK_W8A16_LW>                                                         \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn);              \
   } while (0)
-#define CEK_W8A16(TY, F)                                     \
-  do {                                                       \
-    if (big) CEK_W8A16_PIPE(TY, F, 256, 256, 1, 2, 4);       \
-    else CEK_W8A16_TILE(TY, F, 128, 128, 2, 2, 2);           \
+#define CEK_W8A16(TY, F)                                          \
+  do {                                                            \
+    if (tile == 2) CEK_W8A16_PIPE(TY, F, 256, 256, 1, 2, 4);      \
+    else if (tile == 1) CEK_W8A16_PIPE(TY, F, 256, 192, 1, 2, 4); \
+    else CEK_W8A16_TILE(TY, F, 128, 128, 2, 2, 2);                \
   } while (0)
     if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_W8A16(F16, CEK_E4M3);
     else if (io_dtype == CEK_F16) CEK_W8A16(F16, CEK_E5M2);

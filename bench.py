@@ -189,8 +189,11 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=5):
 def bench_gemv_table(ops, torch, shapes=((4096, 14336), (4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)),
                      Ms=(1, 2, 4, 8, 16)):
     """every (M, K, N), per-launch time over > 2 GB of
-    rotating weights (graph of two passes over the copies, event-timed)."""
-    from esimd_learning_amd import synthetic
+    rotating weights (graph of two passes over the copies, event-timed), and
+    per shape the one-pass read ceiling of its weight bytes
+    (cek_hbm_read_probe over the same copies, timed the same way)."""
+    from esimd_learning_amd import cabi, synthetic
+    lib = cabi.load()
     dev = "cuda:0"
     stream = torch.cuda.Stream()
     rows = []
@@ -200,6 +203,10 @@ def bench_gemv_table(ops, torch, shapes=((4096, 14336), (4096, 6144), (4096, 409
         Wd = W8.to(dev)
         Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
         sd = s.to(dev)
+        pfns = [(lambda W=W: cabi.check(lib.cek_hbm_read_probe(W.data_ptr(), N * K, None, cabi.stream_ptr(stream))))
+                for W in Ws] * 2
+        _, pev_ms, _ = time_graph(pfns, torch, stream, warm_s=0.1)
+        ceil_us = pev_ms * 1e3 / len(pfns)
         for M in Ms:
             x = synthetic.activations(M, K, seed=1).to(dev)
             y = torch.empty(M, N, dtype=torch.float16, device=dev)
@@ -211,7 +218,8 @@ def bench_gemv_table(ops, torch, shapes=((4096, 14336), (4096, 6144), (4096, 409
             _, ev_ms, _ = time_graph(fns, torch, stream, warm_s=0.1)
             us = ev_ms * 1e3 / len(fns)
             rows.append({"M": M, "K": K, "N": N, "us": round(us, 2),
-                         "GBps": round(gemv_bytes(M, N, K) / (us * 1e-6) / 1e9, 1)})
+                         "GBps": round(gemv_bytes(M, N, K) / (us * 1e-6) / 1e9, 1),
+                         "read_ceiling_us": round(ceil_us, 2), "frac_of_read_ceiling": round(ceil_us / us, 3)})
         del Ws, Wd
         torch.cuda.empty_cache()
     return rows
@@ -354,9 +362,20 @@ def bench_layer(torch, steps, M=4, act_fp8=False):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / steps
     wb = layer.weight_bytes()
+    # the four weight matrices read once each by cek_hbm_read_probe, captured
+    # and replayed the same way: the one-pass read floor of a step's GEMVs
+    from esimd_learning_amd import cabi
+    lib = cabi.load()
+    mats = [layer.Wqkv, layer.Wo, layer.Wgu, layer.Wd]
+    stream = torch.cuda.Stream()
+    pfns = [(lambda w=w: cabi.check(lib.cek_hbm_read_probe(w.data_ptr(), w.numel(), None, cabi.stream_ptr(stream))))
+            for w in mats] * steps
+    _, pev_ms, _ = time_graph(pfns, torch, stream, warm_s=WARM_S / 2)
+    floor_us = pev_ms * 1e3 / steps
     return {"config": "Gemma-style decoder layer decode step, M=4, hidden 3072, 16q/16kv x 256, MLP 24576 "
                       "(attention stood in by a copy of q)",
             "us_per_step": round(us, 2), "weight_bytes": wb, "weight_GBps": round(wb / us / 1e3, 1),
+            "weight_read_floor_us": round(floor_us, 2),
             "timing": f"one HIP graph of the step, replayed {steps} times back to back"}
 
 

@@ -397,6 +397,48 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
 // activation loads, which are therefore not __restrict__) on their side.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// lds_reduce_store for one tile of a multi-tile workgroup: the same
+// cross-wave sum and store, in a reduction area of its own (red, 3 x NT x MB
+// x 64 f4), with LDS-only barriers so that the next tile's loads stay in
+// flight, and no early return.  The leading barrier also orders this tile's
+// reduction writes after wave 0's reads of the previous tile's.
+template <int NT, int MB>
+__device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* redp, int wave, int lane, int n0, int N,
+                                             int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
+                                             const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
+  f4* red = reinterpret_cast<f4*>(redp);  // [3][NT][MB][64]
+  lds_barrier();
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) red[(((wave - 1) * NT + t) * MB + b) * 64 + lane] = acc[t][b];
+  }
+  lds_barrier();
+  if (wave == 0) {
+    const int n16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int n = n0 + t * 16 + n16;  // D column = lane & 15
+      if (n >= N) continue;
+      const float sc = scale_value(sc_n[t], skind);
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        f4 c = acc[t][b];
+#pragma unroll
+        for (int w = 0; w < 3; ++w) c += red[((w * NT + t) * MB + b) * 64 + lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = b * 16 + g * 4 + v;  // D row = 4 * (lane >> 4) + v
+          if (m >= M) continue;
+          const float o = c[v] * (xscaled ? sc * sc_m[b][v] : sc);
+          sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+        }
+      }
+    }
+  }
+}
+
 // One kernel for both activation kinds.  XF8 = false: x is T (fp16/bf16), a
 // lane's 16-byte weight unit (16 K values) is decoded to two 8-value operands
 // of v_mfma_f32_16x16x32_{f16,bf16}.  XF8 = true: x holds e4m3 codes with
@@ -408,9 +450,16 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // ahead into registers (a ring of D + 1 slots, so the loop body is unrolled
 // D + 1 times); stage i is copied into one of two LDS buffers, then read back
 // in MFMA layout.  K = 1024 STEPS.
-template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0>
+//
+// TPW > 1: a workgroup owns TPW consecutive tiles of 16*NT rows and streams
+// them as one run of TPW * STEPS stages; each tile ends with its own
+// cross-wave reduction and store while the next tile's stages are already in
+// flight.  For short K (few stages per tile) this spreads the pipeline fill
+// and the epilogue of a workgroup over several tiles.
+template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M) {
-  static_assert(D >= 1 && D <= STEPS, "prefetch depth");
+  constexpr int NS = STEPS * TPW;  // stages of the workgroup
+  static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 8), "activations go through LDS only for M <= 8");
   constexpr int K = STEPS * 1024;
   constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
@@ -425,21 +474,23 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   constexpr int XU = MX > 0 ? MX * XROW / 16 / 256 : 1;
   constexpr int XSTAGE = MX * XROW;
   static_assert(MX == 0 || XU * 16 * 256 == XSTAGE, "activation units per thread");
-  __shared__ __align__(16) uint8_t smem[2 * (STAGE + XSTAGE)];
+  // two stage buffers, then (TPW > 1) the cross-wave reduction area
+  constexpr int RED = TPW > 1 ? 3 * NT * MB * 64 * 16 : 0;
+  __shared__ __align__(16) uint8_t smem[2 * (STAGE + XSTAGE) + RED];
   const SegRef sr = find_seg(sg, blockIdx.x);
   const int N = sr.n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n16 = lane & 15, g = lane >> 4;
-  const int n0 = sr.group * ROWS;
+  const int nw = sr.group * ROWS * TPW;  // first row of the workgroup
   uint32_t sc_n[NT];
   float sc_m[MB][4];
-  lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, n0, N, M, sr, skind, XF8 ? sg.xs : nullptr);
-  const uint8_t* gw[LW];  // this wave loads rows wave + 4 j of every stage
-#pragma unroll
-  for (int j = 0; j < LW; ++j) {
+  lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 ? sg.xs : nullptr);
+  // this wave loads rows wave + 4 j of every stage of tile t: row
+  // nw + ROWS t + wave + 4 j, clamped (clamped rows are never stored)
+  auto wrow = [&](int t, int j) {
     const int r = wave + 4 * j;
-    gw[j] = sr.w + (size_t)min(n0 + r, N - 1) * K + 16 * (lane ^ (r & 15));  // clamped rows are never stored
-  }
+    return sr.w + (size_t)min(nw + ROWS * t + r, N - 1) * K + 16 * (lane ^ (r & 15));
+  };
   const uint8_t* gx[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b)  // rows >= M are never stored
@@ -461,9 +512,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   u4 wr[S][LW];
   u4 xr[S][MX > 0 ? XU : QN][MX > 0 ? 1 : MB][MX > 0 ? 1 : 2];
   auto issue = [&](int i, u4 (&ws)[LW], u4 (&xs)[MX > 0 ? XU : QN][MX > 0 ? 1 : MB][MX > 0 ? 1 : 2]) {
-    const int k0 = i << 10;
+    const int k0 = (i % STEPS) << 10;
 #pragma unroll
-    for (int j = 0; j < LW; ++j) ws[j] = load_u4_stream(gw[j] + k0);  // 1 KB of one row per instruction
+    for (int j = 0; j < LW; ++j) ws[j] = load_u4_stream(wrow(i / STEPS, j) + k0);  // 1 KB of one row per instruction
     asm volatile("" ::: "memory");  // same issue order in every step (weights, then activations)
     if constexpr (MX > 0) {
 #pragma unroll
@@ -487,14 +538,14 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // Fully unrolled over the STEPS stages (the host instantiates the K values
+  // Fully unrolled over the NS stages (the host instantiates the K values
   // it supports), so every slot index and every condition is static and the
   // compiler's in-order vmcnt waits are exact: the wait for stage i leaves
   // the loads of the stages after it in flight.
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, wr[j], xr[j]);
 #pragma unroll
-  for (int i = 0; i < STEPS; ++i) {
+  for (int i = 0; i < NS; ++i) {
     // Stage i into LDS buffer i & 1 (last read at step i - 2, which every
     // wave finished before the barrier of step i - 1).  Lane l's unit lands
     // at slot l, i.e. unit v of row r at slot v ^ (r & 15).
@@ -507,7 +558,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       for (int j = 0; j < XU; ++j) *reinterpret_cast<u4*>(sx + xdst[j]) = xr[i % S][j][0][0];
     }
     lds_barrier();
-    if (i + D < STEPS) issue(i + D, wr[(i + D) % S], xr[(i + D) % S]);
+    if (i + D < NS) issue(i + D, wr[(i + D) % S], xr[(i + D) % S]);
     const int xrow = min(n16, M - 1);  // MX > 0: this lane's operand row in LDS
     const uint8_t* sxr = sx + xrow * XROW;
 #pragma unroll
@@ -547,9 +598,24 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
         }
       }
     }
+    if constexpr (TPW > 1) {
+      if (i % STEPS == STEPS - 1) {  // tile i / STEPS is complete
+        lds_reduce_store_tile<NT, MB>(acc, smem + 2 * (STAGE + XSTAGE), wave, lane, nw + ROWS * (i / STEPS), N, M,
+                                      sr, skind, sc_n, sc_m, XF8, std::is_same<TO, BF16>::value);
+        if (i + 1 < NS) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
+          lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw + ROWS * (i / STEPS + 1), N, M, sr, skind,
+                                  XF8 ? sg.xs : nullptr);
+        }
+      }
+    }
   }
-  lds_reduce_store<NT, MB>(acc, smem, wave, lane, n0, N, M, sr, skind, sc_n, sc_m, XF8,
-                           std::is_same<TO, BF16>::value);
+  if constexpr (TPW == 1)
+    lds_reduce_store<NT, MB>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m, XF8,
+                             std::is_same<TO, BF16>::value);
 }
 
 // ---------------------------------------------------------------------------
@@ -596,16 +662,34 @@ template <typename T, typename TO, int FMT, bool XF8, int S>
 static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int N, hipStream_t st) {
 #define CEK_LDS(NT, MB, D) \
   gemv_lds_kernel<T, TO, FMT, XF8, NT, MB, D, S><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M)
-#define CEK_LDS_MX(NT, D, MX) \
-  gemv_lds_kernel<T, TO, FMT, XF8, NT, 1, D, S, MX><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M)
+#define CEK_LDS_T(NT, D, MX, TPW)                                                                          \
+  gemv_lds_kernel<T, TO, FMT, XF8, NT, 1, D, S, MX, TPW><<<dim3(seg_grid(sg, 16 * (NT) * (TPW))), 256, 0, st>>>( \
+      x, sg, skind, M)
   constexpr bool SHORT = S >= 3 && S <= 5;
+  constexpr bool MULTI = S == 4 || S == 5;  // multi-tile workgroups (K = 4096, 5120)
+#define CEK_LDS_TPW(NT, D, MX)                       \
+  do {                                               \
+    if constexpr (MULTI) {                           \
+      if (tpw == 4) CEK_LDS_T(NT, D, MX, 4);         \
+      else if (tpw == 2) CEK_LDS_T(NT, D, MX, 2);    \
+      else CEK_LDS_T(NT, D, MX, 1);                  \
+    } else {                                         \
+      CEK_LDS_T(NT, D, MX, 1);                       \
+    }                                                \
+  } while (0)
+  // K = 4096 or 5120 (4-5 stages per 16-row tile): consecutive tiles per
+  // workgroup, as many as keep >= 224 workgroups (measured on MI355X: 4
+  // tiles at N = 14336 and 28672, M = 4: 15.7 -> 13.2 and 25.9 -> 22.7 us;
+  // 2 at N = 6144; one below 384 tiles).  At K = 3072 one tile was fastest.
+  const int tiles = (N + 15) / 16;
+  const int tpw = MULTI ? (tiles >= 896 ? 4 : (tiles >= 384 ? 2 : 1)) : 1;
   if constexpr (!XF8) {
-    // fp16/bf16, M <= 8, up to 12288 rows: activations staged through LDS
-    // (contiguous loads of just the M rows) -- 5-20% faster there, slower
-    // for wider matrices.
-    if (M <= 8 && N <= 12288 && !(SHORT && M >= 8 && N >= 6144)) {
-      if (M <= 4) CEK_LDS_MX(1, (S >= 3 ? 3 : 2), 4);
-      else CEK_LDS_MX(1, 2, 8);
+    // fp16/bf16, M <= 8: activations staged through LDS (contiguous loads
+    // of just the M rows); for long K only up to 12288 rows (5-20% faster
+    // there, slower for wider matrices).
+    if (M <= 8 && (SHORT || N <= 12288)) {
+      if (M <= 4) CEK_LDS_TPW(1, (S >= 3 ? 3 : 2), 4);
+      else CEK_LDS_TPW(1, 2, 8);
       return true;
     }
   }
@@ -614,7 +698,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
       // Two 16-row tiles per workgroup halve the activation re-reads once
       // there are enough rows to keep >= 192 workgroups.
       if (N >= 6144 && (XF8 ? M > 8 : M >= 8)) CEK_LDS(2, 1, 2);
-      else CEK_LDS(1, 1, 3);
+      else CEK_LDS_TPW(1, 3, 0);
     } else if constexpr (XF8 && S >= 3) {
       CEK_LDS(1, 1, 3);
     } else {
@@ -635,7 +719,8 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   }
   return false;
 #undef CEK_LDS
-#undef CEK_LDS_MX
+#undef CEK_LDS_T
+#undef CEK_LDS_TPW
 }
 
 template <typename T, typename TO, int FMT, bool XF8>

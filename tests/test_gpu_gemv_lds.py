@@ -8,7 +8,9 @@ through the public ops:
 * esimd_gemv_fp8_pern / _pert, 3 <= M <= 16, fp16/bf16 x e4m3/e5m2;
 * esimd_gemm_fp8_pert with 16 < M <= 32 (the GEMM entry's skinny route);
 * esimd_gemm_fp8_a8w8 with 3 <= M <= 64 (e4m3 activations and weights);
-* the fused multi-matrix GEMV (segment table), whose segments share a launch.
+* the fused multi-matrix GEMV (segment table), whose segments share a launch;
+* K = 4096 or 5120 with many rows, where a workgroup streams two or four
+  consecutive 16-row tiles (N >= 384 or >= 896 tiles, ragged last workgroup).
 
 N values include ones that are not multiples of the 16- and 32-row tiles.
 Reference: the CPU oracle; tolerance |out - ref| <= 1e-2 max|ref| + 2e-2 |ref|.
@@ -106,3 +108,46 @@ def test_fused_segments_lds(ops, dev):
     torch.cuda.synchronize()
     for w, s, y in zip(Ws, Ss, ys):
         assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, w, s), f"fused N={w.shape[0]}")
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 4096, 14336), (3, 4096, 14350), (8, 4096, 28700), (6, 5120, 14400),
+                                   (4, 3072, 12300), (2, 4096, 14336)])
+def test_gemv_multi_tile(ops, dev, M, K, N):
+    """Workgroups that own 2 or 4 consecutive tiles (the last one partly
+    past N), fp16 and bf16 activations."""
+    _say(f"lds gemv multi-tile M={M} K={K} N={N}")
+    W8, s = synthetic.weight_fp8(N, K, seed=N + K)
+    x = synthetic.activations(M, K, seed=M + 11)
+    for io in (torch.float16, torch.bfloat16):
+        xi = x.to(io)
+        y = torch.zeros(M, N, dtype=io, device=dev)
+        ops.esimd_gemv_fp8_pern(xi.to(dev), W8.to(dev), s.to(dev), y, N, K)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(xi, W8, s), f"multi-tile M={M} K={K} N={N} {io}")
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 4096, 14350), (8, 5120, 7000), (1, 4096, 28672)])
+def test_a8w8_multi_tile(ops, dev, M, K, N):
+    """The a8w8 skinny path with multi-tile workgroups (e4m3 activations)."""
+    _say(f"lds a8w8 multi-tile M={M} K={K} N={N}")
+    x = synthetic.activations(M, K, seed=M + 7)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=K + 9)
+    ref = ogemm.gemm_a8w8(q, sa, W8.view(torch.uint8), sb)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.view(torch.uint8).to(dev), sb.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ref, f"a8w8 multi-tile M={M} K={K} N={N}")
+
+
+def test_fused_segments_multi_tile(ops, dev):
+    """Segments of a launch whose total row count selects 4-tile workgroups."""
+    M, K = 4, 4096
+    x = synthetic.activations(M, K, seed=19)
+    Ns = [9000, 1030, 6150]
+    Ws, Ss = zip(*[synthetic.weight_fp8(n, K, seed=n + 1) for n in Ns])
+    ys = [torch.zeros(M, n, dtype=torch.float16, device=dev) for n in Ns]
+    ops.esimd_gemv_fp8_pern_fused(x.to(dev), [w.to(dev) for w in Ws], [s.to(dev) for s in Ss], ys)
+    torch.cuda.synchronize()
+    for w, s, y in zip(Ws, Ss, ys):
+        assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, w, s), f"fused multi-tile N={w.shape[0]}")

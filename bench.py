@@ -336,14 +336,15 @@ def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
     return rows
 
 
-def bench_layer(torch, steps, M=4, act_fp8=False):
+def bench_layer(torch, steps, M=4, act_fp8=False, fuse_glu=True):
     """one Gemma-style decoder-layer decode step, HIP-graph replayed
-    (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations)."""
+    (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations; fuse_glu: gate/up
+    and gelu_and_mul in one launch)."""
     from esimd_learning_amd import synthetic
     from esimd_learning_amd.layer import GemmaDecodeLayer
     dev = "cuda:0"
     p = synthetic.gemma_layer(seed=10)
-    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse_glu)
     h = synthetic.activations(M, p["hidden"], seed=20).to(dev)
     r = synthetic.activations(M, p["hidden"], seed=21).to(dev)
     pos = synthetic.positions(M, seed=22).to(dev)
@@ -520,6 +521,9 @@ def main():
         fp8 = bench_layer(torch, max(20, a.steps // 4), act_fp8=True)
         out["decoder_layer"]["act_fp8_us_per_step"] = fp8["us_per_step"]
         log(f"layer, e4m3 activation hand-off: {fp8['us_per_step']} us/step")
+        unf = bench_layer(torch, max(20, a.steps // 4), fuse_glu=False)
+        out["decoder_layer"]["unfused_glu_us_per_step"] = unf["us_per_step"]
+        log(f"layer, gate/up GEMV and gelu_and_mul as two launches: {unf['us_per_step']} us/step")
     if not a.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch)

@@ -21,12 +21,6 @@
 
 namespace cek {
 
-__device__ inline float gelu_tanh(float u) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  return 0.5f * u * (1.0f + tanhf(k0 * (u + k1 * u * u * u)));
-}
-
 template <typename T>
 __global__ __launch_bounds__(256) void gelu_and_mul_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, int d, int64_t xs, int64_t os, int vec) {

@@ -40,6 +40,16 @@ struct BF16 {
   __device__ static inline uint16_t from_f32(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 };
 
+// gelu with the tanh approximation, fp32 math:
+// gelu_tanh(u) = 0.5 u (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))).  One
+// definition for gelu_and_mul and the GEMV epilogue that fuses it, so the two
+// paths round identically.
+__device__ inline float gelu_tanh(float u) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  return 0.5f * u * (1.0f + tanhf(k0 * (u + k1 * u * u * u)));
+}
+
 // Decode the two fp8 bytes in the low (HI=false) or high (HI=true) half of
 // `w` into a pair of the activation type; FMT is CEK_E4M3 or CEK_E5M2.
 template <typename T, int FMT, bool HI>

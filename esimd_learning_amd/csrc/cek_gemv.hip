@@ -397,15 +397,17 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
 // activation loads, which are therefore not __restrict__) on their side.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// lds_reduce_store for one tile of a multi-tile workgroup: the same
-// cross-wave sum and store, in a reduction area of its own (red, 3 x NT x MB
-// x 64 f4), with LDS-only barriers so that the next tile's loads stay in
-// flight, and no early return.  The leading barrier also orders this tile's
-// reduction writes after wave 0's reads of the previous tile's.
-template <int NT, int MB>
-__device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* redp, int wave, int lane, int n0, int N,
-                                             int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
-                                             const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
+// The cross-wave sum of one tile of a multi-tile workgroup, in a reduction
+// area of its own (red, 3 x NT x MB x 64 f4), with LDS-only barriers so that
+// the next tile's loads stay in flight, and no early return.  The leading
+// barrier also orders this tile's reduction writes after wave 0's reads of
+// the previous tile's.  Wave 0 then calls emit(t, b, v, o) for every element
+// of its fragments: o = the scaled sum of D row 16 b + 4 (lane >> 4) + v,
+// column 16 t + (lane & 15) of the tile (rows and columns not yet bounded).
+template <int NT, int MB, typename Emit>
+__device__ inline void lds_reduce_tile(const f4 (&acc)[NT][MB], uint8_t* redp, int wave, int lane, int skind,
+                                       const uint32_t (&sc_n)[NT], const float (&sc_m)[MB][4], bool xscaled,
+                                       Emit&& emit) {
   f4* red = reinterpret_cast<f4*>(redp);  // [3][NT][MB][64]
   lds_barrier();
   if (wave > 0) {
@@ -416,11 +418,8 @@ __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* r
   }
   lds_barrier();
   if (wave == 0) {
-    const int n16 = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int n = n0 + t * 16 + n16;  // D column = lane & 15
-      if (n >= N) continue;
       const float sc = scale_value(sc_n[t], skind);
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
@@ -428,15 +427,23 @@ __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* r
 #pragma unroll
         for (int w = 0; w < 3; ++w) c += red[((w * NT + t) * MB + b) * 64 + lane];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = b * 16 + g * 4 + v;  // D row = 4 * (lane >> 4) + v
-          if (m >= M) continue;
-          const float o = c[v] * (xscaled ? sc * sc_m[b][v] : sc);
-          sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
-        }
+        for (int v = 0; v < 4; ++v) emit(t, b, v, c[v] * (xscaled ? sc * sc_m[b][v] : sc));
       }
     }
   }
+}
+
+// lds_reduce_store for one tile of a multi-tile workgroup (n0 = the tile's
+// first row).
+template <int NT, int MB>
+__device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* redp, int wave, int lane, int n0, int N,
+                                             int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
+                                             const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
+  const int n16 = lane & 15, g = lane >> 4;
+  lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, xscaled, [&](int t, int b, int v, float o) {
+    const int n = n0 + t * 16 + n16, m = b * 16 + g * 4 + v;  // D column = lane & 15, row = 4 (lane >> 4) + v
+    if (n < N && m < M) sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+  });
 }
 
 // One kernel for both activation kinds.  XF8 = false: x is T (fp16/bf16), a
@@ -456,11 +463,20 @@ __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* r
 // cross-wave reduction and store while the next tile's stages are already in
 // flight.  For short K (few stages per tile) this spreads the pipeline fill
 // and the epilogue of a workgroup over several tiles.
-template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1>
+//
+// GLU (gate/up matrix with gelu_and_mul fused into the epilogue; TPW = 2,
+// one segment of N = 2 d rows): the workgroup's two tiles are gate rows
+// [n, n + 16) and up rows [d + n, d + n + 16); the gate tile's scaled sums
+// are rounded to TO and kept in wave 0's registers, and the up tile's end
+// stores y[m, n + c] = TO(gelu_tanh(gate) * up) into the [M, d] output --
+// the values gelu_and_mul computes from the rounded GEMV output.
+template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
+          bool GLU = false>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M) {
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 8), "activations go through LDS only for M <= 8");
+  static_assert(!GLU || (TPW == 2 && NT == 1), "gate/up pairs are two 16-row tiles");
   constexpr int K = STEPS * 1024;
   constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
@@ -481,15 +497,20 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   const int N = sr.n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n16 = lane & 15, g = lane >> 4;
-  const int nw = sr.group * ROWS * TPW;  // first row of the workgroup
+  const int half = GLU ? N >> 1 : 0;                 // GLU: d, the up rows' offset
+  const int nw = sr.group * ROWS * (GLU ? 1 : TPW);  // first row of the workgroup
+  // first row of tile t
+  auto tile_row = [&](int t) { return GLU ? nw + t * half : nw + ROWS * t; };
   uint32_t sc_n[NT];
   float sc_m[MB][4];
   lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 ? sg.xs : nullptr);
   // this wave loads rows wave + 4 j of every stage of tile t: row
-  // nw + ROWS t + wave + 4 j, clamped (clamped rows are never stored)
+  // tile_row(t) + wave + 4 j, clamped into the tile's matrix (clamped rows are
+  // never stored)
   auto wrow = [&](int t, int j) {
     const int r = wave + 4 * j;
-    return sr.w + (size_t)min(nw + ROWS * t + r, N - 1) * K + 16 * (lane ^ (r & 15));
+    const int row = GLU ? t * half + min(nw + r, half - 1) : min(nw + ROWS * t + r, N - 1);
+    return sr.w + (size_t)row * K + 16 * (lane ^ (r & 15));
   };
   const uint8_t* gx[MB];
 #pragma unroll
@@ -537,6 +558,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
+  [[maybe_unused]] float gate[MB][4];  // GLU: wave 0's rounded gate values (D layout)
 
   // Fully unrolled over the NS stages (the host instantiates the K values
   // it supports), so every slot index and every condition is static and the
@@ -600,14 +622,28 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     }
     if constexpr (TPW > 1) {
       if (i % STEPS == STEPS - 1) {  // tile i / STEPS is complete
-        lds_reduce_store_tile<NT, MB>(acc, smem + 2 * (STAGE + XSTAGE), wave, lane, nw + ROWS * (i / STEPS), N, M,
-                                      sr, skind, sc_n, sc_m, XF8, std::is_same<TO, BF16>::value);
+        uint8_t* redp = smem + 2 * (STAGE + XSTAGE);
+        if constexpr (GLU) {
+          if (i / STEPS == 0) {  // gate tile: keep the rounded values
+            lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8,
+                                    [&](int, int b, int v, float o) { gate[b][v] = TO::to_f32(TO::from_f32(o)); });
+          } else {  // up tile: gelu_and_mul and the store
+            lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8, [&](int, int b, int v, float o) {
+              const int n = nw + n16, m = b * 16 + g * 4 + v;
+              if (n < half && m < M)
+                sr.y[(size_t)m * half + n] = TO::from_f32(gelu_tanh(gate[b][v]) * TO::to_f32(TO::from_f32(o)));
+            });
+          }
+        } else {
+          lds_reduce_store_tile<NT, MB>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
+                                        XF8, std::is_same<TO, BF16>::value);
+        }
         if (i + 1 < NS) {
 #pragma unroll
           for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
-          lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw + ROWS * (i / STEPS + 1), N, M, sr, skind,
+          lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, tile_row(i / STEPS + 1), N, M, sr, skind,
                                   XF8 ? sg.xs : nullptr);
         }
       }
@@ -735,6 +771,41 @@ static bool launch_lds(const void* x, GemvSegs& sg, int skind, int M, int K, int
     case 24: return launch_lds_steps<T, TO, FMT, XF8, 24>(x, sg, skind, M, N, st);
     default: return false;
   }
+}
+
+// Gate/up GEMV with gelu_and_mul fused (gemv_lds_kernel's GLU form): one
+// segment of 2 d rows, one workgroup per 16 output columns.  The per-M
+// configurations are the one-tile ones of launch_lds_steps for these K.
+template <typename T, typename TO, int FMT, bool XF8, int S>
+static void launch_glu_steps(const void* x, GemvSegs& sg, int skind, int M, int d, hipStream_t st) {
+  const int grid = (d + 15) / 16;
+  sg.gstart[0] = 0;
+  for (int i = 1; i <= MAX_SEGS; ++i) sg.gstart[i] = grid;
+#define CEK_GLU(D, MX) \
+  gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, 2, true><<<dim3(grid), 256, 0, st>>>(x, sg, skind, M)
+  if constexpr (!XF8) {
+    if (M <= 4) {
+      CEK_GLU(3, 4);
+      return;
+    }
+    if (M <= 8) {
+      CEK_GLU(2, 8);
+      return;
+    }
+  }
+  CEK_GLU(3, 0);
+#undef CEK_GLU
+}
+
+template <typename T, typename TO, int FMT, bool XF8>
+static int launch_glu(const void* x, GemvSegs& sg, int skind, int M, int d, int K, hipStream_t st) {
+  switch (K >> 10) {
+    case 3: launch_glu_steps<T, TO, FMT, XF8, 3>(x, sg, skind, M, d, st); break;
+    case 4: launch_glu_steps<T, TO, FMT, XF8, 4>(x, sg, skind, M, d, st); break;
+    case 5: launch_glu_steps<T, TO, FMT, XF8, 5>(x, sg, skind, M, d, st); break;
+    default: return CEK_ERR_UNSUPPORTED;
+  }
+  return check_launch();
 }
 
 template <typename T, typename TO, int FMT, bool XF8>
@@ -879,7 +950,50 @@ static int scale_kind(int scale_dtype) {
   return -1;
 }
 
+// y[m, i] = gelu_tanh(g[m, i]) * u[m, i] with g = GEMV over weight rows
+// [0, d), u over rows [d, 2 d), both rounded to the output type first.
+// xs == null: x is io_dtype [M, K]; else x holds e4m3 codes [M, K] with
+// per-row fp32 scales xs (the a8w8 contract: e4m3 weights, fp32 scales).
+int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* scale, int skind, void* y,
+                    int64_t M, int64_t d, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st) {
+  if (M < 0 || d < 0 || K <= 0 || d > INT32_MAX / 2 || K > INT32_MAX) return CEK_ERR_INVALID;
+  if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
+  if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
+  if (skind < 0 || skind == SK_F32_SCALAR) return CEK_ERR_INVALID;
+  if (xs && (fp8_fmt != CEK_E4M3 || skind != SK_F32)) return CEK_ERR_INVALID;
+  if (M == 0 || d == 0) return CEK_OK;
+  if (!x || !w || !scale || !y) return CEK_ERR_INVALID;
+  if (2 * d * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
+  // The fused kernel: up to 16 rows, K of 3, 4 or 5 KiB values, 16-byte
+  // aligned operands; other requests are left to GEMV + gelu_and_mul.
+  if (M > 16 || K % 1024 != 0 || K < 3072 || K > 5120 || !aligned(x, 16) || !aligned(w, 16))
+    return CEK_ERR_UNSUPPORTED;
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = static_cast<const uint8_t*>(w);
+  sg.s[0] = scale;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)(2 * d);
+  sg.xs = xs;
+  const int m = (int)M, dd = (int)d, k = (int)K;
+  if (xs) {
+    if (io_dtype == CEK_F16) return launch_glu<F16, F16, CEK_E4M3, true>(x, sg, SK_F32, m, dd, k, st);
+    return launch_glu<F16, BF16, CEK_E4M3, true>(x, sg, SK_F32, m, dd, k, st);
+  }
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) return launch_glu<F16, F16, CEK_E4M3, false>(x, sg, skind, m, dd, k, st);
+  if (io_dtype == CEK_F16) return launch_glu<F16, F16, CEK_E5M2, false>(x, sg, skind, m, dd, k, st);
+  if (fp8_fmt == CEK_E4M3) return launch_glu<BF16, BF16, CEK_E4M3, false>(x, sg, skind, m, dd, k, st);
+  return launch_glu<BF16, BF16, CEK_E5M2, false>(x, sg, skind, m, dd, k, st);
+}
+
 }  // namespace cek
+
+extern "C" int cek_gemv_fp8_gelu_and_mul(const void* x, const float* x_scale, const void* w, const void* scale,
+                                         void* y, int64_t M, int64_t d, int64_t K, int io_dtype, int fp8_fmt,
+                                         int scale_dtype, void* stream) {
+  return cek::launch_gemv_glu(x, x_scale, w, scale, cek::scale_kind(scale_dtype), y, M, d, K, io_dtype, fp8_fmt,
+                              (hipStream_t)stream);
+}
 
 extern "C" int cek_gemv_fp8_pern(const void* x, const void* w, const void* scale, void* y,
                                  int64_t M, int64_t N, int64_t K,

@@ -253,6 +253,56 @@ void esimd_gelu_and_mul(at::Tensor out, at::Tensor input) {
            op);
 }
 
+// Gate/up GEMV over a merged [2d, K] weight with gelu_and_mul fused into its
+// epilogue: output[m, i] = gelu_tanh(g[m, i]) * u[m, i], g and u the GEMV's
+// rounded outputs of rows i and d + i.  Slabs of up to 16 rows go to the
+// fused kernel; shapes it does not cover run the GEMV into a workspace and
+// then gelu_and_mul (the same values).
+void esimd_gemv_fp8_gelu_and_mul(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output) {
+  const char* op = "esimd_gemv_fp8_gelu_and_mul";
+  check_gemv_io(input, output, op);
+  check_fp8_weight(weight, op);
+  check_device(weight, input, op, "weight");
+  check_device(weight_scale, input, op, "weight_scale");
+  check_device(output, input, op, "output");
+  check_contig(input, op, "input");
+  check_contig(weight, op, "weight");
+  check_contig(weight_scale, op, "weight_scale");
+  check_contig(output, op, "output");
+  TORCH_CHECK(weight.dim() == 2 && weight.size(0) % 2 == 0 && weight.size(0) > 0 && weight.size(1) > 0, op,
+              ": weight must be [2d, K]");
+  const int64_t d = weight.size(0) / 2, K = weight.size(1);
+  TORCH_CHECK(input.size(-1) == K, op, ": input must be [M, K]");
+  const int64_t M = input.numel() / K;
+  TORCH_CHECK(output.size(-1) == d && output.numel() == M * d, op, ": output must be [M, d]");
+  const auto sdt = weight_scale.scalar_type();
+  TORCH_CHECK(sdt == at::ScalarType::Half || sdt == at::ScalarType::BFloat16 || sdt == at::ScalarType::Float, op,
+              ": weight_scale must be fp16, bf16 or fp32");
+  TORCH_CHECK(weight_scale.numel() == 2 * d, op, ": weight_scale must hold 2d elements");
+  const int scale_code = sdt == at::ScalarType::Float ? CEK_F32 : (sdt == at::ScalarType::Half ? CEK_F16 : CEK_BF16);
+  c10::OptionalDeviceGuard guard(input.device());
+  void* st = current_stream(input);
+  const int io = io_code(input.scalar_type());
+  const int fmt = fp8_code(weight);
+  const size_t esz = input.element_size();
+  at::Tensor gu;  // workspace of the unfused path, [16, 2d]
+  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    const int64_t mb = std::min<int64_t>(16, M - m0);
+    const char* x = static_cast<const char*>(input.data_ptr()) + m0 * K * esz;
+    char* y = static_cast<char*>(output.data_ptr()) + m0 * d * esz;
+    int rc = cek_gemv_fp8_gelu_and_mul(x, nullptr, weight.data_ptr(), weight_scale.data_ptr(), y, mb, d, K, io, fmt,
+                                       scale_code, st);
+    if (rc == CEK_ERR_UNSUPPORTED) {
+      if (!gu.defined()) gu = at::empty({16, 2 * d}, input.options());
+      check_rc(cek_gemv_fp8_pern(x, weight.data_ptr(), weight_scale.data_ptr(), gu.data_ptr(), mb, 2 * d, K, io, fmt,
+                                 scale_code, st),
+               op);
+      rc = cek_gelu_and_mul(y, gu.data_ptr(), mb, d, 2 * d, d, io, st);
+    }
+    check_rc(rc, op);
+  }
+}
+
 // q / k are [T, n * hd] or [T, n, hd] views (rows may be strided, heads
 // contiguous within a row), modified in place.
 static int64_t rows_and_stride(const at::Tensor& t, int64_t hd, int64_t& n_heads, const char* op,

@@ -68,3 +68,46 @@ at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, a
            op);
   return output;
 }
+
+// a8w8 gate/up GEMM over a merged [2d, K] e4m3 weight with gelu_and_mul fused
+// into the epilogue: output[m, i] = gelu_tanh(g[m, i]) * u[m, i], g and u the
+// rounded outputs of weight rows i and d + i.  Decode batches (M <= 16) take
+// the fused kernel; other shapes run esimd_gemm_fp8_a8w8's kernels into a
+// workspace and then gelu_and_mul (the same values).
+void esimd_gemm_fp8_a8w8_gelu_and_mul(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
+                                      at::Tensor output) {
+  const char* op = "esimd_gemm_fp8_a8w8_gelu_and_mul";
+  TORCH_CHECK(a.element_size() == 1 && b.element_size() == 1, op, ": a and b must be 8-bit (e4m3) tensors");
+  TORCH_CHECK(a.scalar_type() != at::ScalarType::Float8_e5m2 && b.scalar_type() != at::ScalarType::Float8_e5m2, op,
+              ": a and b must be e4m3");
+  TORCH_CHECK(a_scale.scalar_type() == at::ScalarType::Float && b_scale.scalar_type() == at::ScalarType::Float, op,
+              ": scales must be fp32");
+  TORCH_CHECK(is_io(output.scalar_type()), op, ": output must be fp16 or bf16");
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2 && a.size(1) == b.size(1), op, ": a [M, K] and b [2d, K] required");
+  TORCH_CHECK(b.size(0) % 2 == 0, op, ": b must have an even number of rows (gate rows, then up rows)");
+  for (auto* t : {&a_scale, &b, &b_scale, &output}) check_device(*t, a, op, "operand");
+  check_contig(a, op, "a");
+  check_contig(b, op, "b");
+  check_contig(a_scale, op, "a_scale");
+  check_contig(b_scale, op, "b_scale");
+  check_contig(output, op, "output");
+  const int64_t M = a.size(0), K = a.size(1), d = b.size(0) / 2;
+  TORCH_CHECK(K % 16 == 0, op, ": K must be a multiple of 16");
+  TORCH_CHECK(a_scale.numel() == M && b_scale.numel() == 2 * d, op, ": a_scale [M] and b_scale [2d] required");
+  TORCH_CHECK(output.numel() == M * d, op, ": output must be [M, d]");
+  c10::OptionalDeviceGuard guard(a.device());
+  void* st = current_stream(a);
+  const int io = io_code(output.scalar_type());
+  const auto* ap = static_cast<const uint8_t*>(a.data_ptr());
+  const auto* sa = static_cast<const float*>(a_scale.data_ptr());
+  const auto* bp = static_cast<const uint8_t*>(b.data_ptr());
+  const auto* sb = static_cast<const float*>(b_scale.data_ptr());
+  int rc = M <= 16 ? cek_gemv_fp8_gelu_and_mul(ap, sa, bp, sb, output.data_ptr(), M, d, K, io, CEK_E4M3, CEK_F32, st)
+                   : CEK_ERR_UNSUPPORTED;
+  if (rc == CEK_ERR_UNSUPPORTED && M > 0 && d > 0) {
+    at::Tensor gu = at::empty({M, 2 * d}, output.options());
+    check_rc(cek_gemm_fp8_a8w8(ap, sa, bp, sb, gu.data_ptr(), M, 2 * d, K, io, st), op);
+    rc = cek_gelu_and_mul(output.data_ptr(), gu.data_ptr(), M, d, 2 * d, d, io, st);
+  }
+  check_rc(rc, op);
+}

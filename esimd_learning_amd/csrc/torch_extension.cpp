@@ -41,6 +41,10 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
   m.def("esimd_gelu_and_mul(Tensor(a!) out, Tensor input) -> ()");
   m.impl("esimd_gelu_and_mul", c10::DispatchKey::CUDA, &esimd_gelu_and_mul);
 
+  m.def("esimd_gemv_fp8_gelu_and_mul(Tensor input, Tensor weight, Tensor weight_scale, "
+        "Tensor(a!) output) -> ()");
+  m.impl("esimd_gemv_fp8_gelu_and_mul", c10::DispatchKey::CUDA, &esimd_gemv_fp8_gelu_and_mul);
+
   m.def("esimd_qk_norm_rope(Tensor(a!) q, Tensor(b!) k, Tensor q_weight, Tensor k_weight, "
         "Tensor positions, float eps, float theta, bool is_neox) -> ()");
   m.impl("esimd_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_qk_norm_rope);

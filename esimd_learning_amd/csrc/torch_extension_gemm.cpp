@@ -13,10 +13,14 @@ TORCH_LIBRARY_FRAGMENT(custom_esimd_kernels_vllm, m) {
         "Tensor output) -> Tensor");
   m.impl("esimd_gemm_fp8_pert", c10::DispatchKey::CUDA, &esimd_gemm_fp8_pert);
 
-  // ---- new op ----
+  // ---- new ops ----
   m.def("esimd_gemm_fp8_a8w8(Tensor a, Tensor a_scale, Tensor b, Tensor b_scale, "
         "Tensor(a!) output) -> Tensor(a!)");
   m.impl("esimd_gemm_fp8_a8w8", c10::DispatchKey::CUDA, &esimd_gemm_fp8_a8w8);
+
+  m.def("esimd_gemm_fp8_a8w8_gelu_and_mul(Tensor a, Tensor a_scale, Tensor b, Tensor b_scale, "
+        "Tensor(a!) output) -> ()");
+  m.impl("esimd_gemm_fp8_a8w8_gelu_and_mul", c10::DispatchKey::CUDA, &esimd_gemm_fp8_a8w8_gelu_and_mul);
 }
 
 PyMODINIT_FUNC PyInit_custom_esimd_kernels_gemm() {

@@ -38,8 +38,15 @@ void esimd_per_token_quant_fp8(at::Tensor input, at::Tensor out_q, at::Tensor ou
 
 void esimd_gelu_and_mul(at::Tensor out, at::Tensor input);
 
+// Gate/up GEMV over a merged [2d, K] weight with gelu_and_mul fused.
+void esimd_gemv_fp8_gelu_and_mul(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output);
+
 void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Tensor k_weight,
                         at::Tensor positions, double eps, double theta, bool is_neox);
 
 at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
                                at::Tensor output);
+
+// The a8w8 form of esimd_gemv_fp8_gelu_and_mul (e4m3 activations and weights).
+void esimd_gemm_fp8_a8w8_gelu_and_mul(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
+                                      at::Tensor output);

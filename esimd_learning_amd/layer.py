@@ -6,13 +6,18 @@
     a      = attention(q, k, v)        -- out of scope: q stands in for its output
     o      = a @ Wo^T * so                                esimd_gemv_fp8_pern
     h2, r2 = add_rmsnorm(o, r1, w_post)                   esimd_fused_add_rms_norm_batched
-    gu     = h2 @ Wgu^T * sgu                             esimd_gemv_fp8_pern
-    g      = gelu_tanh(gu[:, :d]) * gu[:, d:]             esimd_gelu_and_mul
+    g      = gelu_tanh(h2 @ Wg^T * sg) * (h2 @ Wu^T * su) esimd_gemv_fp8_gelu_and_mul
     out    = g @ Wd^T * sd                                esimd_gemv_fp8_pern
+
+The gate/up projection and gelu_and_mul run as one launch (Wgu = [Wg; Wu],
+the GEMV's epilogue applies gelu_tanh(gate) * up to the rounded outputs);
+``fuse_glu=False`` runs them as esimd_gemv_fp8_pern into [M, 2d] followed by
+esimd_gelu_and_mul, which gives the same values.
 
 With ``act_fp8=True`` the two norm -> GEMV hand-offs carry e4m3 activations
 instead of fp16: esimd_fused_add_rms_norm_quant_fp8 writes per-token codes
-and scales, and esimd_gemm_fp8_a8w8 consumes them (the hidden input is then
+and scales, and esimd_gemm_fp8_a8w8 (esimd_gemm_fp8_a8w8_gelu_and_mul for
+gate/up) consumes them (the hidden input is then
 only read, not overwritten with the normed value).  Needs e4m3 weights.
 
 All intermediate buffers are allocated once in the constructor, so a step
@@ -25,7 +30,7 @@ import torch
 
 
 class GemmaDecodeLayer:
-    def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False):
+    def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False, fuse_glu=True):
         from . import ops as _load_ops
         self.ops = _load_ops()
         p = params
@@ -48,6 +53,7 @@ class GemmaDecodeLayer:
         self.act = mk(self.mlp)
         self.out = mk(self.hidden)
         self.act_fp8 = act_fp8
+        self.fuse_glu = fuse_glu
         if act_fp8:
             if self.Wqkv.dtype != torch.float8_e4m3fn or self.Wgu.dtype != torch.float8_e4m3fn:
                 raise ValueError("act_fp8 needs e4m3 weights")
@@ -75,11 +81,19 @@ class GemmaDecodeLayer:
         o.esimd_gemv_fp8_pern(self.attn, self.Wo, self.so, self.o, self.hidden, nq * hd)
         if self.act_fp8:
             o.esimd_fused_add_rms_norm_quant_fp8(self.o, residual, self.w_post, self.eps, self.q8, self.s8)
-            o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wgu8, self.sgu32, self.gu)
+            if self.fuse_glu:
+                o.esimd_gemm_fp8_a8w8_gelu_and_mul(self.q8.view(torch.uint8), self.s8, self.Wgu8, self.sgu32,
+                                                   self.act)
+            else:
+                o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wgu8, self.sgu32, self.gu)
         else:
             o.esimd_fused_add_rms_norm_batched(self.o, residual, self.w_post, self.eps)
-            o.esimd_gemv_fp8_pern(self.o, self.Wgu, self.sgu, self.gu, 2 * self.mlp, self.hidden)
-        o.esimd_gelu_and_mul(self.act, self.gu)
+            if self.fuse_glu:
+                o.esimd_gemv_fp8_gelu_and_mul(self.o, self.Wgu, self.sgu, self.act)
+            else:
+                o.esimd_gemv_fp8_pern(self.o, self.Wgu, self.sgu, self.gu, 2 * self.mlp, self.hidden)
+        if not self.fuse_glu:
+            o.esimd_gelu_and_mul(self.act, self.gu)
         o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
         return self.out
 

@@ -99,6 +99,19 @@ def esimd_gelu_and_mul(out: torch.Tensor, input: torch.Tensor) -> None:
     _ops.esimd_gelu_and_mul(out, input)
 
 
+def esimd_gemv_fp8_gelu_and_mul(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
+) -> None:
+    """Gate/up GEMV over a merged fp8 weight with gelu_and_mul fused.
+
+    input [M, K] fp16/bf16; weight [2d, K] fp8 (gate rows, then up rows);
+    weight_scale [2d] fp16/bf16/fp32; output [M, d] of input's dtype.
+    output equals esimd_gemv_fp8_pern into [M, 2d] followed by
+    esimd_gelu_and_mul, in one launch for decode batches.
+    """
+    _ops.esimd_gemv_fp8_gelu_and_mul(input, weight, weight_scale, output)
+
+
 def esimd_qk_norm_rope(
     q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
     positions: torch.Tensor, eps: float, theta: float = 10000.0, is_neox: bool = True,
@@ -113,3 +126,12 @@ def esimd_gemm_fp8_a8w8(
 ) -> torch.Tensor:
     """output[m, n] = a_scale[m] * b_scale[n] * sum_k a[m, k] * b[n, k] (e4m3 x e4m3)."""
     return _ops.esimd_gemm_fp8_a8w8(a, a_scale, b, b_scale, output)
+
+
+def esimd_gemm_fp8_a8w8_gelu_and_mul(
+    a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
+    output: torch.Tensor,
+) -> None:
+    """esimd_gemm_fp8_a8w8 over a merged [2d, K] gate/up weight, then
+    gelu_and_mul, fused for M <= 16: output [M, d]."""
+    _ops.esimd_gemm_fp8_a8w8_gelu_and_mul(a, a_scale, b, b_scale, output)

@@ -141,6 +141,25 @@ int cek_gelu_and_mul(void* out, const void* x, int64_t T, int64_t d,
                      int64_t x_stride, int64_t out_stride, int io_dtype, void* stream);
 
 /*
+ * NEW: gate/up GEMV with gelu_and_mul fused into its epilogue (no
+ * counterpart in the reference: it is esimd_gemv_fp8_pern over a merged
+ * [2d, K] gate/up weight, csrc/xpu/esimd_kernel.sycl:22-53, followed by
+ * cek_gelu_and_mul, in one launch):
+ *   g[m, i] = Out(sum_k x[m, k] * dq(W[i, k]) * s[i])          rows [0, d)
+ *   u[m, i] = Out(sum_k x[m, k] * dq(W[d + i, k]) * s[d + i])  rows [d, 2d)
+ *   y[m, i] = Out(gelu_tanh(g[m, i]) * u[m, i])                y [M, d]
+ * x_scale == NULL: x is io_dtype [M, K], s [2d] of scale_dtype (F16|BF16|F32),
+ * W e4m3 or e5m2 (fp8_fmt).  x_scale != NULL: x holds e4m3 codes [M, K] with
+ * per-row fp32 scales x_scale [M], W e4m3 and s fp32 (the a8w8 contract; the
+ * sums then carry x_scale[m] too).  Covers M <= 16, K in {3072, 4096, 5120}
+ * and 16-byte aligned x and W; CEK_ERR_UNSUPPORTED otherwise, for the caller
+ * to run the GEMV and cek_gelu_and_mul instead.
+ */
+int cek_gemv_fp8_gelu_and_mul(const void* x, const float* x_scale, const void* w, const void* scale,
+                              void* y, int64_t M, int64_t d, int64_t K, int io_dtype, int fp8_fmt,
+                              int scale_dtype, void* stream);
+
+/*
  * NEW: per-head RMSNorm (weight qw / kw of length head_dim, Gemma w+1) then
  * rotary embedding, in place on q [T, n_q * head_dim] and
  * k [T, n_k * head_dim] (row strides q_stride / k_stride elements, so both

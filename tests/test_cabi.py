@@ -84,6 +84,21 @@ def test_host_rejects_invalid_arguments():
     assert lib.cek_gemv_fp8_pern_multi(p, 0, P3(p, p, p), P3(p, p, p), P3(p, p, p), Ns, 1, 64, 0, 0, 2, None) == E
     assert lib.cek_gemv_fp8_pern_multi(p, 9, P3(p, p, p), P3(p, p, p), P3(p, p, p), Ns, 1, 64, 0, 0, 2, None) == E
     assert lib.cek_gemv_fp8_pert_multi(p, 3, None, P3(p, p, p), P3(p, p, p), Ns, 1, 64, 0, 0, None) == E
+    # fused gate/up GEMV + gelu_and_mul: bad enums, a8w8 contract, then shapes
+    # the fused kernel leaves to the caller's two-launch path
+    glu = lib.cek_gemv_fp8_gelu_and_mul
+    U = cabi.CEK_ERR_UNSUPPORTED
+    assert glu(p, None, p, p, p, 4, 64, 4096, 5, 0, 2, None) == E                     # io dtype
+    assert glu(p, None, p, p, p, 4, 64, 4096, 0, 0, 7, None) == E                     # scale dtype
+    assert glu(p, p, p, p, p, 4, 64, 4096, 0, 1, 2, None) == E                        # a8w8 with e5m2
+    assert glu(p, p, p, p, p, 4, 64, 4096, 0, 0, 0, None) == E                        # a8w8 with fp16 scales
+    assert glu(p, None, p, p, p, -1, 64, 4096, 0, 0, 2, None) == E
+    assert glu(None, None, p, p, p, 4, 64, 4096, 0, 0, 2, None) == E                  # null x
+    assert glu(p, None, p, p, p, 17, 64, 4096, 0, 0, 2, None) == U                    # M > 16
+    assert glu(p, None, p, p, p, 4, 64, 2048, 0, 0, 2, None) == U                     # K outside 3-5 KiB
+    assert glu(p, None, p, p, p, 4, 64, 4100, 0, 0, 2, None) == U
+    assert glu(C.c_void_p(24), None, p, p, p, 4, 64, 4096, 0, 0, 2, None) == U        # alignment
+    assert glu(None, None, None, None, None, 0, 64, 4096, 0, 0, 2, None) == cabi.CEK_OK
     # empty problems are no-ops that succeed without touching memory
     assert lib.cek_gemv_fp8_pern(None, None, None, None, 0, 8, 64, 0, 0, 2, None) == cabi.CEK_OK
     assert lib.cek_fused_add_rms_norm(None, None, None, 0, 64, 1e-6, 0, None) == cabi.CEK_OK

@@ -27,12 +27,13 @@ SMALL = dict(hidden=512, n_q=4, n_kv=2, head_dim=64, mlp=1024)
 CONFIG5 = dict(hidden=3072, n_q=16, n_kv=16, head_dim=256, mlp=24576)
 
 
+@pytest.mark.parametrize("fuse_glu", [True, False])
 @pytest.mark.parametrize("act_fp8", [False, True])
 @pytest.mark.parametrize("dims,M", [(SMALL, 3), (CONFIG5, 4)])
-def test_decoder_step_vs_oracle(ops, dev, dims, M, act_fp8):
-    _say(f"decoder step M={M} {dims} act_fp8={act_fp8}")
+def test_decoder_step_vs_oracle(ops, dev, dims, M, act_fp8, fuse_glu):
+    _say(f"decoder step M={M} {dims} act_fp8={act_fp8} fuse_glu={fuse_glu}")
     p = synthetic.gemma_layer(seed=10, **dims)
-    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse_glu)
     h = synthetic.activations(M, dims["hidden"], seed=20)
     r = synthetic.activations(M, dims["hidden"], seed=21)
     pos = synthetic.positions(M, seed=22)
@@ -68,3 +69,21 @@ def test_decoder_step_graph_replays(ops, dev, act_fp8):
         assert torch.equal(out, ref)
         assert torch.equal(rb, ref_r)
         torch.randn(1000, device=dev).sum().item()   # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("act_fp8", [False, True])
+def test_decoder_step_fused_glu_equals_unfused(ops, dev, act_fp8):
+    """The fused gate/up + gelu launch gives the step the unfused ops give, bit for bit."""
+    M, dims = 4, CONFIG5
+    p = synthetic.gemma_layer(seed=12, **dims)
+    outs = []
+    for fuse in (True, False):
+        layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse)
+        h = synthetic.activations(M, dims["hidden"], seed=40).to(dev)
+        r = synthetic.activations(M, dims["hidden"], seed=41).to(dev)
+        outs.append((layer.step(h, r, synthetic.positions(M, seed=42).to(dev)).clone(), r.clone(),
+                     layer.act.clone()))
+        del layer
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

@@ -33,14 +33,14 @@ __global__ __launch_bounds__(256) void gelu_and_mul_kernel(
     u4 a = load_u4(xr + i), b = load_u4(xr + d + i), o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      float g0 = gelu_tanh(T::to_f32(a[e] & 0xFFFF)) * T::to_f32(b[e] & 0xFFFF);
-      float g1 = gelu_tanh(T::to_f32(a[e] >> 16)) * T::to_f32(b[e] >> 16);
+      float g0 = f32_round(gelu_tanh(T::to_f32(a[e] & 0xFFFF)) * T::to_f32(b[e] & 0xFFFF));
+      float g1 = f32_round(gelu_tanh(T::to_f32(a[e] >> 16)) * T::to_f32(b[e] >> 16));
       o[e] = (uint32_t)T::from_f32(g0) | ((uint32_t)T::from_f32(g1) << 16);
     }
     *reinterpret_cast<u4*>(orow + i) = o;
   } else {
     for (int i = (blockIdx.x * 256 + threadIdx.x) * 8, e = 0; e < 8; ++e, ++i)
-      if (i < d) orow[i] = T::from_f32(gelu_tanh(T::to_f32(xr[i])) * T::to_f32(xr[d + i]));
+      if (i < d) orow[i] = T::from_f32(f32_round(gelu_tanh(T::to_f32(xr[i])) * T::to_f32(xr[d + i])));
   }
 }
 

@@ -40,11 +40,25 @@ struct BF16 {
   __device__ static inline uint16_t from_f32(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 };
 
+// An fp32 value as a register value: the empty asm keeps the compiler from
+// folding the multiply that produced v into the 16-bit conversion that
+// follows (a mixed-precision fma, v_fma_mix*, that rounds the exact product
+// straight to 16 bits).  Whether it folds differs between call sites, so
+// kernels that must agree bit for bit (a fused kernel and the ops it fuses)
+// round every stored product through here: to fp32, then to the 16-bit type,
+// as the source and the torch oracle do.
+__device__ inline float f32_round(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // gelu with the tanh approximation, fp32 math:
 // gelu_tanh(u) = 0.5 u (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))).  One
-// definition for gelu_and_mul and the GEMV epilogue that fuses it, so the two
-// paths round identically.
+// definition for gelu_and_mul and the GEMV epilogue that fuses it, each
+// operation rounded to fp32 (no contraction into fma), so every call site
+// computes the same value.
 __device__ inline float gelu_tanh(float u) {
+#pragma clang fp contract(off)
   const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
   const float k1 = 0.044715f;
   return 0.5f * u * (1.0f + tanhf(k0 * (u + k1 * u * u * u)));
@@ -141,6 +155,16 @@ __device__ inline uint32_t f32_to_e4m3(float v) {
 __device__ inline uint32_t f32x4_to_e4m3x4(float a, float b, float c, float d) {
   int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// Per-token e4m3 quantisation: scale = max(amax / 448, 1 / (448 * 512)),
+// code = e4m3_rne(clamp(v / scale, -448, 448)).  Shared by the norm kernels
+// and the GEMV whose prologue fuses the norm.
+constexpr float E4M3_MAX = 448.0f;
+constexpr float MIN_SCALE = 1.0f / (448.0f * 512.0f);
+__device__ inline float quant_scale(float amax) { return fmaxf(amax / E4M3_MAX, MIN_SCALE); }
+__device__ inline float quant_clamp(float v, float s) {
+  return fminf(fmaxf(v / s, -E4M3_MAX), E4M3_MAX);  // IEEE divide (no fast math)
 }
 
 // Butterfly sum over the 64 lanes of a wave; every lane gets the total.

@@ -80,6 +80,19 @@ struct GemvSegs {
   const float* xs;  // per-row activation scales [M] when x holds e4m3 codes
 };
 
+// Inputs and side outputs of the add+RMSNorm (+ e4m3 quant) that
+// gemv_lds_kernel's NORM form computes in its prologue (unused otherwise).
+struct NormArgs {
+  const uint16_t* h;  // hidden [M, K]
+  const uint16_t* r;  // residual [M, K] (read)
+  const uint16_t* w;  // RMSNorm weight [K] (Gemma w+1 convention)
+  uint16_t* r_out;    // h + r rounded [M, K], written by workgroup 0
+  uint16_t* h_out;    // normed rows [M, K] (fp16/bf16 form; may be null), workgroup 0
+  uint8_t* q_out;     // e4m3 codes [M, K] (quant form), workgroup 0
+  float* s_out;       // per-row scales [M] (quant form), workgroup 0
+  float eps;
+};
+
 struct SegRef {
   const uint8_t* w;
   const void* s;
@@ -384,7 +397,7 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
       for (int v = 0; v < 4; ++v) {
         const int m = b * 16 + g * 4 + v;  // D row = 4 * (lane >> 4) + v
         if (m >= M) continue;
-        const float o = c[v] * (xscaled ? sc * sc_m[b][v] : sc);
+        const float o = f32_round(c[v] * (xscaled ? sc * sc_m[b][v] : sc));
         sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
       }
     }
@@ -427,7 +440,7 @@ __device__ inline void lds_reduce_tile(const f4 (&acc)[NT][MB], uint8_t* redp, i
 #pragma unroll
         for (int w = 0; w < 3; ++w) c += red[((w * NT + t) * MB + b) * 64 + lane];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) emit(t, b, v, c[v] * (xscaled ? sc * sc_m[b][v] : sc));
+        for (int v = 0; v < 4; ++v) emit(t, b, v, f32_round(c[v] * (xscaled ? sc * sc_m[b][v] : sc)));
       }
     }
   }
@@ -470,13 +483,24 @@ __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* r
 // are rounded to TO and kept in wave 0's registers, and the up tile's end
 // stores y[m, n + c] = TO(gelu_tanh(gate) * up) into the [M, d] output --
 // the values gelu_and_mul computes from the rounded GEMV output.
+//
+// NORM (M <= MX <= 4 rows, one tile row block): the activations are not read
+// from x but computed in the prologue from (na.h, na.r, na.w) -- the
+// add+RMSNorm of add_rmsnorm_kernel, with its thread layout and reduction
+// order, so the values are bit-identical, and with XF8 its per-row e4m3
+// quantisation -- for the whole K into LDS, where the stages read them.  The
+// loads of h and r are issued before the weight prologue, so the norm runs
+// while the first weight stages are in flight.  Workgroup 0 also writes the
+// side outputs (na.r_out, na.h_out or na.q_out / na.s_out); the other
+// workgroups read na.r meanwhile, so na.r_out must not alias it.
 template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
-          bool GLU = false>
-__global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M) {
+          bool GLU = false, bool NORM = false>
+__global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M, NormArgs na) {
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 8), "activations go through LDS only for M <= 8");
   static_assert(!GLU || (TPW == 2 && NT == 1), "gate/up pairs are two 16-row tiles");
+  static_assert(!NORM || (MX >= 1 && MX <= 4 && NT == 1), "fused norm: up to four rows");
   constexpr int K = STEPS * 1024;
   constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
@@ -487,12 +511,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   // weights, XU units per thread; MX = 0: each lane loads its MFMA operands
   // straight from L2 (all 16 operand rows, the clamped ones included).
   constexpr int XROW = 1024 * XB;                  // activation bytes per row and stage
-  constexpr int XU = MX > 0 ? MX * XROW / 16 / 256 : 1;
+  constexpr int XU = MX > 0 && !NORM ? MX * XROW / 16 / 256 : 1;
   constexpr int XSTAGE = MX * XROW;
-  static_assert(MX == 0 || XU * 16 * 256 == XSTAGE, "activation units per thread");
-  // two stage buffers, then (TPW > 1) the cross-wave reduction area
+  static_assert(MX == 0 || NORM || XU * 16 * 256 == XSTAGE, "activation units per thread");
+  // two weight stage buffers; the activations of two stages (NORM: of all
+  // STEPS stages); (TPW > 1) the cross-wave reduction area; (NORM) the
+  // norm's per-row partial sums and maxima
+  constexpr int XAREA = NORM ? STEPS * XSTAGE : 2 * XSTAGE;
   constexpr int RED = TPW > 1 ? 3 * NT * MB * 64 * 16 : 0;
-  __shared__ __align__(16) uint8_t smem[2 * (STAGE + XSTAGE) + RED];
+  constexpr int NSH = NORM ? 2 * 4 * MX * 4 : 0;
+  __shared__ __align__(16) uint8_t smem[2 * STAGE + XAREA + RED + NSH];
   const SegRef sr = find_seg(sg, blockIdx.x);
   const int N = sr.n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -503,7 +531,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   auto tile_row = [&](int t) { return GLU ? nw + t * half : nw + ROWS * t; };
   uint32_t sc_n[NT];
   float sc_m[MB][4];
-  lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 ? sg.xs : nullptr);
+  lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 && !NORM ? sg.xs : nullptr);
   // this wave loads rows wave + 4 j of every stage of tile t: row
   // tile_row(t) + wave + 4 j, clamped into the tile's matrix (clamped rows are
   // never stored)
@@ -537,7 +565,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 #pragma unroll
     for (int j = 0; j < LW; ++j) ws[j] = load_u4_stream(wrow(i / STEPS, j) + k0);  // 1 KB of one row per instruction
     asm volatile("" ::: "memory");  // same issue order in every step (weights, then activations)
-    if constexpr (MX > 0) {
+    if constexpr (NORM) {
+      (void)xs;  // activations are resident in LDS
+    } else if constexpr (MX > 0) {
 #pragma unroll
       for (int j = 0; j < XU; ++j) xs[j][0][0] = load_u4(gxu[j] + (size_t)k0 * XB);
     } else {
@@ -560,22 +590,156 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
   [[maybe_unused]] float gate[MB][4];  // GLU: wave 0's rounded gate values (D layout)
 
+  // NORM: thread t's 8-element units t + 256 j of every row (add_rmsnorm_kernel's
+  // layout), rows >= M repeating row M - 1 and units past the row repeating
+  // the last (both never used), so that every load is unconditional.
+  constexpr int NU = NORM ? (K / 8 + 255) / 256 : 1;
+  constexpr int NR = NORM ? MX : 1;
+  [[maybe_unused]] u4 nh[NR][NU], nr[NR][NU], ng[NU];
+  [[maybe_unused]] float rsc[NR];  // NORM + XF8: the rows' quantisation scales
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      const int u = min((int)threadIdx.x + 256 * j, K / 8 - 1);
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        const size_t o = (size_t)min(m, M - 1) * K + (size_t)u * 8;
+        nh[m][j] = load_u4(na.h + o);
+        nr[m][j] = load_u4(na.r + o);
+      }
+      ng[j] = load_u4(na.w + u * 8);
+    }
+    asm volatile("" ::: "memory");  // before the weight prologue
+  }
+  // NORM + XF8: wave 0's epilogue row scales, sc_m[0][v] for row 4 (lane >> 4) + v
+  auto pick_row_scales = [&]() {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = min(g * 4 + v, M - 1);
+      float pick = rsc[0];
+#pragma unroll
+      for (int mm = 1; mm < NR; ++mm) pick = m == mm ? rsc[mm] : pick;
+      sc_m[0][v] = pick;
+    }
+  };
+
   // Fully unrolled over the NS stages (the host instantiates the K values
   // it supports), so every slot index and every condition is static and the
   // compiler's in-order vmcnt waits are exact: the wait for stage i leaves
   // the loads of the stages after it in flight.
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, wr[j], xr[j]);
+
+  if constexpr (NORM) {
+    // add_rmsnorm_kernel's arithmetic, row by row: s = h + r in fp32, r' =
+    // Out(s) (stored by workgroup 0), sum of s^2 over the unrounded s (fmaf in
+    // unit order, wave butterfly, then the four waves in order), inv =
+    // rsqrt(sum / K + eps), normed = Out(r' * inv * w).
+    typedef typename std::conditional<XF8, TO, T>::type TN;  // the norm's activation type
+    constexpr int UNITS = K / 8;
+    const int t = threadIdx.x;
+    const bool side = blockIdx.x == 0;  // writes the side outputs
+    uint8_t* xall = smem + 2 * STAGE;
+    float* nsh = reinterpret_cast<float*>(smem + 2 * STAGE + XAREA + RED);  // [2][MX][4]
+    float ss[MX];
+    u4 rp[MX][NU];
+#pragma unroll
+    for (int m = 0; m < MX; ++m) {
+      ss[m] = 0.f;
+#pragma unroll
+      for (int j = 0; j < NU; ++j) {
+        const int u = t + 256 * j;
+        u4 o = u4{0, 0, 0, 0};
+        if (u < UNITS) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a0 = TN::to_f32(nh[m][j][e] & 0xFFFF) + TN::to_f32(nr[m][j][e] & 0xFFFF);
+            const float a1 = TN::to_f32(nh[m][j][e] >> 16) + TN::to_f32(nr[m][j][e] >> 16);
+            ss[m] = fmaf(a0, a0, ss[m]);
+            ss[m] = fmaf(a1, a1, ss[m]);
+            o[e] = (uint32_t)TN::from_f32(a0) | ((uint32_t)TN::from_f32(a1) << 16);
+          }
+          if (side && m < M) *reinterpret_cast<u4*>(na.r_out + (size_t)m * K + u * 8) = o;
+        }
+        rp[m][j] = o;
+      }
+      const float v = wave_sum(ss[m]);
+      if (lane == 0) nsh[m * 4 + wave] = v;
+    }
+    lds_barrier();
+    float amax[MX];
+    u4 nv[MX][NU];
+#pragma unroll
+    for (int m = 0; m < MX; ++m) {
+      const float inv = rsqrtf((nsh[m * 4] + nsh[m * 4 + 1] + nsh[m * 4 + 2] + nsh[m * 4 + 3]) / (float)K + na.eps);
+      amax[m] = 0.f;
+#pragma unroll
+      for (int j = 0; j < NU; ++j) {
+        const int u = t + 256 * j;
+        if (u >= UNITS) continue;
+        u4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float n0 = f32_round(TN::to_f32(rp[m][j][e] & 0xFFFF) * inv * TN::to_f32(ng[j][e] & 0xFFFF));
+          const float n1 = f32_round(TN::to_f32(rp[m][j][e] >> 16) * inv * TN::to_f32(ng[j][e] >> 16));
+          const uint16_t b0 = TN::from_f32(n0), b1 = TN::from_f32(n1);
+          if (XF8) amax[m] = fmaxf(amax[m], fmaxf(fabsf(TN::to_f32(b0)), fabsf(TN::to_f32(b1))));
+          o[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+        }
+        if constexpr (XF8) {
+          nv[m][j] = o;
+        } else {
+          // unit u = chunk u % 128 of stage u / 128, rows swizzled as the stages' are
+          *reinterpret_cast<u4*>(xall + (u >> 7) * XSTAGE + m * XROW + 16 * ((u & 127) ^ (m & 7))) = o;
+          if (side && m < M && na.h_out) *reinterpret_cast<u4*>(na.h_out + (size_t)m * K + u * 8) = o;
+        }
+      }
+    }
+    if constexpr (XF8) {
+      // per_token_quant_kernel's quantisation of the rounded normed rows
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        const float v = wave_max(amax[m]);
+        if (lane == 0) nsh[(MX + m) * 4 + wave] = v;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        const float* mx = nsh + (MX + m) * 4;
+        const float sq = quant_scale(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
+        rsc[m] = sq;
+        if (side && m < M && t == 0) na.s_out[m] = sq;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+          const int u = t + 256 * j;
+          if (u >= UNITS) continue;
+          uint32_t c[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const uint32_t a = nv[m][j][2 * e], b = nv[m][j][2 * e + 1];
+            c[e] = f32x4_to_e4m3x4(quant_clamp(TN::to_f32(a & 0xFFFF), sq), quant_clamp(TN::to_f32(a >> 16), sq),
+                                   quant_clamp(TN::to_f32(b & 0xFFFF), sq), quant_clamp(TN::to_f32(b >> 16), sq));
+          }
+          // unit u = half u & 1 of 16-code chunk (u % 128) / 2 of stage u / 128
+          *reinterpret_cast<uint2*>(xall + (u >> 7) * XSTAGE + m * XROW + 16 * (((u & 127) >> 1) ^ (m & 7)) +
+                                    8 * (u & 1)) = make_uint2(c[0], c[1]);
+          if (side && m < M) *reinterpret_cast<uint2*>(na.q_out + (size_t)m * K + u * 8) = make_uint2(c[0], c[1]);
+        }
+      }
+      pick_row_scales();
+    }
+    // the first stage's barrier orders these LDS writes before any read
+  }
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
     // Stage i into LDS buffer i & 1 (last read at step i - 2, which every
     // wave finished before the barrier of step i - 1).  Lane l's unit lands
     // at slot l, i.e. unit v of row r at slot v ^ (r & 15).
     uint8_t* sw = smem + (i & 1) * STAGE;
-    uint8_t* sx = smem + 2 * STAGE + (i & 1) * XSTAGE;
+    uint8_t* sx = smem + 2 * STAGE + (NORM ? i % STEPS : i & 1) * XSTAGE;
 #pragma unroll
     for (int jj = 0; jj < LW; ++jj) *reinterpret_cast<u4*>(sw + (wave + 4 * jj) * 1024 + 16 * lane) = wr[i % S][jj];
-    if constexpr (MX > 0) {
+    if constexpr (MX > 0 && !NORM) {
 #pragma unroll
       for (int j = 0; j < XU; ++j) *reinterpret_cast<u4*>(sx + xdst[j]) = xr[i % S][j][0][0];
     }
@@ -622,7 +786,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     }
     if constexpr (TPW > 1) {
       if (i % STEPS == STEPS - 1) {  // tile i / STEPS is complete
-        uint8_t* redp = smem + 2 * (STAGE + XSTAGE);
+        uint8_t* redp = smem + 2 * STAGE + XAREA;
         if constexpr (GLU) {
           if (i / STEPS == 0) {  // gate tile: keep the rounded values
             lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8,
@@ -631,7 +795,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
             lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8, [&](int, int b, int v, float o) {
               const int n = nw + n16, m = b * 16 + g * 4 + v;
               if (n < half && m < M)
-                sr.y[(size_t)m * half + n] = TO::from_f32(gelu_tanh(gate[b][v]) * TO::to_f32(TO::from_f32(o)));
+                sr.y[(size_t)m * half + n] =
+                    TO::from_f32(f32_round(gelu_tanh(gate[b][v]) * TO::to_f32(TO::from_f32(o))));
             });
           }
         } else {
@@ -644,7 +809,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
           lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, tile_row(i / STEPS + 1), N, M, sr, skind,
-                                  XF8 ? sg.xs : nullptr);
+                                  XF8 && !NORM ? sg.xs : nullptr);
+          if constexpr (NORM && XF8) pick_row_scales();
         }
       }
     }
@@ -697,10 +863,10 @@ static int seg_grid(GemvSegs& sg, int rows_per_wg) {
 template <typename T, typename TO, int FMT, bool XF8, int S>
 static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int N, hipStream_t st) {
 #define CEK_LDS(NT, MB, D) \
-  gemv_lds_kernel<T, TO, FMT, XF8, NT, MB, D, S><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M)
+  gemv_lds_kernel<T, TO, FMT, XF8, NT, MB, D, S><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
 #define CEK_LDS_T(NT, D, MX, TPW)                                                                          \
   gemv_lds_kernel<T, TO, FMT, XF8, NT, 1, D, S, MX, TPW><<<dim3(seg_grid(sg, 16 * (NT) * (TPW))), 256, 0, st>>>( \
-      x, sg, skind, M)
+      x, sg, skind, M, NormArgs{})
   constexpr bool SHORT = S >= 3 && S <= 5;
   constexpr bool MULTI = S == 4 || S == 5;  // multi-tile workgroups (K = 4096, 5120)
 #define CEK_LDS_TPW(NT, D, MX)                       \
@@ -782,7 +948,7 @@ static void launch_glu_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   sg.gstart[0] = 0;
   for (int i = 1; i <= MAX_SEGS; ++i) sg.gstart[i] = grid;
 #define CEK_GLU(D, MX) \
-  gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, 2, true><<<dim3(grid), 256, 0, st>>>(x, sg, skind, M)
+  gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, 2, true><<<dim3(grid), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
   if constexpr (!XF8) {
     if (M <= 4) {
       CEK_GLU(3, 4);
@@ -804,6 +970,92 @@ static int launch_glu(const void* x, GemvSegs& sg, int skind, int M, int d, int 
     case 4: launch_glu_steps<T, TO, FMT, XF8, 4>(x, sg, skind, M, d, st); break;
     case 5: launch_glu_steps<T, TO, FMT, XF8, 5>(x, sg, skind, M, d, st); break;
     default: return CEK_ERR_UNSUPPORTED;
+  }
+  return check_launch();
+}
+
+// add+RMSNorm (+ quant) fused into the GEMV (gemv_lds_kernel's NORM form):
+// e4m3 weights, prefetch depth 3, MX = 1 or 4 activation rows in LDS; with
+// gelu_and_mul also the GLU form (N = 2 d rows).  Two consecutive tiles per
+// workgroup from 384 tiles at K = 4096 / 5120, as for the plain GEMV.
+template <typename T, typename TO, bool XF8, int S, int MX>
+static void launch_norm_steps(GemvSegs& sg, const NormArgs& na, int skind, int M, int N, bool glu, hipStream_t st) {
+  if (glu) {
+    const int grid = (N / 2 + 15) / 16;
+    sg.gstart[0] = 0;
+    for (int i = 1; i <= MAX_SEGS; ++i) sg.gstart[i] = grid;
+    gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 2, true, true><<<dim3(grid), 256, 0, st>>>(
+        nullptr, sg, skind, M, na);
+    return;
+  }
+  if constexpr (S == 4 || S == 5) {
+    if ((N + 15) / 16 >= 384) {
+      gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 2, false, true><<<dim3(seg_grid(sg, 32)), 256, 0, st>>>(
+          nullptr, sg, skind, M, na);
+      return;
+    }
+  }
+  gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 1, false, true><<<dim3(seg_grid(sg, 16)), 256, 0, st>>>(
+      nullptr, sg, skind, M, na);
+}
+
+template <typename T, typename TO, bool XF8>
+static void launch_norm_t(GemvSegs& sg, const NormArgs& na, int skind, int M, int N, int K, bool glu, hipStream_t st) {
+  // one activation row (M = 1) or up to four
+  auto by_rows = [&](auto s) {
+    constexpr int S_ = decltype(s)::value;
+    if (M == 1) launch_norm_steps<T, TO, XF8, S_, 1>(sg, na, skind, M, N, glu, st);
+    else launch_norm_steps<T, TO, XF8, S_, 4>(sg, na, skind, M, N, glu, st);
+  };
+  if (K == 3072) by_rows(std::integral_constant<int, 3>{});
+  else if (K == 4096) by_rows(std::integral_constant<int, 4>{});
+  else by_rows(std::integral_constant<int, 5>{});
+}
+
+static bool overlaps(const void* a, const void* b, int64_t bytes) {
+  const char* pa = static_cast<const char*>(a);
+  const char* pb = static_cast<const char*>(b);
+  return pa < pb + bytes && pb < pa + bytes;
+}
+
+// The fused launch covers M <= 4 rows, K in {3072, 4096, 5120}, e4m3
+// weights, 16-byte aligned operands and side outputs that do not overlap the
+// inputs; CEK_ERR_UNSUPPORTED otherwise (the caller runs the norm, then the
+// GEMV).  q_out != null selects the quantising form (a8w8 GEMV: fp32
+// per-channel weight scales).
+int launch_norm_gemv(const NormArgs& na, const void* w, const void* scale, int skind, void* y, int64_t M,
+                     int64_t N, int64_t K, bool glu, int io_dtype, int fp8_fmt, hipStream_t st) {
+  const bool quant = na.q_out != nullptr;
+  if (M < 0 || N < 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
+  if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
+  if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
+  if (skind < 0 || skind == SK_F32_SCALAR) return CEK_ERR_INVALID;
+  if (quant && (fp8_fmt != CEK_E4M3 || skind != SK_F32 || !na.s_out || na.h_out)) return CEK_ERR_INVALID;
+  if (glu && N % 2) return CEK_ERR_INVALID;
+  if (M == 0) return CEK_OK;
+  if (!na.h || !na.r || !na.w || !na.r_out || !w || !scale || !y) return CEK_ERR_INVALID;
+  if (N * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
+  const int64_t rb = M * K * 2;  // bytes of one [M, K] activation matrix
+  if (N == 0 || M > 4 || (K != 3072 && K != 4096 && K != 5120) || fp8_fmt != CEK_E4M3) return CEK_ERR_UNSUPPORTED;
+  if (!aligned(na.h, 16) || !aligned(na.r, 16) || !aligned(na.w, 16) || !aligned(na.r_out, 16) || !aligned(w, 16) ||
+      (na.h_out && !aligned(na.h_out, 16)) || (quant && !aligned(na.q_out, 16)))
+    return CEK_ERR_UNSUPPORTED;
+  if (overlaps(na.r_out, na.r, rb) || overlaps(na.r_out, na.h, rb) ||
+      (na.h_out && (overlaps(na.h_out, na.r, rb) || overlaps(na.h_out, na.h, rb))))
+    return CEK_ERR_UNSUPPORTED;
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = static_cast<const uint8_t*>(w);
+  sg.s[0] = scale;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)N;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  if (quant) {
+    if (io_dtype == CEK_F16) launch_norm_t<F16, F16, true>(sg, na, SK_F32, m, n, k, glu, st);
+    else launch_norm_t<F16, BF16, true>(sg, na, SK_F32, m, n, k, glu, st);
+  } else {
+    if (io_dtype == CEK_F16) launch_norm_t<F16, F16, false>(sg, na, skind, m, n, k, glu, st);
+    else launch_norm_t<BF16, BF16, false>(sg, na, skind, m, n, k, glu, st);
   }
   return check_launch();
 }
@@ -987,6 +1239,17 @@ int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* s
 }
 
 }  // namespace cek
+
+extern "C" int cek_add_rms_norm_gemv_fp8(const void* hidden, const void* residual, const void* norm_weight, float eps,
+                                         void* residual_out, void* hidden_out, uint8_t* q_out, float* q_scale,
+                                         const void* w, const void* scale, void* y, int64_t M, int64_t N, int64_t K,
+                                         int gelu_and_mul, int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
+  cek::NormArgs na{static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(residual),
+                   static_cast<const uint16_t*>(norm_weight), static_cast<uint16_t*>(residual_out),
+                   static_cast<uint16_t*>(hidden_out), q_out, q_scale, eps};
+  return cek::launch_norm_gemv(na, w, scale, cek::scale_kind(scale_dtype), y, M, N, K, gelu_and_mul != 0, io_dtype,
+                               fp8_fmt, (hipStream_t)stream);
+}
 
 extern "C" int cek_gemv_fp8_gelu_and_mul(const void* x, const float* x_scale, const void* w, const void* scale,
                                          void* y, int64_t M, int64_t d, int64_t K, int io_dtype, int fp8_fmt,

@@ -19,8 +19,6 @@
 namespace cek {
 
 constexpr int NORM_THREADS = 256;
-constexpr float E4M3_MAX = 448.0f;
-constexpr float MIN_SCALE = 1.0f / (448.0f * 512.0f);
 
 // Workgroup-wide sum / max for NORM_THREADS threads (4 waves).
 __device__ inline float block_sum(float v, float* sh) {
@@ -42,10 +40,6 @@ __device__ inline float block_max(float v, float* sh) {
   return t;
 }
 
-__device__ inline float quant_scale(float amax) { return fmaxf(amax / E4M3_MAX, MIN_SCALE); }
-__device__ inline float quant_clamp(float v, float s) {
-  return fminf(fmaxf(v / s, -E4M3_MAX), E4M3_MAX);  // IEEE divide (no fast math)
-}
 
 // Vector path: H % 8 == 0, 16-byte aligned rows, H <= 8 * NORM_THREADS * UPT.
 template <typename T, int UPT, bool QUANT>
@@ -93,8 +87,8 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(
       u4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float n0 = T::to_f32(rv[j][e] & 0xFFFF) * inv * T::to_f32(wv[e] & 0xFFFF);
-        float n1 = T::to_f32(rv[j][e] >> 16) * inv * T::to_f32(wv[e] >> 16);
+        float n0 = f32_round(T::to_f32(rv[j][e] & 0xFFFF) * inv * T::to_f32(wv[e] & 0xFFFF));
+        float n1 = f32_round(T::to_f32(rv[j][e] >> 16) * inv * T::to_f32(wv[e] >> 16));
         uint16_t b0 = T::from_f32(n0), b1 = T::from_f32(n1);
         if (QUANT) amax = fmaxf(amax, fmaxf(fabsf(T::to_f32(b0)), fabsf(T::to_f32(b1))));
         o[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
@@ -145,7 +139,7 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_generic_kernel(
   const float inv = rsqrtf(ss / (float)H + eps);
   float amax = 0.f;
   for (int i = threadIdx.x; i < H; i += NORM_THREADS) {
-    uint16_t b = T::from_f32(T::to_f32(rr[i]) * inv * T::to_f32(weight[i]));
+    uint16_t b = T::from_f32(f32_round(T::to_f32(rr[i]) * inv * T::to_f32(weight[i])));
     if (QUANT) amax = fmaxf(amax, fabsf(T::to_f32(b)));
     else hr[i] = b;
   }
@@ -154,7 +148,7 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_generic_kernel(
   const float s = quant_scale(amax);
   if (threadIdx.x == 0) qscale[row] = s;
   for (int i = threadIdx.x; i < H; i += NORM_THREADS) {
-    uint16_t b = T::from_f32(T::to_f32(rr[i]) * inv * T::to_f32(weight[i]));
+    uint16_t b = T::from_f32(f32_round(T::to_f32(rr[i]) * inv * T::to_f32(weight[i])));
     q[(size_t)row * H + i] = (uint8_t)f32_to_e4m3(quant_clamp(T::to_f32(b), s));
   }
 }

@@ -348,3 +348,110 @@ void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Ten
                             (float)theta, is_neox ? 1 : 0, io_code(q.scalar_type()), current_stream(q)),
            op);
 }
+
+// ---- add+RMSNorm (+ quant) fused into the GEMV that consumes it ----
+// residual_out = hidden + residual; the normed rows (or their e4m3 codes and
+// scales) feed the GEMV (or the gate/up GEMV with gelu_and_mul).  Decode
+// batches of up to four rows run as one launch; other shapes, and a
+// residual_out that aliases the inputs, run the norm op on a copy and then
+// the GEMV op (the same values).
+static void check_norm_gemv_common(const at::Tensor& h, const at::Tensor& r, const at::Tensor& nw,
+                                   const at::Tensor& r_out, const at::Tensor& w, const at::Tensor& ws,
+                                   const at::Tensor& y, bool glu, const char* op, int64_t& M, int64_t& N,
+                                   int64_t& K) {
+  check_norm(h, r, nw, op);
+  TORCH_CHECK(r_out.scalar_type() == h.scalar_type() && r_out.numel() == h.numel(), op,
+              ": residual_out must match hidden_states");
+  check_device(r_out, h, op, "residual_out");
+  check_contig(r_out, op, "residual_out");
+  check_fp8_weight(w, op);
+  check_device(w, h, op, "weight");
+  check_device(ws, h, op, "weight_scale");
+  check_device(y, h, op, "output");
+  check_contig(w, op, "weight");
+  check_contig(ws, op, "weight_scale");
+  check_contig(y, op, "output");
+  K = h.size(-1);
+  M = h.numel() / K;
+  TORCH_CHECK(w.dim() == 2 && w.size(1) == K && w.size(0) > 0, op, ": weight must be [N, K] with K = hidden size");
+  N = w.size(0);
+  TORCH_CHECK(!glu || N % 2 == 0, op, ": with gelu_and_mul the weight must have 2d rows");
+  TORCH_CHECK(y.scalar_type() == h.scalar_type(), op, ": output must have the dtype of hidden_states");
+  TORCH_CHECK(y.numel() == M * (glu ? N / 2 : N), op, ": output must be [M, ", glu ? "d" : "N", "]");
+}
+
+void esimd_fused_add_rms_norm_gemv_fp8(at::Tensor hidden_states, at::Tensor residual, at::Tensor weight, double eps,
+                                       at::Tensor residual_out, at::Tensor w, at::Tensor w_scale, at::Tensor output,
+                                       bool gelu_and_mul) {
+  const char* op = "esimd_fused_add_rms_norm_gemv_fp8";
+  int64_t M, N, K;
+  check_norm_gemv_common(hidden_states, residual, weight, residual_out, w, w_scale, output, gelu_and_mul, op, M, N, K);
+  const auto sdt = w_scale.scalar_type();
+  TORCH_CHECK(sdt == at::ScalarType::Half || sdt == at::ScalarType::BFloat16 || sdt == at::ScalarType::Float, op,
+              ": weight_scale must be fp16, bf16 or fp32");
+  TORCH_CHECK(w_scale.numel() == N, op, ": weight_scale must hold N elements");
+  const int scale_code = sdt == at::ScalarType::Float ? CEK_F32 : (sdt == at::ScalarType::Half ? CEK_F16 : CEK_BF16);
+  c10::OptionalDeviceGuard guard(hidden_states.device());
+  void* st = current_stream(hidden_states);
+  const int io = io_code(hidden_states.scalar_type());
+  const int fmt = fp8_code(w);
+  int rc = cek_add_rms_norm_gemv_fp8(hidden_states.data_ptr(), residual.data_ptr(), weight.data_ptr(), (float)eps,
+                                     residual_out.data_ptr(), nullptr, nullptr, nullptr, w.data_ptr(),
+                                     w_scale.data_ptr(), output.data_ptr(), M, N, K, gelu_and_mul ? 1 : 0, io, fmt,
+                                     scale_code, st);
+  if (rc != CEK_ERR_UNSUPPORTED) {
+    check_rc(rc, op);
+    return;
+  }
+  // two launches: the norm in place on copies, then the GEMV
+  at::Tensor x = hidden_states.clone();
+  if (!residual_out.is_same(residual)) residual_out.copy_(residual);
+  check_rc(cek_fused_add_rms_norm(x.data_ptr(), residual_out.data_ptr(), weight.data_ptr(), M, K, (float)eps, io, st),
+           op);
+  if (gelu_and_mul) esimd_gemv_fp8_gelu_and_mul(x.view({M, K}), w, w_scale, output.view({M, N / 2}));
+  else run_gemv(x, w, w_scale, output, N, K, false, op);
+}
+
+void esimd_fused_add_rms_norm_quant_gemv_fp8(at::Tensor hidden_states, at::Tensor residual, at::Tensor weight,
+                                             double eps, at::Tensor residual_out, at::Tensor out_q,
+                                             at::Tensor out_scale, at::Tensor b, at::Tensor b_scale,
+                                             at::Tensor output, bool gelu_and_mul) {
+  const char* op = "esimd_fused_add_rms_norm_quant_gemv_fp8";
+  int64_t M, N, K;
+  check_norm_gemv_common(hidden_states, residual, weight, residual_out, b, b_scale, output, gelu_and_mul, op, M, N, K);
+  TORCH_CHECK(b.scalar_type() != at::ScalarType::Float8_e5m2, op, ": b must be e4m3");
+  TORCH_CHECK(b_scale.scalar_type() == at::ScalarType::Float && b_scale.numel() == N, op,
+              ": b_scale must be fp32 [N]");
+  check_quant_out(hidden_states, out_q, out_scale, M, op);
+  c10::OptionalDeviceGuard guard(hidden_states.device());
+  void* st = current_stream(hidden_states);
+  const int io = io_code(hidden_states.scalar_type());
+  auto* q = static_cast<uint8_t*>(out_q.data_ptr());
+  auto* qs = static_cast<float*>(out_scale.data_ptr());
+  int rc = cek_add_rms_norm_gemv_fp8(hidden_states.data_ptr(), residual.data_ptr(), weight.data_ptr(), (float)eps,
+                                     residual_out.data_ptr(), nullptr, q, qs, b.data_ptr(), b_scale.data_ptr(),
+                                     output.data_ptr(), M, N, K, gelu_and_mul ? 1 : 0, io, CEK_E4M3, CEK_F32, st);
+  if (rc != CEK_ERR_UNSUPPORTED) {
+    check_rc(rc, op);
+    return;
+  }
+  // two launches: norm + quant (hidden only read), then the a8w8 product
+  if (!residual_out.is_same(residual)) residual_out.copy_(residual);
+  check_rc(cek_fused_add_rms_norm_quant_fp8(hidden_states.data_ptr(), residual_out.data_ptr(), weight.data_ptr(), M, K,
+                                            (float)eps, io, q, qs, st),
+           op);
+  const auto* bp = static_cast<const uint8_t*>(b.data_ptr());
+  const auto* sb = static_cast<const float*>(b_scale.data_ptr());
+  if (!gelu_and_mul) {
+    check_rc(cek_gemm_fp8_a8w8(q, qs, bp, sb, output.data_ptr(), M, N, K, io, st), op);
+    return;
+  }
+  rc = M <= 16 ? cek_gemv_fp8_gelu_and_mul(q, qs, bp, sb, output.data_ptr(), M, N / 2, K, io, CEK_E4M3, CEK_F32, st)
+               : CEK_ERR_UNSUPPORTED;
+  if (rc == CEK_ERR_UNSUPPORTED) {
+    at::Tensor gu = at::empty({M, N}, output.options());
+    check_rc(cek_gemm_fp8_a8w8(q, qs, bp, sb, gu.data_ptr(), M, N, K, io, st), op);
+    rc = cek_gelu_and_mul(output.data_ptr(), gu.data_ptr(), M, N / 2, N, N / 2, io, st);
+  }
+  check_rc(rc, op);
+}

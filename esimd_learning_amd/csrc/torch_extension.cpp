@@ -45,6 +45,15 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
         "Tensor(a!) output) -> ()");
   m.impl("esimd_gemv_fp8_gelu_and_mul", c10::DispatchKey::CUDA, &esimd_gemv_fp8_gelu_and_mul);
 
+  m.def("esimd_fused_add_rms_norm_gemv_fp8(Tensor hidden_states, Tensor residual, Tensor weight, float eps, "
+        "Tensor(a!) residual_out, Tensor w, Tensor w_scale, Tensor(b!) output, bool gelu_and_mul=False) -> ()");
+  m.impl("esimd_fused_add_rms_norm_gemv_fp8", c10::DispatchKey::CUDA, &esimd_fused_add_rms_norm_gemv_fp8);
+
+  m.def("esimd_fused_add_rms_norm_quant_gemv_fp8(Tensor hidden_states, Tensor residual, Tensor weight, "
+        "float eps, Tensor(a!) residual_out, Tensor(b!) out_q, Tensor(c!) out_scale, Tensor b, Tensor b_scale, "
+        "Tensor(d!) output, bool gelu_and_mul=False) -> ()");
+  m.impl("esimd_fused_add_rms_norm_quant_gemv_fp8", c10::DispatchKey::CUDA, &esimd_fused_add_rms_norm_quant_gemv_fp8);
+
   m.def("esimd_qk_norm_rope(Tensor(a!) q, Tensor(b!) k, Tensor q_weight, Tensor k_weight, "
         "Tensor positions, float eps, float theta, bool is_neox) -> ()");
   m.impl("esimd_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_qk_norm_rope);

@@ -38,6 +38,15 @@ void esimd_per_token_quant_fp8(at::Tensor input, at::Tensor out_q, at::Tensor ou
 
 void esimd_gelu_and_mul(at::Tensor out, at::Tensor input);
 
+// add+RMSNorm (+ per-token e4m3 quant) fused into the GEMV it feeds.
+void esimd_fused_add_rms_norm_gemv_fp8(at::Tensor hidden_states, at::Tensor residual, at::Tensor weight, double eps,
+                                       at::Tensor residual_out, at::Tensor w, at::Tensor w_scale, at::Tensor output,
+                                       bool gelu_and_mul);
+void esimd_fused_add_rms_norm_quant_gemv_fp8(at::Tensor hidden_states, at::Tensor residual, at::Tensor weight,
+                                             double eps, at::Tensor residual_out, at::Tensor out_q,
+                                             at::Tensor out_scale, at::Tensor b, at::Tensor b_scale,
+                                             at::Tensor output, bool gelu_and_mul);
+
 // Gate/up GEMV over a merged [2d, K] weight with gelu_and_mul fused.
 void esimd_gemv_fp8_gelu_and_mul(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output);
 

@@ -112,6 +112,32 @@ def esimd_gemv_fp8_gelu_and_mul(
     _ops.esimd_gemv_fp8_gelu_and_mul(input, weight, weight_scale, output)
 
 
+def esimd_fused_add_rms_norm_gemv_fp8(
+    hidden_states: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+    residual_out: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, output: torch.Tensor,
+    gelu_and_mul: bool = False,
+) -> None:
+    """residual_out = hidden_states + residual; output = the fp8 GEMV of
+    rmsnorm(residual_out) * weight (with ``gelu_and_mul``: w holds gate then up
+    rows and output [M, d] is gelu_tanh(gate) * up).  One launch for up to
+    four rows; the values equal esimd_fused_add_rms_norm_batched followed by
+    the GEMV.  hidden_states and residual are only read."""
+    _ops.esimd_fused_add_rms_norm_gemv_fp8(hidden_states, residual, weight, eps, residual_out, w, w_scale, output,
+                                           gelu_and_mul)
+
+
+def esimd_fused_add_rms_norm_quant_gemv_fp8(
+    hidden_states: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+    residual_out: torch.Tensor, out_q: torch.Tensor, out_scale: torch.Tensor,
+    b: torch.Tensor, b_scale: torch.Tensor, output: torch.Tensor, gelu_and_mul: bool = False,
+) -> None:
+    """esimd_fused_add_rms_norm_quant_fp8 (into residual_out, out_q, out_scale)
+    followed by esimd_gemm_fp8_a8w8 (or its gelu_and_mul form), one launch
+    for up to four rows."""
+    _ops.esimd_fused_add_rms_norm_quant_gemv_fp8(hidden_states, residual, weight, eps, residual_out, out_q,
+                                                 out_scale, b, b_scale, output, gelu_and_mul)
+
+
 def esimd_qk_norm_rope(
     q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
     positions: torch.Tensor, eps: float, theta: float = 10000.0, is_neox: bool = True,

@@ -141,6 +141,29 @@ int cek_gelu_and_mul(void* out, const void* x, int64_t T, int64_t d,
                      int64_t x_stride, int64_t out_stride, int io_dtype, void* stream);
 
 /*
+ * NEW: fused residual add + RMSNorm (+ per-token e4m3 quantisation) feeding
+ * the fp8 GEMV, in one launch (no counterpart in the reference: it is
+ * esimd_fused_add_rms_norm_batched, csrc/xpu/esimd_kernel.sycl:92-109,
+ * followed by esimd_gemv_fp8_pern, :22-53):
+ *   residual_out = Out(hidden + residual)                      [M, K]
+ *   x            = Out(residual_out * rsqrt(mean((hidden + residual)^2) + eps) * norm_weight)
+ *   q_out == NULL: hidden_out = x (if not NULL); y = GEMV(x, W, scale)
+ *   q_out != NULL: q_out, q_scale = per-token e4m3 quant of x (the formula
+ *                  of cek_fused_add_rms_norm_quant_fp8); y = a8w8 GEMV of
+ *                  the codes (W e4m3, scale fp32 [N])
+ * with gelu_and_mul != 0: W holds 2d = N rows (gate, then up) and y [M, d]
+ * is gelu_tanh(gate) * up, as cek_gemv_fp8_gelu_and_mul.  Every value
+ * equals the unfused ops', bit for bit.  residual_out and hidden_out must
+ * not overlap hidden or residual.  Covers M <= 4, K in {3072, 4096, 5120},
+ * e4m3 weights and 16-byte aligned operands; CEK_ERR_UNSUPPORTED otherwise,
+ * for the caller to run the norm and the GEMV as two launches.
+ */
+int cek_add_rms_norm_gemv_fp8(const void* hidden, const void* residual, const void* norm_weight, float eps,
+                              void* residual_out, void* hidden_out, uint8_t* q_out, float* q_scale,
+                              const void* w, const void* scale, void* y, int64_t M, int64_t N, int64_t K,
+                              int gelu_and_mul, int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+
+/*
  * NEW: gate/up GEMV with gelu_and_mul fused into its epilogue (no
  * counterpart in the reference: it is esimd_gemv_fp8_pern over a merged
  * [2d, K] gate/up weight, csrc/xpu/esimd_kernel.sycl:22-53, followed by

@@ -99,6 +99,22 @@ def test_host_rejects_invalid_arguments():
     assert glu(p, None, p, p, p, 4, 64, 4100, 0, 0, 2, None) == U
     assert glu(C.c_void_p(24), None, p, p, p, 4, 64, 4096, 0, 0, 2, None) == U        # alignment
     assert glu(None, None, None, None, None, 0, 64, 4096, 0, 0, 2, None) == cabi.CEK_OK
+    # add+RMSNorm fused into the GEMV: quant form needs e4m3 weights, fp32
+    # scales and no hidden_out; unsupported shapes and aliasing side outputs
+    # are left to the caller's two launches
+    ng = lib.cek_add_rms_norm_gemv_fp8
+    q = C.c_void_p(4096)
+    assert ng(p, p, p, 1e-6, q, None, p, p, p, p, p, 4, 64, 4096, 0, 0, 1, 2, None) == E   # quant with e5m2
+    assert ng(p, p, p, 1e-6, q, None, p, None, p, p, p, 4, 64, 4096, 0, 0, 0, 2, None) == E  # no scale output
+    assert ng(p, p, p, 1e-6, q, p, p, p, p, p, p, 4, 64, 4096, 0, 0, 0, 2, None) == E      # quant with hidden_out
+    assert ng(p, p, p, 1e-6, q, None, None, None, p, p, p, 4, 65, 4096, 1, 0, 0, 2, None) == E  # odd 2d
+    assert ng(p, None, p, 1e-6, q, None, None, None, p, p, p, 4, 64, 4096, 0, 0, 0, 2, None) == E  # null residual
+    assert ng(p, p, p, 1e-6, q, None, None, None, p, p, p, 5, 64, 4096, 0, 0, 0, 2, None) == U   # M > 4
+    assert ng(p, p, p, 1e-6, q, None, None, None, p, p, p, 4, 64, 2048, 0, 0, 0, 2, None) == U   # K
+    assert ng(p, p, p, 1e-6, q, None, None, None, p, p, p, 4, 64, 4096, 0, 0, 1, 2, None) == U   # e5m2
+    assert ng(p, p, p, 1e-6, p, None, None, None, p, p, p, 4, 64, 4096, 0, 0, 0, 2, None) == U   # r_out aliases
+    assert ng(None, None, None, 1e-6, None, None, None, None, None, None, None, 0, 64, 4096, 0, 0, 0, 2,
+              None) == cabi.CEK_OK
     # empty problems are no-ops that succeed without touching memory
     assert lib.cek_gemv_fp8_pern(None, None, None, None, 0, 8, 64, 0, 0, 2, None) == cabi.CEK_OK
     assert lib.cek_fused_add_rms_norm(None, None, None, 0, 64, 1e-6, 0, None) == cabi.CEK_OK

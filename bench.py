@@ -229,7 +229,8 @@ def bench_norm_quant_gemv(ops, torch, reps=50, N=6144):
     """fused add+RMSNorm+per-token e4m3 quant, then the
     fp8 x fp8 GEMV/GEMM to N = 6144 on its codes and scales.  Per (T, H):
     the two kernels' times (each a graph of `reps` launches, event-timed;
-    the GEMV rotates over > 2 GB of weights) and the pair back to back."""
+    the GEMV rotates over > 2 GB of weights), the pair back to back, and for
+    T <= 4 the single launch that computes the same outputs (fused_us)."""
     from esimd_learning_amd import synthetic
     dev = "cuda:0"
     stream = torch.cuda.Stream()
@@ -259,9 +260,17 @@ def bench_norm_quant_gemv(ops, torch, reps=50, N=6144):
             for i in range(reps):
                 pair += [norm, gemv[i % copies]]
             _, p_ms, _ = time_graph(pair, torch, stream, warm_s=0.05)
-            rows.append({"T": T, "H": H, "norm_quant_us": round(n_ms * 1e3 / reps, 2),
-                         "gemv_us": round(g_ms * 1e3 / (2 * copies), 2),
-                         "pair_us": round(p_ms * 1e3 / reps, 2)})
+            row = {"T": T, "H": H, "norm_quant_us": round(n_ms * 1e3 / reps, 2),
+                   "gemv_us": round(g_ms * 1e3 / (2 * copies), 2),
+                   "pair_us": round(p_ms * 1e3 / reps, 2)}
+            if T <= 4:
+                # the same outputs from one launch: norm + quant in the GEMV's prologue
+                r_out = torch.empty_like(r)
+                fused = [(lambda W=W: ops.esimd_fused_add_rms_norm_quant_gemv_fp8(h, r, w, 1e-6, r_out, q, sa, W,
+                                                                                    sbd, y)) for W in Ws]
+                _, f_ms, _ = time_graph(fused * 2, torch, stream, warm_s=0.05)
+                row["fused_us"] = round(f_ms * 1e3 / (2 * copies), 2)
+            rows.append(row)
         del Ws, Wd
         torch.cuda.empty_cache()
     return rows
@@ -336,15 +345,17 @@ def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
     return rows
 
 
-def bench_layer(torch, steps, M=4, act_fp8=False, fuse_glu=True):
+def bench_layer(torch, steps, M=4, act_fp8=False, fuse_glu=True, fuse_norm=False, floor=True):
     """one Gemma-style decoder-layer decode step, HIP-graph replayed
-    (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations; fuse_glu: gate/up
-    and gelu_and_mul in one launch)."""
+    (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations; fuse_glu:
+    gelu_and_mul in the gate/up GEMV's epilogue; fuse_norm: both add+RMSNorms
+    in the prologue of the GEMV they feed; floor: also time the read probe
+    over the step's weights)."""
     from esimd_learning_amd import synthetic
     from esimd_learning_amd.layer import GemmaDecodeLayer
     dev = "cuda:0"
     p = synthetic.gemma_layer(seed=10)
-    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse_glu)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse_glu, fuse_norm=fuse_norm)
     h = synthetic.activations(M, p["hidden"], seed=20).to(dev)
     r = synthetic.activations(M, p["hidden"], seed=21).to(dev)
     pos = synthetic.positions(M, seed=22).to(dev)
@@ -363,6 +374,8 @@ def bench_layer(torch, steps, M=4, act_fp8=False, fuse_glu=True):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / steps
     wb = layer.weight_bytes()
+    if not floor:
+        return {"us_per_step": round(us, 2)}
     # the four weight matrices read once each by cek_hbm_read_probe, captured
     # and replayed the same way: the one-pass read floor of a step's GEMVs
     from esimd_learning_amd import cabi
@@ -518,12 +531,13 @@ def main():
     if not a.no_layer:
         out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))
         log(f"layer: {out['decoder_layer']['us_per_step']} us/step, {out['decoder_layer']['weight_GBps']} GB/s")
-        fp8 = bench_layer(torch, max(20, a.steps // 4), act_fp8=True)
-        out["decoder_layer"]["act_fp8_us_per_step"] = fp8["us_per_step"]
-        log(f"layer, e4m3 activation hand-off: {fp8['us_per_step']} us/step")
-        unf = bench_layer(torch, max(20, a.steps // 4), fuse_glu=False)
-        out["decoder_layer"]["unfused_glu_us_per_step"] = unf["us_per_step"]
-        log(f"layer, gate/up GEMV and gelu_and_mul as two launches: {unf['us_per_step']} us/step")
+        ls = max(20, a.steps // 4)
+        variants = {"act_fp8_us_per_step": dict(act_fp8=True),
+                    "unfused_us_per_step": dict(fuse_glu=False),
+                    "norm_fused_us_per_step": dict(fuse_norm=True)}
+        for key, kw in variants.items():
+            out["decoder_layer"][key] = bench_layer(torch, ls, floor=False, **kw)["us_per_step"]
+            log(f"layer {key}: {out['decoder_layer'][key]} us/step")
     if not a.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch)

@@ -2,17 +2,24 @@
 
     h1, r1 = add_rmsnorm(hidden, residual, w_in)          esimd_fused_add_rms_norm_batched
     qkv    = h1 @ Wqkv^T * sqkv                           esimd_gemv_fp8_pern
+                                   (the two as one launch: esimd_fused_add_rms_norm_gemv_fp8)
     q, k   = per-head RMSNorm + RoPE (in place in qkv)     esimd_qk_norm_rope
     a      = attention(q, k, v)        -- out of scope: q stands in for its output
     o      = a @ Wo^T * so                                esimd_gemv_fp8_pern
     h2, r2 = add_rmsnorm(o, r1, w_post)                   esimd_fused_add_rms_norm_batched
     g      = gelu_tanh(h2 @ Wg^T * sg) * (h2 @ Wu^T * su) esimd_gemv_fp8_gelu_and_mul
+                                   (the two as one launch: esimd_fused_add_rms_norm_gemv_fp8)
     out    = g @ Wd^T * sd                                esimd_gemv_fp8_pern
 
 The gate/up projection and gelu_and_mul run as one launch (Wgu = [Wg; Wu],
 the GEMV's epilogue applies gelu_tanh(gate) * up to the rounded outputs);
 ``fuse_glu=False`` runs them as esimd_gemv_fp8_pern into [M, 2d] followed by
-esimd_gelu_and_mul, which gives the same values.
+esimd_gelu_and_mul, which gives the same values.  With ``fuse_norm`` (up to
+four rows) each add+RMSNorm runs in the prologue of the GEMV it feeds; r1 is
+then kept in a buffer of the layer, hidden is only read, and residual
+receives r2 as before.  It is off by default: every workgroup of the GEMV
+then normalises the rows itself, which at M = 4 over the 768 and 1536
+workgroups of QKV and gate/up costs more than the norm launch it saves.
 
 With ``act_fp8=True`` the two norm -> GEMV hand-offs carry e4m3 activations
 instead of fp16: esimd_fused_add_rms_norm_quant_fp8 writes per-token codes
@@ -30,7 +37,8 @@ import torch
 
 
 class GemmaDecodeLayer:
-    def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False, fuse_glu=True):
+    def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False, fuse_glu=True,
+                 fuse_norm=False):
         from . import ops as _load_ops
         self.ops = _load_ops()
         p = params
@@ -54,6 +62,8 @@ class GemmaDecodeLayer:
         self.out = mk(self.hidden)
         self.act_fp8 = act_fp8
         self.fuse_glu = fuse_glu
+        self.fuse_norm = fuse_norm and M <= 4   # the fused launch covers up to four rows
+        self.r_mid = mk(self.hidden)            # r1 between the two fused norms
         if act_fp8:
             if self.Wqkv.dtype != torch.float8_e4m3fn or self.Wgu.dtype != torch.float8_e4m3fn:
                 raise ValueError("act_fp8 needs e4m3 weights")
@@ -69,6 +79,8 @@ class GemmaDecodeLayer:
     def step(self, hidden, residual, positions):
         """hidden, residual: [M, hidden] (residual updated in place); returns out."""
         o, hd, nq, nk = self.ops, self.hd, self.nq, self.nk
+        if self.fuse_norm:
+            return self._step_fused(hidden, residual, positions)
         if self.act_fp8:
             o.esimd_fused_add_rms_norm_quant_fp8(hidden, residual, self.w_in, self.eps, self.q8, self.s8)
             o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wqkv8, self.sqkv32, self.qkv)
@@ -93,6 +105,31 @@ class GemmaDecodeLayer:
             else:
                 o.esimd_gemv_fp8_pern(self.o, self.Wgu, self.sgu, self.gu, 2 * self.mlp, self.hidden)
         if not self.fuse_glu:
+            o.esimd_gelu_and_mul(self.act, self.gu)
+        o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
+        return self.out
+
+    def _step_fused(self, hidden, residual, positions):
+        o, hd, nq, nk = self.ops, self.hd, self.nq, self.nk
+        if self.act_fp8:
+            o.esimd_fused_add_rms_norm_quant_gemv_fp8(hidden, residual, self.w_in, self.eps, self.r_mid, self.q8,
+                                                      self.s8, self.Wqkv8, self.sqkv32, self.qkv)
+        else:
+            o.esimd_fused_add_rms_norm_gemv_fp8(hidden, residual, self.w_in, self.eps, self.r_mid, self.Wqkv,
+                                                self.sqkv, self.qkv)
+        o.esimd_qk_norm_rope(self.qkv[:, : nq * hd], self.qkv[:, nq * hd:(nq + nk) * hd], self.qw, self.kw,
+                             positions, self.eps, self.theta, True)
+        self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
+        o.esimd_gemv_fp8_pern(self.attn, self.Wo, self.so, self.o, self.hidden, nq * hd)
+        glu = self.fuse_glu
+        y = self.act if glu else self.gu
+        if self.act_fp8:
+            o.esimd_fused_add_rms_norm_quant_gemv_fp8(self.o, self.r_mid, self.w_post, self.eps, residual, self.q8,
+                                                      self.s8, self.Wgu8, self.sgu32, y, glu)
+        else:
+            o.esimd_fused_add_rms_norm_gemv_fp8(self.o, self.r_mid, self.w_post, self.eps, residual, self.Wgu,
+                                                self.sgu, y, glu)
+        if not glu:
             o.esimd_gelu_and_mul(self.act, self.gu)
         o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
         return self.out

@@ -27,13 +27,13 @@ SMALL = dict(hidden=512, n_q=4, n_kv=2, head_dim=64, mlp=1024)
 CONFIG5 = dict(hidden=3072, n_q=16, n_kv=16, head_dim=256, mlp=24576)
 
 
-@pytest.mark.parametrize("fuse_glu", [True, False])
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("act_fp8", [False, True])
-@pytest.mark.parametrize("dims,M", [(SMALL, 3), (CONFIG5, 4)])
-def test_decoder_step_vs_oracle(ops, dev, dims, M, act_fp8, fuse_glu):
-    _say(f"decoder step M={M} {dims} act_fp8={act_fp8} fuse_glu={fuse_glu}")
+@pytest.mark.parametrize("dims,M", [(SMALL, 3), (CONFIG5, 4), (SMALL, 6)])
+def test_decoder_step_vs_oracle(ops, dev, dims, M, act_fp8, fused):
+    _say(f"decoder step M={M} {dims} act_fp8={act_fp8} fused={fused}")
     p = synthetic.gemma_layer(seed=10, **dims)
-    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse_glu)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fused, fuse_norm=fused)
     h = synthetic.activations(M, dims["hidden"], seed=20)
     r = synthetic.activations(M, dims["hidden"], seed=21)
     pos = synthetic.positions(M, seed=22)
@@ -45,12 +45,13 @@ def test_decoder_step_vs_oracle(ops, dev, dims, M, act_fp8, fuse_glu):
     assert_close_fp(out.cpu(), ref_out, "layer output")
 
 
+@pytest.mark.parametrize("fuse_norm", [False, True])
 @pytest.mark.parametrize("act_fp8", [False, True])
-def test_decoder_step_graph_replays(ops, dev, act_fp8):
+@pytest.mark.parametrize("dims", [SMALL, CONFIG5])
+def test_decoder_step_graph_replays(ops, dev, act_fp8, fuse_norm, dims):
     M = 4
-    dims = SMALL
     p = synthetic.gemma_layer(seed=11, **dims)
-    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8)
+    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_norm=fuse_norm)
     h0 = synthetic.activations(M, dims["hidden"], seed=30).to(dev)
     r0 = synthetic.activations(M, dims["hidden"], seed=31).to(dev)
     pos = synthetic.positions(M, seed=32).to(dev)
@@ -72,13 +73,14 @@ def test_decoder_step_graph_replays(ops, dev, act_fp8):
 
 
 @pytest.mark.parametrize("act_fp8", [False, True])
-def test_decoder_step_fused_glu_equals_unfused(ops, dev, act_fp8):
-    """The fused gate/up + gelu launch gives the step the unfused ops give, bit for bit."""
+def test_decoder_step_fused_equals_unfused(ops, dev, act_fp8):
+    """The fused launches (norm into the GEMV prologue, gelu into the gate/up
+    epilogue) give the step the unfused ops give, bit for bit."""
     M, dims = 4, CONFIG5
     p = synthetic.gemma_layer(seed=12, **dims)
     outs = []
     for fuse in (True, False):
-        layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse)
+        layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse, fuse_norm=fuse)
         h = synthetic.activations(M, dims["hidden"], seed=40).to(dev)
         r = synthetic.activations(M, dims["hidden"], seed=41).to(dev)
         outs.append((layer.step(h, r, synthetic.positions(M, seed=42).to(dev)).clone(), r.clone(),

@@ -54,6 +54,38 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   __shared__ float cs[256], sn[256];
   const int t = blockIdx.x;
   const int half = hd >> 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h0 = (int)blockIdx.y * heads_per_wg + wave;
+  const int h_end = min(nq + nk, ((int)blockIdx.y + 1) * heads_per_wg);
+  auto head = [&](int h) {
+    return h < nq ? q + (size_t)t * qs + (size_t)h * hd : k + (size_t)t * ks + (size_t)(h - nq) * hd;
+  };
+  // This lane's pairs p = lane + 64 j of a head: element indices, raw values
+  // and norm weights (0 past the head).
+  int ia[PPL], ib[PPL];
+  uint16_t ra[PPL], rb[PPL], wa[PPL], wb[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int p = lane + 64 * j;
+    ia[j] = neox ? p : 2 * p;
+    ib[j] = neox ? p + half : 2 * p + 1;
+  }
+  auto load_head = [&](int h) {
+    const uint16_t* v = head(h);
+    const uint16_t* w = h < nq ? qw : kw;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      const bool in = lane + 64 * j < half;
+      ra[j] = in ? v[ia[j]] : 0;
+      rb[j] = in ? v[ib[j]] : 0;
+      wa[j] = in ? w[ia[j]] : 0;
+      wb[j] = in ? w[ib[j]] : 0;
+    }
+  };
+  // The first head's loads are issued before the fp64 cos/sin table, so
+  // their latency overlaps its arithmetic (the barrier below waits for both).
+  if (h0 < h_end) load_head(h0);
+  asm volatile("" ::: "memory");
   const double pos = (double)positions[t];
   const double lt = log2((double)theta);
   for (int i = threadIdx.x; i < half; i += 256) {
@@ -65,27 +97,15 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int h_end = min(nq + nk, ((int)blockIdx.y + 1) * heads_per_wg);
-  for (int h = (int)blockIdx.y * heads_per_wg + wave; h < h_end; h += 4) {
-    const bool isq = h < nq;
-    uint16_t* v = isq ? q + (size_t)t * qs + (size_t)h * hd : k + (size_t)t * ks + (size_t)(h - nq) * hd;
-    const uint16_t* w = isq ? qw : kw;
+  for (int h = h0; h < h_end; h += 4) {
+    if (h != h0) load_head(h);
+    uint16_t* v = head(h);
     float a[PPL], b[PPL];
-    int ia[PPL], ib[PPL];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
-      const int p = lane + 64 * j;
-      ia[j] = neox ? p : 2 * p;
-      ib[j] = neox ? p + half : 2 * p + 1;
-      if (p < half) {
-        a[j] = T::to_f32(v[ia[j]]);
-        b[j] = T::to_f32(v[ib[j]]);
-      } else {
-        a[j] = 0.f;
-        b[j] = 0.f;
-      }
+      a[j] = T::to_f32(ra[j]);
+      b[j] = T::to_f32(rb[j]);
       ss = fmaf(a[j], a[j], ss);
       ss = fmaf(b[j], b[j], ss);
     }
@@ -96,8 +116,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       const int p = lane + 64 * j;
       if (p >= half) continue;
       // norm, then round to the activation type before the rotation
-      const float na = T::to_f32(T::from_f32(a[j] * inv * T::to_f32(w[ia[j]])));
-      const float nb = T::to_f32(T::from_f32(b[j] * inv * T::to_f32(w[ib[j]])));
+      const float na = T::to_f32(T::from_f32(a[j] * inv * T::to_f32(wa[j])));
+      const float nb = T::to_f32(T::from_f32(b[j] * inv * T::to_f32(wb[j])));
       const float c = cs[p], s = sn[p];
       v[ia[j]] = T::from_f32(na * c - nb * s);
       v[ib[j]] = T::from_f32(nb * c + na * s);

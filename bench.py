@@ -345,37 +345,53 @@ def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
     return rows
 
 
-def bench_layer(torch, steps, M=4, act_fp8=False, fuse_glu=True, fuse_norm=False, floor=True):
-    """one Gemma-style decoder-layer decode step, HIP-graph replayed
-    (act_fp8: the norm -> GEMV hand-offs carry e4m3 activations; fuse_glu:
-    gelu_and_mul in the gate/up GEMV's epilogue; fuse_norm: both add+RMSNorms
-    in the prologue of the GEMV they feed; floor: also time the read probe
-    over the step's weights)."""
+# Decoder-step variants timed side by side: the default step (gelu_and_mul in
+# the gate/up GEMV's epilogue), the e4m3 hand-off, every op its own launch,
+# and the add+RMSNorms also in the GEMV prologues.
+LAYER_VARIANTS = {"us_per_step": dict(),
+                  "act_fp8_us_per_step": dict(act_fp8=True),
+                  "unfused_us_per_step": dict(fuse_glu=False),
+                  "norm_fused_us_per_step": dict(fuse_norm=True)}
+
+
+def bench_layer(torch, steps, M=4, rounds=5):
+    """one Gemma-style decoder-layer decode step, HIP-graph
+    replayed.  Every variant of LAYER_VARIANTS is captured first, then the
+    variants are timed in turn, `rounds` times round-robin (so that all see
+    the same clock state), and each reports its median round; plus the read
+    probe over the step's four weight matrices (the one-pass floor)."""
     from esimd_learning_amd import synthetic
     from esimd_learning_amd.layer import GemmaDecodeLayer
     dev = "cuda:0"
     p = synthetic.gemma_layer(seed=10)
-    layer = GemmaDecodeLayer(p, M, dev, act_fp8=act_fp8, fuse_glu=fuse_glu, fuse_norm=fuse_norm)
     h = synthetic.activations(M, p["hidden"], seed=20).to(dev)
     r = synthetic.activations(M, p["hidden"], seed=21).to(dev)
     pos = synthetic.positions(M, seed=22).to(dev)
-    layer.step(h, r, pos)
-    torch.cuda.synchronize()
-    g = layer.capture(h, r, pos)
-    t_end = time.perf_counter() + WARM_S / 2
-    while time.perf_counter() < t_end:
-        g.replay()
+    graphs, layers = {}, {}
+    for key, kw in LAYER_VARIANTS.items():
+        layer = GemmaDecodeLayer(p, M, dev, **kw)
+        layer.step(h, r, pos)
         torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / steps
+        graphs[key] = layer.capture(h, r, pos)
+        layers[key] = layer
+    t_end = time.perf_counter() + WARM_S
+    while time.perf_counter() < t_end:
+        for g in graphs.values():
+            g.replay()
+        torch.cuda.synchronize()
+    times = {key: [] for key in graphs}
+    for _ in range(rounds):
+        for key, g in graphs.items():
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times[key].append(e0.elapsed_time(e1) * 1e3 / steps)
+    med = {key: sorted(v)[len(v) // 2] for key, v in times.items()}
+    layer = layers["us_per_step"]
     wb = layer.weight_bytes()
-    if not floor:
-        return {"us_per_step": round(us, 2)}
     # the four weight matrices read once each by cek_hbm_read_probe, captured
     # and replayed the same way: the one-pass read floor of a step's GEMVs
     from esimd_learning_amd import cabi
@@ -386,11 +402,17 @@ def bench_layer(torch, steps, M=4, act_fp8=False, fuse_glu=True, fuse_norm=False
             for w in mats] * steps
     _, pev_ms, _ = time_graph(pfns, torch, stream, warm_s=WARM_S / 2)
     floor_us = pev_ms * 1e3 / steps
-    return {"config": "Gemma-style decoder layer decode step, M=4, hidden 3072, 16q/16kv x 256, MLP 24576 "
-                      "(attention stood in by a copy of q)",
-            "us_per_step": round(us, 2), "weight_bytes": wb, "weight_GBps": round(wb / us / 1e3, 1),
-            "weight_read_floor_us": round(floor_us, 2),
-            "timing": f"one HIP graph of the step, replayed {steps} times back to back"}
+    us = med["us_per_step"]
+    out = {"config": "Gemma-style decoder layer decode step, M=4, hidden 3072, 16q/16kv x 256, MLP 24576 "
+                     "(attention stood in by a copy of q)",
+           "us_per_step": round(us, 2), "weight_bytes": wb, "weight_GBps": round(wb / us / 1e3, 1),
+           "weight_read_floor_us": round(floor_us, 2)}
+    for key in LAYER_VARIANTS:
+        if key != "us_per_step":
+            out[key] = round(med[key], 2)
+    out["timing"] = (f"one HIP graph per variant, {steps} replays back to back, variants timed round-robin "
+                     f"{rounds} times, median round")
+    return out
 
 
 def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
@@ -530,14 +552,9 @@ def main():
                                               for r in out["gemm_pert"]))
     if not a.no_layer:
         out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))
-        log(f"layer: {out['decoder_layer']['us_per_step']} us/step, {out['decoder_layer']['weight_GBps']} GB/s")
-        ls = max(20, a.steps // 4)
-        variants = {"act_fp8_us_per_step": dict(act_fp8=True),
-                    "unfused_us_per_step": dict(fuse_glu=False),
-                    "norm_fused_us_per_step": dict(fuse_norm=True)}
-        for key, kw in variants.items():
-            out["decoder_layer"][key] = bench_layer(torch, ls, floor=False, **kw)["us_per_step"]
-            log(f"layer {key}: {out['decoder_layer'][key]} us/step")
+        dl = out["decoder_layer"]
+        log(f"layer: {dl['us_per_step']} us/step, {dl['weight_GBps']} GB/s; " +
+            ", ".join(f"{k} {dl[k]}" for k in LAYER_VARIANTS if k != "us_per_step"))
     if not a.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch)

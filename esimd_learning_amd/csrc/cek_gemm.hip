@@ -895,9 +895,11 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   {
     // Tiles: 128 x 128 with 4 waves and two workgroups per CU, or the
     // register-pipelined 8-wave kernel (2 x 4 waves, four loader waves) at
-    // 256 x 192 or 256 x 256 -- each configuration's measured rate (MI355X,
-    // config-4 shapes with fp16 activations, TFLOP/s at full occupancy)
-    // times the fill of its last round over 256 CUs, best score wins.
+    // 256 x 128, 256 x 192 or 256 x 256 -- each configuration's measured rate
+    // (MI355X, config-4 shapes with fp16 activations, TFLOP/s at full
+    // occupancy) times the fill of its last round over 256 CUs, best score
+    // wins.  (256 x 128: 205 us at M = 2048, K = 14336, N = 4096, against
+    // 217 us for 128 x 128.)
     auto score = [&](int bm, int bn, double rate, int slots) {
       const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
       const int64_t rounds = (tiles + slots - 1) / slots;
@@ -909,7 +911,12 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
     const double s128 = score(128, 128, 1150, 512);
     const double s192 = off32 ? score(256, 192, 1250, 256) : -1.0;
     const double s256 = off32 ? score(256, 256, 1400, 256) : -1.0;
-    const int tile = s256 > s192 && s256 > s128 ? 2 : (s192 > s128 ? 1 : 0);
+    // 256 x 128 only from one full round of tiles (at M = 512 it measured
+    // 24-28% slower than 128 x 128, whose fill the score rates the same)
+    const bool full256n128 = ((M + 255) / 256) * ((N + 127) / 128) >= 256;
+    const double s256n128 = off32 && full256n128 ? score(256, 128, 1170, 256) : -1.0;
+    const double best = std::max(std::max(s128, s192), std::max(s256, s256n128));
+    const int tile = best == s256 ? 2 : (best == s192 ? 1 : (best == s256n128 ? 3 : 0));
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     uint16_t* yp = static_cast<uint16_t*>(y);
@@ -929,6 +936,7 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   do {                                                            \
     if (tile == 2) CEK_W8A16_PIPE(TY, F, 256, 256, 1, 2, 4);      \
     else if (tile == 1) CEK_W8A16_PIPE(TY, F, 256, 192, 1, 2, 4); \
+    else if (tile == 3) CEK_W8A16_PIPE(TY, F, 256, 128, 1, 2, 4); \
     else CEK_W8A16_TILE(TY, F, 128, 128, 2, 2, 2);                \
   } while (0)
     if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_W8A16(F16, CEK_E4M3);

@@ -148,10 +148,11 @@ def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
         assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
 
 
-@pytest.mark.parametrize("M,K,N", [(4096, 1024, 4096), (4000, 576, 4090), (2048, 512, 6144), (2000, 576, 6100)])
+@pytest.mark.parametrize("M,K,N", [(4096, 1024, 4096), (4000, 576, 4090), (2048, 512, 6144), (2000, 576, 6100),
+                                   (2048, 512, 4096), (2000, 576, 4000)])
 @pytest.mark.parametrize("io,fmt", [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)])
 def test_gemm_pert_large_tiles_vs_gpu_fp32(ops, dev, M, K, N, io, fmt):
-    """w8a16 256 x 256 tiles (8 waves), ragged edges, both activation types
+    """w8a16 256 x 256, 256 x 192 and 256 x 128 tiles (8 waves), ragged edges, both activation types
     and fp8 formats, against a float32 torch GPU matmul of the dequantised
     weights."""
     _say(f"gemm pert large tiles M={M} K={K} N={N} {io} {fmt}")

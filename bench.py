@@ -304,15 +304,30 @@ def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
                          "traffic": None}}
 
 
-def bench_gemm_all(ops, torch, steps, warmup):
-    """BASELINE config 4 at M = 2048: the headline (K, N) = (4096, 6144) plus
-    the other two projections, each timed the same way."""
+def bench_gemm_all(ops, torch, steps, warmup, all_m=True):
+    """the headline M = 2048, (K, N) = (4096, 6144), plus
+    the other two projections ("shapes"), each timed the same way; with all_m
+    also M = 512 and 4096 ("m_table", each row with the roofline time
+    max(flop / fp8 peak, bytes / HBM peak), bytes = M K + N K + 2 M N + 4 M +
+    4 N: M = 512 sits near the ridge point)."""
     head = bench_gemm(ops, torch, steps, warmup)
     head["shapes"] = []
     for K, N in ((4096, 6144), (4096, 28672), (14336, 4096)):
         r = head if (K, N) == (4096, 6144) else bench_gemm(ops, torch, steps, warmup, K=K, N=N)
         head["shapes"].append({"config": r["config"], "avg_launch_us": round(r["avg_launch_us"], 2),
                                "tflops": round(r["tflops"], 1)})
+    if all_m:
+        head["m_table"] = []
+        for M in (512, 4096):
+            for K, N in ((4096, 6144), (4096, 28672), (14336, 4096)):
+                r = bench_gemm(ops, torch, steps, warmup, M=M, K=K, N=N)
+                flops = 2.0 * M * N * K
+                byts = M * K + N * K + 2 * M * N + 4 * M + 4 * N
+                roof_us = max(flops / (FP8_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9)) * 1e6
+                head["m_table"].append({"M": M, "K": K, "N": N, "avg_launch_us": round(r["avg_launch_us"], 2),
+                                        "tflops": round(r["tflops"], 1), "roofline_us": round(roof_us, 2),
+                                        "frac_of_roofline": round(roof_us / r["avg_launch_us"], 3),
+                                        "weights": "one copy, re-read across launches (Infinity Cache resident)"})
     return head
 
 

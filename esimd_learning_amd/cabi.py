@@ -32,6 +32,8 @@ SIGNATURES = {
     "cek_fused_add_rms_norm_quant_fp8": (_i, [_p, _p, _p, _i64, _i64, _f, _i, _p, _p, _p]),
     "cek_per_token_quant_fp8": (_i, [_p, _i64, _i64, _i, _p, _p, _p]),
     "cek_gemm_fp8_a8w8": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p]),
+    "cek_gemm_fp8_a8w8_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "cek_gemm_fp8_a8w8_ws": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p, _i64, _p]),
     "cek_gelu_and_mul": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p]),
     "cek_gemv_fp8_gelu_and_mul": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_add_rms_norm_gemv_fp8": (_i, [_p, _p, _p, _f, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _i,

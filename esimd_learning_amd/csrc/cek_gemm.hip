@@ -396,11 +396,17 @@ __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uin
   }
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int OCC, int LW>
+//
+// SPLIT > 1 (split K, for shapes with too few tiles to fill the GPU):
+// workgroup b computes tile b / SPLIT over the K range of part b % SPLIT
+// ((K / SPLIT) % 128 == 0) and stores its unscaled fp32 sums to part
+// P[b % SPLIT] of the [SPLIT][M][N] workspace P; gemm_splitk_finalize then
+// adds the parts in order, scales and converts.
+template <typename T, int BM, int BN, int WM, int WN, int OCC, int LW, int SPLIT = 1>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sa,
     const uint8_t* __restrict__ B, const float* __restrict__ sb,
-    uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
+    uint16_t* __restrict__ Y, float* __restrict__ P, int M, int N, int K, int tiles_m, int tiles_n) {
   using C = PipeCfg<BM, BN, WM, WN>;
   using L = LoadSplit<BM, BN, LW>;
   constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NW = C::NW;
@@ -419,8 +425,9 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const bool loader = wave < LW;
+  const int part = SPLIT > 1 ? (int)blockIdx.x % SPLIT : 0;
   int tm, tn;
-  tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_of<BM, BN, 8>(SPLIT > 1 ? blockIdx.x / SPLIT : blockIdx.x, tiles_m, tiles_n, tm, tn);
   // A last tile that would cross M (N) is moved back to end there (M >= BM,
   // N >= BN): every row it loads exists, so no load needs a clamp, and it
   // stores only from its own first row (column) mlo (nlo) on -- the rows
@@ -444,8 +451,9 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   // & 7 for every chunk).  Byte offsets into A and B of this lane's chunk 0
   // rows; chunk i is LW * 8 rows further (a uniform stride).
   const uint32_t cofs = (uint32_t)(((lane & 7) ^ swz<1>(lane >> 3)) * 16);
-  const uint32_t ga = (uint32_t)(m0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs;
-  const uint32_t gb = (uint32_t)(n0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs;
+  const uint32_t kpart = (uint32_t)(part * (K / SPLIT));  // first K value of this part
+  const uint32_t ga = (uint32_t)(m0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs + kpart;
+  const uint32_t gb = (uint32_t)(n0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs + kpart;
   const int r16 = lane & 15, g = lane >> 4;
   const int p0 = g ^ swz<1>(r16), p1 = (g + 4) ^ swz<1>(r16);
 
@@ -455,7 +463,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int KT = K / BK;
+  const int KT = K / BK / SPLIT;
   // Prologue: steps 0 and 1, then wait for step 0 (a loader's step 1 loads,
   // issued last, may fly; a non-loader has at most its older scale load out).
   if (loader) {
@@ -487,7 +495,47 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   // here: each step's barrier waited for vmcnt(0), and with KT == 1 the
   // prologue's did
   static_assert(SMEM >= BM * BN * 2, "output tile must fit");
-  store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y, mlo, nlo);
+  if constexpr (SPLIT > 1) {
+    // fp32 partial sums in D layout: lane l holds column l & 15, rows
+    // 4 (l >> 4) + v of each 16 x 16 block (rows before mlo / columns before
+    // nlo belong to the previous tile)
+    float* Pp = P + (size_t)part * M * N;
+    const int r16 = lane & 15, g4 = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * TN + j * 16 + r16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = m0 + wm * TM + i * 16 + g4 + v;
+          if (m >= mlo && n >= nlo) Pp[(size_t)m * N + n] = acc[i][j][v];
+        }
+      }
+  } else {
+    store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y, mlo, nlo);
+  }
+}
+
+// Y[m, n] = Out(sa[m] * sb[n] * (P[0][m, n] + P[1][m, n] + ...)), the parts
+// added in order (so the result does not depend on which part finished
+// first).  Four outputs per thread.
+template <typename T, int SPLIT>
+__global__ __launch_bounds__(256) void gemm_splitk_finalize(const float* __restrict__ P, const float* __restrict__ sa,
+                                                            const float* __restrict__ sb, uint16_t* __restrict__ Y,
+                                                            int M, int N) {
+  const int64_t total = (int64_t)M * N;
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t i = i0 + e;
+    if (i >= total) break;
+    float s = P[i];
+#pragma unroll
+    for (int q = 1; q < SPLIT; ++q) s += P[(size_t)q * total + i];
+    const int m = (int)(i / N), n = (int)(i % N);
+    Y[i] = T::from_f32(f32_round(s * sa[m] * sb[n]));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -959,14 +1007,106 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   return check_launch();
 }
 
+namespace cek {
+
+// Tiled a8w8 configurations: tile, measured rate at full occupancy (MI355X,
+// BASELINE prefill shapes, TFLOP/s) and workgroup slots over 256 CUs (the
+// 8-wave tiles fit one workgroup per CU, the 4-wave ones two):
+//  * 64 x 128 for few, small tiles;
+//  * 128 x 128, 4 waves, two workgroups per CU so that one's MFMAs cover
+//    the other's LDS reads and barrier waits;
+//  * 256 x 192, 8 waves (2 x 4, four loader waves);
+//  * 256 x 256, 8 waves (2 x 4, wave tile 128 x 64, two waves per SIMD,
+//    four loader waves): the least load and LDS traffic per MFMA.
+struct A8w8Opt { int bm, bn; double rate; int slots; };
+constexpr A8w8Opt kA8w8Opts[4] = {{64, 128, 1750, 512}, {128, 128, 2250, 512}, {256, 192, 2480, 256}, {256, 256, 2650, 256}};
+
+struct A8w8Plan { int cfg, split; };
+
+// Estimated time of each configuration: its rounds of workgroups at the
+// full-occupancy rate (a partial round costs a full one), for the 4-wave
+// tiles also with K split in 2 or 4 parts (each part a workgroup) plus the
+// fp32 partials' traffic and the finalize launch.  Split only when allowed
+// (a workspace is there), on the pipelined path, and 10% faster than the
+// best unsplit plan.  Unsplit, this picks the fastest measured tile, or one
+// within 2% of it, on all nine config-4 shapes; split, the fastest of the
+// four split forms at M = 512, K = 14336 (128 x 128 in 4 parts: 44 us
+// against 65 us unsplit), and no split where splitting measured slower
+// (M = 512, K = 4096; M = 1024).
+static A8w8Plan plan_a8w8(int64_t M, int64_t N, int64_t K, bool pipe_ok, bool allow_split) {
+  A8w8Plan best{0, 1};
+  double tbest = -1.0;
+  for (int c = 0; c < 4; ++c) {
+    const A8w8Opt& o = kA8w8Opts[c];
+    const int64_t tiles = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
+    const int64_t rounds = (tiles + o.slots - 1) / o.slots;
+    const double t = (double)(rounds * o.slots) * 2.0 * o.bm * o.bn * (double)K / (o.rate * 1e12);
+    if (tbest < 0 || t < tbest) {
+      tbest = t;
+      best = A8w8Plan{c, 1};
+    }
+  }
+  if (!allow_split) return best;
+  const double tplain = tbest;
+  for (int c = 0; c < 2; ++c) {
+    const A8w8Opt& o = kA8w8Opts[c];
+    if (!pipe_ok || M < o.bm || N < o.bn) continue;
+    for (int sp : {2, 4}) {
+      if ((K / 128) % sp) continue;
+      const int64_t units = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn) * sp;
+      const int64_t rounds = (units + o.slots - 1) / o.slots;
+      const double tg = (double)(rounds * o.slots) * 2.0 * o.bm * o.bn * (double)(K / sp) / (o.rate * 1e12);
+      // partials written and read back (mostly from the Infinity Cache), the output, a launch
+      const double tx = ((double)sp * M * N * 4.0 * 2.0 + (double)M * N * 2.0) / 8e12 + 2e-6;
+      if (tg + tx < 0.9 * tplain && tg + tx < tbest) {
+        tbest = tg + tx;
+        best = A8w8Plan{c, sp};
+      }
+    }
+  }
+  return best;
+}
+
+static bool a8w8_off32(int64_t M, int64_t N, int64_t K) {
+  return (uint64_t)M * (uint64_t)K < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
+}
+
+// Bytes of fp32 partials the split-K plan for this shape needs (0: unsplit).
+static int64_t a8w8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 64 || K % 128 != 0 || M > 65535 * 64 || N > INT32_MAX || K > INT32_MAX || M <= 0 || N <= 0) return 0;
+  const A8w8Plan p = plan_a8w8(M, N, K, a8w8_off32(M, N, K), true);
+  return p.split > 1 ? (int64_t)p.split * M * N * 4 : 0;
+}
+
+static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb, void* y, int64_t M,
+                       int64_t N, int64_t K, int out_dtype, float* ws, int64_t ws_bytes, hipStream_t st);
+
+}  // namespace cek
+
+extern "C" int64_t cek_gemm_fp8_a8w8_workspace_size(int64_t M, int64_t N, int64_t K) {
+  return cek::a8w8_workspace_bytes(M, N, K);
+}
+
+extern "C" int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb, void* y,
+                                    int64_t M, int64_t N, int64_t K, int out_dtype, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) return CEK_ERR_INVALID;
+  return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, static_cast<float*>(workspace), workspace_bytes,
+                          (hipStream_t)stream);
+}
+
 extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
                                  void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream) {
+  return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, nullptr, 0, (hipStream_t)stream);
+}
+
+static int cek::launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb, void* y, int64_t M,
+                            int64_t N, int64_t K, int out_dtype, float* ws, int64_t ws_bytes, hipStream_t st) {
   if (M < 0 || N < 0 || K <= 0 || K % 16 != 0) return CEK_ERR_INVALID;
   if (M > 65535 * 64 || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
   if (M == 0 || N == 0) return CEK_OK;
   if (!a || !sa || !b || !sb || !y) return CEK_ERR_INVALID;
   if (!aligned(a, 16) || !aligned(b, 16)) return CEK_ERR_INVALID;
-  hipStream_t st = (hipStream_t)stream;
   uint16_t* yp = static_cast<uint16_t*>(y);
   if (out_dtype != CEK_F16 && out_dtype != CEK_BF16) return CEK_ERR_INVALID;
   // Skinny A: stream the weights once with the GEMV kernels rather than tile
@@ -976,34 +1116,17 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     if (rc != CEK_ERR_UNSUPPORTED) return rc;
   }
   if (K % 128 == 0) {
-    // Tile choice: each configuration's measured rate at full occupancy
-    // (MI355X, BASELINE prefill shapes, TFLOP/s) times the useful share of
-    // the tile area its rounds of workgroups cover (256 CUs; the 8-wave tiles
-    // fit one workgroup per CU, the 4-wave ones two), best score wins:
-    //  * 256 x 256, 8 waves (2 x 4, wave tile 128 x 64, two waves per SIMD,
-    //    four loader waves): the least load and LDS traffic per MFMA;
-    //  * 256 x 192, 8 waves (2 x 4, four loader waves);
-    //  * 128 x 128, 4 waves, two workgroups per CU so that one's MFMAs cover
-    //    the other's LDS reads and barrier waits;
-    //  * 64 x 128 for few, small tiles.
-    // All four run gemm_a8w8_pipe_kernel (register-pipelined fragment reads,
-    // single-offset addressing) when the matrices are below 4 GB and at
+    // Tile (and split-K) choice: plan_a8w8.  Every configuration runs
+    // gemm_a8w8_pipe_kernel (register-pipelined fragment reads,
+    // single-offset addressing) when the matrices are below 4 GB and hold at
     // least one tile in each dimension; otherwise gemm_a8w8_lds_kernel with
-    // the same tile (its loads clamp rows).  This picks the fastest measured
-    // configuration, or one within 2% of it, on all nine config-4 shapes.
-    struct Opt { int bm, bn; double rate; int slots; };
-    constexpr Opt opts[4] = {{64, 128, 1750, 512}, {128, 128, 2250, 512}, {256, 192, 2480, 256}, {256, 256, 2650, 256}};
-    int cfg = 0;
-    double best = -1.0;
-    for (int c = 0; c < 4; ++c) {
-      const int64_t tiles = ((M + opts[c].bm - 1) / opts[c].bm) * ((N + opts[c].bn - 1) / opts[c].bn);
-      const int64_t rounds = (tiles + opts[c].slots - 1) / opts[c].slots;
-      // useful share of the tile area the rounds could cover
-      const double score = opts[c].rate * (double)(M * N) / ((double)(rounds * opts[c].slots) * opts[c].bm * opts[c].bn);
-      if (score > best) { best = score; cfg = c; }
-    }
-    const bool off32 = (uint64_t)M * (uint64_t)K < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
-    const bool pipe = off32 && M >= opts[cfg].bm && N >= opts[cfg].bn;
+    // the same tile (its loads clamp rows).  Split K needs a workspace of
+    // a8w8_workspace_bytes; without one the unsplit plan runs.
+    const bool off32 = a8w8_off32(M, N, K);
+    const int64_t need = a8w8_workspace_bytes(M, N, K);
+    const A8w8Plan plan = plan_a8w8(M, N, K, off32, need > 0 && ws && ws_bytes >= need);
+    const int cfg = plan.cfg;
+    const bool pipe = off32 && M >= kA8w8Opts[cfg].bm && N >= kA8w8Opts[cfg].bn;
 #define CEK_A8W8(TY, BM, BN, WM, WN, OCC)                                                               \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
@@ -1014,11 +1137,27 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
     gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW>                                                \
-        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, nullptr, M, N, K, tm, tn); \
+  } while (0)
+#define CEK_A8W8_SPLIT(TY, BM, BN, OCC, LW, SP)                                                          \
+  do {                                                                                                \
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, 2, 2, OCC, LW, SP>                                              \
+        <<<dim3((unsigned)(tm * tn * SP)), 256, 0, st>>>(a, sa, b, sb, yp, ws, M, N, K, tm, tn);      \
+    gemm_splitk_finalize<TY, SP><<<dim3((unsigned)((M * N + 1023) / 1024)), 256, 0, st>>>(ws, sa, sb, yp, \
+                                                                                         (int)M, (int)N); \
   } while (0)
 #define CEK_A8W8_ALL(TY)                                                               \
   do {                                                                                 \
-    if (cfg == 3) {                                                                    \
+    if (plan.split > 1) {                                                              \
+      if (cfg == 1) {                                                                  \
+        if (plan.split == 2) CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 2);                    \
+        else CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 4);                                    \
+      } else {                                                                         \
+        if (plan.split == 2) CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 2);                     \
+        else CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 4);                                     \
+      }                                                                                \
+    } else if (cfg == 3) {                                                             \
       if (pipe) CEK_A8W8_PIPE(TY, 256, 256, 2, 4, 1, 4);                               \
       else CEK_A8W8(TY, 256, 256, 4, 2, 1);                                            \
     } else if (cfg == 2) {                                                             \
@@ -1036,6 +1175,7 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
     else CEK_A8W8_ALL(BF16);
 #undef CEK_A8W8
 #undef CEK_A8W8_PIPE
+#undef CEK_A8W8_SPLIT
 #undef CEK_A8W8_ALL
     return check_launch();
   }

@@ -62,10 +62,23 @@ at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, a
   TORCH_CHECK(a_scale.numel() == M && b_scale.numel() == N, op, ": a_scale [M] and b_scale [N] required");
   TORCH_CHECK(output.numel() == M * N, op, ": output must be [M, N]");
   c10::OptionalDeviceGuard guard(a.device());
-  check_rc(cek_gemm_fp8_a8w8(static_cast<const uint8_t*>(a.data_ptr()), static_cast<const float*>(a_scale.data_ptr()),
-                             static_cast<const uint8_t*>(b.data_ptr()), static_cast<const float*>(b_scale.data_ptr()),
-                             output.data_ptr(), M, N, K, io_code(output.scalar_type()), current_stream(a)),
-           op);
+  const auto* ap = static_cast<const uint8_t*>(a.data_ptr());
+  const auto* sap = static_cast<const float*>(a_scale.data_ptr());
+  const auto* bp = static_cast<const uint8_t*>(b.data_ptr());
+  const auto* sbp = static_cast<const float*>(b_scale.data_ptr());
+  // shapes with too few tiles split K: fp32 partials in a workspace from the
+  // caching allocator (no kernel runs to allocate or clear it)
+  const int64_t need = cek_gemm_fp8_a8w8_workspace_size(M, N, K);
+  if (need > 0) {
+    at::Tensor ws = at::empty({(need + 3) / 4}, a_scale.options());
+    check_rc(cek_gemm_fp8_a8w8_ws(ap, sap, bp, sbp, output.data_ptr(), M, N, K, io_code(output.scalar_type()),
+                                  ws.data_ptr(), need, current_stream(a)),
+             op);
+  } else {
+    check_rc(cek_gemm_fp8_a8w8(ap, sap, bp, sbp, output.data_ptr(), M, N, K, io_code(output.scalar_type()),
+                               current_stream(a)),
+             op);
+  }
   return output;
 }
 

@@ -134,6 +134,21 @@ int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const
                       void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
 
 /*
+ * NEW: the same product with a caller-provided workspace, which lets shapes
+ * with too few output tiles to fill the GPU (e.g. M = 512, K = 14336) split
+ * K into parts: each part's fp32 partial sums go to the workspace, and a
+ * second launch adds them in order, scales and converts (deterministic).
+ * cek_gemm_fp8_a8w8_workspace_size returns the bytes that plan needs for
+ * (M, N, K), 0 when the shape runs unsplit; with a smaller workspace (or
+ * none) the call runs unsplit, like cek_gemm_fp8_a8w8.  The workspace is
+ * fully written before it is read: it needs no initialisation.
+ */
+int64_t cek_gemm_fp8_a8w8_workspace_size(int64_t M, int64_t N, int64_t K);
+int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
+                         void* y, int64_t M, int64_t N, int64_t K, int out_dtype,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * NEW: out[t, i] = gelu_tanh(x[t, i]) * x[t, d + i], fp32 math.
  * x rows have stride x_stride elements (>= 2d), out rows out_stride (>= d).
  */

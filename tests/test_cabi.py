@@ -115,6 +115,12 @@ def test_host_rejects_invalid_arguments():
     assert ng(p, p, p, 1e-6, p, None, None, None, p, p, p, 4, 64, 4096, 0, 0, 0, 2, None) == U   # r_out aliases
     assert ng(None, None, None, 1e-6, None, None, None, None, None, None, None, 0, 64, 4096, 0, 0, 0, 2,
               None) == cabi.CEK_OK
+    # split-K workspace: size query, and a negative or missing workspace
+    assert lib.cek_gemm_fp8_a8w8_workspace_size(2048, 6144, 4096) == 0
+    ws = lib.cek_gemm_fp8_a8w8_workspace_size(512, 4096, 14336)           # K split in parts
+    assert ws > 0 and ws % (512 * 4096 * 4) == 0 and ws // (512 * 4096 * 4) in (2, 4)
+    assert lib.cek_gemm_fp8_a8w8_ws(p, p, p, p, p, 512, 4096, 14336, 0, None, 64, None) == E
+    assert lib.cek_gemm_fp8_a8w8_ws(p, p, p, p, p, 512, 4096, 14336, 0, p, -1, None) == E
     # empty problems are no-ops that succeed without touching memory
     assert lib.cek_gemv_fp8_pern(None, None, None, None, 0, 8, 64, 0, 0, 2, None) == cabi.CEK_OK
     assert lib.cek_fused_add_rms_norm(None, None, None, 0, 64, 1e-6, 0, None) == cabi.CEK_OK

@@ -148,6 +148,43 @@ def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
         assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
 
 
+@pytest.mark.parametrize("M,K,N", [(65, 1024, 200), (100, 2048, 512), (300, 4096, 4096), (300, 14336, 4096),
+                                   (512, 14336, 4096), (640, 14336, 4096)])
+def test_a8w8_split_k(ops, dev, M, K, N):
+    """Shapes with too few output tiles split K (the op allocates the
+    workspace the plan asks for): 64 x 128 tiles in 4 and 2 parts, 128 x 128
+    in 4 and 2 parts.  Against a float32 torch GPU matmul of the dequantised codes;
+    the unsplit C-ABI call (no workspace) agrees within the same tolerance;
+    two split calls agree bit for bit (the parts are added in order)."""
+    from esimd_learning_amd import cabi
+    _say(f"a8w8 split K M={M} K={K} N={N}")
+    lib = cabi.load()
+    need = lib.cek_gemm_fp8_a8w8_workspace_size(M, N, K)
+    assert need > 0 and need % (M * N * 4) == 0, need
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M + K)
+    qd, Wd, sad, sbd = q.to(dev), W8.to(dev), sa.to(dev), sb.to(dev)
+    A = qd.view(torch.float8_e4m3fn).float()
+    B = Wd.view(torch.float8_e4m3fn).float()
+    ref = ((A @ B.T) * sad[:, None] * sbd[None, :]).cpu()
+    y1 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    y2 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y1)
+    ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y2)
+    y3 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    st = cabi.stream_ptr(torch.cuda.current_stream())
+    assert lib.cek_gemm_fp8_a8w8(qd.data_ptr(), sad.data_ptr(), Wd.data_ptr(), sbd.data_ptr(), y3.data_ptr(),
+                                 M, N, K, 0, st) == 0
+    yb = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(need // 4, dtype=torch.float32, device=dev)
+    assert lib.cek_gemm_fp8_a8w8_ws(qd.data_ptr(), sad.data_ptr(), Wd.data_ptr(), sbd.data_ptr(), yb.data_ptr(),
+                                    M, N, K, 1, ws.data_ptr(), need, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert_close_fp(y1.cpu(), ref, f"a8w8 split M={M} K={K} N={N}")
+    assert_close_fp(y3.cpu(), ref, f"a8w8 unsplit M={M} K={K} N={N}")
+    assert_close_fp(yb.cpu(), ref, f"a8w8 split bf16 M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("M,K,N", [(4096, 1024, 4096), (4000, 576, 4090), (2048, 512, 6144), (2000, 576, 6100),
                                    (2048, 512, 4096), (2000, 576, 4000)])
 @pytest.mark.parametrize("io,fmt", [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)])

@@ -1100,8 +1100,10 @@ extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_
   return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, nullptr, 0, (hipStream_t)stream);
 }
 
-static int cek::launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb, void* y, int64_t M,
-                            int64_t N, int64_t K, int out_dtype, float* ws, int64_t ws_bytes, hipStream_t st) {
+namespace cek {
+
+static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb, void* y, int64_t M,
+                       int64_t N, int64_t K, int out_dtype, float* ws, int64_t ws_bytes, hipStream_t st) {
   if (M < 0 || N < 0 || K <= 0 || K % 16 != 0) return CEK_ERR_INVALID;
   if (M > 65535 * 64 || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
   if (M == 0 || N == 0) return CEK_OK;
@@ -1185,3 +1187,5 @@ static int cek::launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b,
   else return CEK_ERR_INVALID;
   return check_launch();
 }
+
+}  // namespace cek

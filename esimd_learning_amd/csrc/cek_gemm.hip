@@ -519,22 +519,53 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
 
 // Y[m, n] = Out(sa[m] * sb[n] * (P[0][m, n] + P[1][m, n] + ...)), the parts
 // added in order (so the result does not depend on which part finished
-// first).  Four outputs per thread.
+// first).  Grid (ceil(N / 2048), rows): eight consecutive outputs of one row
+// per thread, read as 16-byte pieces of every part and stored as one 16-byte
+// piece when N % 8 == 0 (P and Y 16-byte aligned), element by element
+// otherwise; rows past gridDim.y are taken grid-stride.
 template <typename T, int SPLIT>
 __global__ __launch_bounds__(256) void gemm_splitk_finalize(const float* __restrict__ P, const float* __restrict__ sa,
                                                             const float* __restrict__ sb, uint16_t* __restrict__ Y,
                                                             int M, int N) {
-  const int64_t total = (int64_t)M * N;
-  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const size_t total = (size_t)M * N;
+  const int n = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
+  if (n >= N) return;
+  const bool vec = (N & 7) == 0 && ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(sb)) & 15) == 0;
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const size_t i = (size_t)m * N + n;
+    const float rs = sa[m];
+    if (vec) {
+      f4 s0 = *reinterpret_cast<const f4*>(P + i), s1 = *reinterpret_cast<const f4*>(P + i + 4);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t i = i0 + e;
-    if (i >= total) break;
-    float s = P[i];
+      for (int q = 1; q < SPLIT; ++q) {
+        const f4 p0 = *reinterpret_cast<const f4*>(P + q * total + i);
+        const f4 p1 = *reinterpret_cast<const f4*>(P + q * total + i + 4);
 #pragma unroll
-    for (int q = 1; q < SPLIT; ++q) s += P[(size_t)q * total + i];
-    const int m = (int)(i / N), n = (int)(i % N);
-    Y[i] = T::from_f32(f32_round(s * sa[m] * sb[n]));
+        for (int e = 0; e < 4; ++e) {
+          s0[e] += p0[e];
+          s1[e] += p1[e];
+        }
+      }
+      const f4 c0 = *reinterpret_cast<const f4*>(sb + n), c1 = *reinterpret_cast<const f4*>(sb + n + 4);
+      u4 o;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t lo0 = T::from_f32(f32_round(s0[2 * e] * rs * c0[2 * e]));
+        const uint32_t hi0 = T::from_f32(f32_round(s0[2 * e + 1] * rs * c0[2 * e + 1]));
+        const uint32_t lo1 = T::from_f32(f32_round(s1[2 * e] * rs * c1[2 * e]));
+        const uint32_t hi1 = T::from_f32(f32_round(s1[2 * e + 1] * rs * c1[2 * e + 1]));
+        o[e] = lo0 | (hi0 << 16);
+        o[2 + e] = lo1 | (hi1 << 16);
+      }
+      *reinterpret_cast<u4*>(Y + i) = o;
+    } else {
+      for (int e = 0; e < 8 && n + e < N; ++e) {
+        float s = P[i + e];
+#pragma unroll
+        for (int q = 1; q < SPLIT; ++q) s += P[q * total + i + e];
+        Y[i + e] = T::from_f32(f32_round(s * rs * sb[n + e]));
+      }
+    }
   }
 }
 
@@ -1090,7 +1121,7 @@ extern "C" int64_t cek_gemm_fp8_a8w8_workspace_size(int64_t M, int64_t N, int64_
 extern "C" int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb, void* y,
                                     int64_t M, int64_t N, int64_t K, int out_dtype, void* workspace,
                                     int64_t workspace_bytes, void* stream) {
-  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) return CEK_ERR_INVALID;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !cek::aligned(workspace, 4)))) return CEK_ERR_INVALID;
   return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, static_cast<float*>(workspace), workspace_bytes,
                           (hipStream_t)stream);
 }
@@ -1146,8 +1177,8 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
     gemm_a8w8_pipe_kernel<TY, BM, BN, 2, 2, OCC, LW, SP>                                              \
         <<<dim3((unsigned)(tm * tn * SP)), 256, 0, st>>>(a, sa, b, sb, yp, ws, M, N, K, tm, tn);      \
-    gemm_splitk_finalize<TY, SP><<<dim3((unsigned)((M * N + 1023) / 1024)), 256, 0, st>>>(ws, sa, sb, yp, \
-                                                                                         (int)M, (int)N); \
+    gemm_splitk_finalize<TY, SP><<<dim3((unsigned)((N + 2047) / 2048), (unsigned)(M < 65535 ? M : 65535)), \
+                                   256, 0, st>>>(ws, sa, sb, yp, (int)M, (int)N);                       \
   } while (0)
 #define CEK_A8W8_ALL(TY)                                                               \
   do {                                                                                 \

@@ -141,7 +141,9 @@ int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const
  * cek_gemm_fp8_a8w8_workspace_size returns the bytes that plan needs for
  * (M, N, K), 0 when the shape runs unsplit; with a smaller workspace (or
  * none) the call runs unsplit, like cek_gemm_fp8_a8w8.  The workspace is
- * fully written before it is read: it needs no initialisation.
+ * fully written before it is read: it needs no initialisation.  It must be
+ * 4-byte aligned (CEK_ERR_INVALID otherwise); 16-byte alignment lets the
+ * second launch use 16-byte accesses.
  */
 int64_t cek_gemm_fp8_a8w8_workspace_size(int64_t M, int64_t N, int64_t K);
 int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,

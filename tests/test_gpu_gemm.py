@@ -149,13 +149,15 @@ def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(65, 1024, 200), (100, 2048, 512), (300, 4096, 4096), (300, 14336, 4096),
-                                   (512, 14336, 4096), (640, 14336, 4096)])
+                                   (512, 14336, 4096), (640, 14336, 4096), (65, 1024, 203), (100, 2048, 1001)])
 def test_a8w8_split_k(ops, dev, M, K, N):
     """Shapes with too few output tiles split K (the op allocates the
     workspace the plan asks for): 64 x 128 tiles in 4 and 2 parts, 128 x 128
     in 4 and 2 parts.  Against a float32 torch GPU matmul of the dequantised codes;
     the unsplit C-ABI call (no workspace) agrees within the same tolerance;
-    two split calls agree bit for bit (the parts are added in order)."""
+    two split calls agree bit for bit (the parts are added in order), and a
+    workspace 4 bytes off 16-byte alignment (the finalize's element-by-element
+    form, also taken for N % 8 != 0) gives the same outputs."""
     from esimd_learning_amd import cabi
     _say(f"a8w8 split K M={M} K={K} N={N}")
     lib = cabi.load()
@@ -178,8 +180,13 @@ def test_a8w8_split_k(ops, dev, M, K, N):
     ws = torch.empty(need // 4, dtype=torch.float32, device=dev)
     assert lib.cek_gemm_fp8_a8w8_ws(qd.data_ptr(), sad.data_ptr(), Wd.data_ptr(), sbd.data_ptr(), yb.data_ptr(),
                                     M, N, K, 1, ws.data_ptr(), need, st) == 0
+    y4 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    ws4 = torch.empty(need // 4 + 1, dtype=torch.float32, device=dev)
+    assert lib.cek_gemm_fp8_a8w8_ws(qd.data_ptr(), sad.data_ptr(), Wd.data_ptr(), sbd.data_ptr(), y4.data_ptr(),
+                                    M, N, K, 0, ws4.data_ptr() + 4, need, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
+    assert torch.equal(y1, y4)
     assert_close_fp(y1.cpu(), ref, f"a8w8 split M={M} K={K} N={N}")
     assert_close_fp(y3.cpu(), ref, f"a8w8 unsplit M={M} K={K} N={N}")
     assert_close_fp(yb.cpu(), ref, f"a8w8 split bf16 M={M} K={K} N={N}")

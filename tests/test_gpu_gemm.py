@@ -192,6 +192,38 @@ def test_a8w8_split_k(ops, dev, M, K, N):
     assert_close_fp(yb.cpu(), ref, f"a8w8 split bf16 M={M} K={K} N={N}")
 
 
+def test_a8w8_split_k_graph_replays(ops, dev):
+    """The split-K op captured in a HIP graph (its workspace then comes from
+    the graph's memory pool): three replays, with eager work on the same
+    buffers and synchronisations between them, each equal bit for bit to the
+    eager call on fresh inputs."""
+    M, K, N = 512, 14336, 4096
+    _say(f"a8w8 split K graph M={M} K={K} N={N}")
+    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=7)
+    qd, Wd, sad, sbd = q.to(dev), W8.to(dev), sa.to(dev), sb.to(dev)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):  # warm-up outside the capture
+        ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y)
+    g2 = torch.Generator().manual_seed(11)
+    for r in range(3):
+        qd.view(torch.uint8).copy_(torch.randint(0, 0x7E, (M, K), generator=g2, dtype=torch.uint8))  # finite codes
+        sad.mul_(1.0 + 0.25 * r)
+        eager = torch.empty_like(y)
+        ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, eager)
+        torch.cuda.synchronize()
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {r}"
+
+
 @pytest.mark.parametrize("M,K,N", [(4096, 1024, 4096), (4000, 576, 4090), (2048, 512, 6144), (2000, 576, 6100),
                                    (2048, 512, 4096), (2000, 576, 4000)])
 @pytest.mark.parametrize("io,fmt", [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)])

@@ -1082,8 +1082,11 @@ static A8w8Plan plan_a8w8(int64_t M, int64_t N, int64_t K, bool pipe_ok, bool al
   for (int c = 0; c < 2; ++c) {
     const A8w8Opt& o = kA8w8Opts[c];
     if (!pipe_ok || M < o.bm || N < o.bn) continue;
-    for (int sp : {2, 4}) {
-      if ((K / 128) % sp) continue;
+    for (int sp : {2, 4, 8}) {
+      // at least 1024 K values per part: a part's prologue and partial-sum
+      // epilogue do not shrink with its K range (measured at M = 64, K = 4096:
+      // 4 parts 11.2 us, 8 parts 13.8 us)
+      if ((K / 128) % sp || K / sp < 1024) continue;
       const int64_t units = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn) * sp;
       const int64_t rounds = (units + o.slots - 1) / o.slots;
       const double tg = (double)(rounds * o.slots) * 2.0 * o.bm * o.bn * (double)(K / sp) / (o.rate * 1e12);
@@ -1104,7 +1107,7 @@ static bool a8w8_off32(int64_t M, int64_t N, int64_t K) {
 
 // Bytes of fp32 partials the split-K plan for this shape needs (0: unsplit).
 static int64_t a8w8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 64 || K % 128 != 0 || M > 65535 * 64 || N > INT32_MAX || K > INT32_MAX || M <= 0 || N <= 0) return 0;
+  if (M < 64 || K % 128 != 0 || M > 65535 * 64 || N > INT32_MAX || K > INT32_MAX || M <= 0 || N <= 0) return 0;
   const A8w8Plan p = plan_a8w8(M, N, K, a8w8_off32(M, N, K), true);
   return p.split > 1 ? (int64_t)p.split * M * N * 4 : 0;
 }
@@ -1144,9 +1147,15 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
   if (out_dtype != CEK_F16 && out_dtype != CEK_BF16) return CEK_ERR_INVALID;
   // Skinny A: stream the weights once with the GEMV kernels rather than tile
   // a mostly empty GEMM (they decline the shapes the tiles serve better).
+  // At M = 64 (the 64-row tile's smallest M), given the workspace the
+  // split-K plan asks for, the tiled GEMM in K parts is 1.2-1.8x faster
+  // (measured on MI355X, K = 4096..14336, N = 4096..28672).
   if (M <= 64) {
-    const int rc = launch_gemv_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, st);
-    if (rc != CEK_ERR_UNSUPPORTED) return rc;
+    const int64_t need64 = M == 64 ? a8w8_workspace_bytes(M, N, K) : 0;
+    if (!(need64 > 0 && ws && ws_bytes >= need64)) {
+      const int rc = launch_gemv_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, st);
+      if (rc != CEK_ERR_UNSUPPORTED) return rc;
+    }
   }
   if (K % 128 == 0) {
     // Tile (and split-K) choice: plan_a8w8.  Every configuration runs
@@ -1185,10 +1194,12 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     if (plan.split > 1) {                                                              \
       if (cfg == 1) {                                                                  \
         if (plan.split == 2) CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 2);                    \
-        else CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 4);                                    \
+        else if (plan.split == 4) CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 4);               \
+        else CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 8);                                    \
       } else {                                                                         \
         if (plan.split == 2) CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 2);                     \
-        else CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 4);                                     \
+        else if (plan.split == 4) CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 4);                \
+        else CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 8);                                     \
       }                                                                                \
     } else if (cfg == 3) {                                                             \
       if (pipe) CEK_A8W8_PIPE(TY, 256, 256, 2, 4, 1, 4);                               \

@@ -135,7 +135,7 @@ int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const
 
 /*
  * NEW: the same product with a caller-provided workspace, which lets shapes
- * with too few output tiles to fill the GPU (e.g. M = 512, K = 14336) split
+ * with too few output tiles to fill the GPU (e.g. M = 512, K = 14336; M = 64) split
  * K into parts: each part's fp32 partial sums go to the workspace, and a
  * second launch adds them in order, scales and converts (deterministic).
  * cek_gemm_fp8_a8w8_workspace_size returns the bytes that plan needs for

@@ -148,12 +148,15 @@ def test_a8w8_large_tiles_vs_gpu_fp32(ops, dev, M, K, N):
         assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
 
 
-@pytest.mark.parametrize("M,K,N", [(65, 1024, 200), (100, 2048, 512), (300, 4096, 4096), (300, 14336, 4096),
-                                   (512, 14336, 4096), (640, 14336, 4096), (65, 1024, 203), (100, 2048, 1001)])
+@pytest.mark.parametrize("M,K,N", [(65, 4096, 200), (100, 2048, 512), (300, 4096, 4096), (300, 14336, 4096),
+                                   (512, 14336, 4096), (640, 14336, 4096), (65, 4096, 203), (100, 2048, 1001),
+                                   (64, 4096, 6144), (64, 14336, 4096), (64, 4096, 300), (64, 4096, 28672)])
 def test_a8w8_split_k(ops, dev, M, K, N):
     """Shapes with too few output tiles split K (the op allocates the
-    workspace the plan asks for): 64 x 128 tiles in 4 and 2 parts, 128 x 128
-    in 4 and 2 parts.  Against a float32 torch GPU matmul of the dequantised codes;
+    workspace the plan asks for): 64 x 128 tiles in 8, 4 and 2 parts (M = 64
+    included, which without a workspace takes the weight-streaming kernels),
+    128 x 128 in 4 and 2 parts.  Against a float32 torch GPU matmul of the
+    dequantised codes;
     the unsplit C-ABI call (no workspace) agrees within the same tolerance;
     two split calls agree bit for bit (the parts are added in order), and a
     workspace 4 bytes off 16-byte alignment (the finalize's element-by-element

@@ -124,7 +124,7 @@ def encode_e4m3_bruteforce(x):
 
 
 def per_token_quant(xf):
-    """Per-row e4m3 quantisation of float32 rows (SURVEY a6/a12 recipe).
+    """Per-row e4m3 quantisation of float32 rows (the per-token activation quant).
 
     s_t = max(amax_t / 448, MIN_SCALE) in fp32,
     q   = e4m3(RNE(clamp(x / s_t, -448, 448))) with an IEEE fp32 divide.

@@ -2,7 +2,7 @@
 
 Test infrastructure only (see ``oracle/__init__.py``).
 
-No reference op exists.  Definition, fp32 accumulate:
+The reference has no a8w8 op.  Definition, fp32 accumulate:
     Y[m, n] = f16(sa[m] * sb[n] * sum_k dq(A[m, k]) * dq(B[n, k]))
 computed here as the fp32 dequantise-then-matmul of the codes, the same
 style as the reference's GEMM oracle (``tests/test_gemm_fp8.py:35-36``).

@@ -13,7 +13,7 @@ The reference test's formula (``tests/test_fused_add_rms_norm_batched_fp8.py:7-2
 uses the unrounded sum in pass 2; ``fused_add_rms_norm_testformula`` restates
 it and the oracle tests check both agree within the op tolerance.
 
-The fp8 extension (no reference op): quantise the fp16-rounded
+The fp8 extension (the reference has no op for it): quantise the fp16-rounded
 normed row per token with ``oracle.fp8.per_token_quant``.
 
 Pins (tests/test_oracle_norm.py): r' is f16(h+r) elementwise (checked
@@ -56,7 +56,7 @@ def fused_add_rms_norm_quant(h, r, w, eps):
 
 
 def per_token_quant(x):
-    """x [T,H] fp16/bf16 -> (codes uint8 [T,H], scale fp32 [T])."""
+    """x [T,H] fp16/bf16 -> (codes uint8 [T,H], scale fp32 [T]), per-token e4m3."""
     q, s = fp8.per_token_quant(x.cpu().float().numpy())
     return torch.from_numpy(q), torch.from_numpy(s)
 

@@ -23,24 +23,27 @@ namespace cek {
 
 template <typename T>
 __global__ __launch_bounds__(256) void gelu_and_mul_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ x, int d, int64_t xs, int64_t os, int vec) {
-  const int t = blockIdx.y;
-  const uint16_t* xr = x + (size_t)t * xs;
-  uint16_t* orow = out + (size_t)t * os;
-  if (vec) {
-    const int i = (blockIdx.x * 256 + threadIdx.x) * 8;
-    if (i >= d) return;
-    u4 a = load_u4(xr + i), b = load_u4(xr + d + i), o;
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ x, int64_t T_rows, int d, int64_t xs, int64_t os,
+    int vec) {
+  const int i0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i0 >= d) return;
+  // rows blockIdx.y, + gridDim.y, ... (the grid's y extent is capped at 65535)
+  for (int64_t t = blockIdx.y; t < T_rows; t += gridDim.y) {
+    const uint16_t* xr = x + t * xs;
+    uint16_t* orow = out + t * os;
+    if (vec) {
+      u4 a = load_u4(xr + i0), b = load_u4(xr + d + i0), o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float g0 = f32_round(gelu_tanh(T::to_f32(a[e] & 0xFFFF)) * T::to_f32(b[e] & 0xFFFF));
-      float g1 = f32_round(gelu_tanh(T::to_f32(a[e] >> 16)) * T::to_f32(b[e] >> 16));
-      o[e] = (uint32_t)T::from_f32(g0) | ((uint32_t)T::from_f32(g1) << 16);
+      for (int e = 0; e < 4; ++e) {
+        float g0 = f32_round(gelu_tanh(T::to_f32(a[e] & 0xFFFF)) * T::to_f32(b[e] & 0xFFFF));
+        float g1 = f32_round(gelu_tanh(T::to_f32(a[e] >> 16)) * T::to_f32(b[e] >> 16));
+        o[e] = (uint32_t)T::from_f32(g0) | ((uint32_t)T::from_f32(g1) << 16);
+      }
+      *reinterpret_cast<u4*>(orow + i0) = o;
+    } else {
+      for (int i = i0, e = 0; e < 8; ++e, ++i)
+        if (i < d) orow[i] = T::from_f32(f32_round(gelu_tanh(T::to_f32(xr[i])) * T::to_f32(xr[d + i])));
     }
-    *reinterpret_cast<u4*>(orow + i) = o;
-  } else {
-    for (int i = (blockIdx.x * 256 + threadIdx.x) * 8, e = 0; e < 8; ++e, ++i)
-      if (i < d) orow[i] = T::from_f32(f32_round(gelu_tanh(T::to_f32(xr[i])) * T::to_f32(xr[d + i])));
   }
 }
 
@@ -125,22 +128,139 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
+// 16-byte form for hd = 16 L (L = 2 .. 32, a power of two), 16-byte aligned
+// rows and weights: L lanes own a head, lane c of them the 16-byte chunks c
+// and c + L (elements 8 c .. 8 c + 7 and hd / 2 + 8 c ..).  NeoX pairs are
+// then element e of the first chunk with element e of the second; GPT-J
+// pairs sit inside each chunk.  A wave holds 64 / L heads at once; the head's
+// sum of squares is an xor-butterfly over its L lanes.  Same arithmetic per
+// element as qk_norm_rope_kernel (its order of the squares' sum aside).
+template <typename T, int L>
+__global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
+    uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    const int64_t* __restrict__ positions, int nq, int nk,
+    int64_t qs, int64_t ks, float eps, float theta, int neox, int heads_per_wg) {
+  constexpr int HD = 16 * L, HALF = 8 * L, HPW = 64 / L;  // heads per wave and pass
+  __shared__ float cs[HALF], sn[HALF];
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane % L;
+  const int hbase = (int)blockIdx.y * heads_per_wg;
+  const int h_end = min(nq + nk, hbase + heads_per_wg);
+  auto head = [&](int h) {
+    return h < nq ? q + (size_t)t * qs + (size_t)h * HD : k + (size_t)t * ks + (size_t)(h - nq) * HD;
+  };
+  // the pass's head of this lane, its two chunks and their weights
+  u4 va, vb, wa, wb;
+  auto load_head = [&](int h) {
+    if (h < h_end) {
+      const uint16_t* v = head(h);
+      const uint16_t* w = h < nq ? qw : kw;
+      va = load_u4(v + 8 * c);
+      vb = load_u4(v + HALF + 8 * c);
+      wa = load_u4(w + 8 * c);
+      wb = load_u4(w + HALF + 8 * c);
+    } else {
+      va = vb = wa = wb = u4{0u, 0u, 0u, 0u};
+    }
+  };
+  const int h_first = hbase + wave * HPW + lane / L;
+  // the first pass's loads go out before the fp64 cos/sin table, so their
+  // latency overlaps its arithmetic (the barrier below waits for both)
+  load_head(h_first);
+  asm volatile("" ::: "memory");
+  const double pos = (double)positions[t];
+  const double lt = log2((double)theta);
+  for (int i = threadIdx.x; i < HALF; i += 256) {
+    const double inv_freq = exp2(-(double)(2 * i) / (double)HD * lt);
+    double sd, cd;
+    sincos(pos * inv_freq, &sd, &cd);
+    cs[i] = (float)cd;
+    sn[i] = (float)sd;
+  }
+  __syncthreads();
+
+  for (int h = h_first; h - lane / L - wave * HPW < h_end; h += 4 * HPW) {
+    if (h != h_first) load_head(h);
+    float a[8], b[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[2 * e] = T::to_f32(va[e] & 0xFFFF);
+      a[2 * e + 1] = T::to_f32(va[e] >> 16);
+      b[2 * e] = T::to_f32(vb[e] & 0xFFFF);
+      b[2 * e + 1] = T::to_f32(vb[e] >> 16);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss = fmaf(a[e], a[e], ss);
+      ss = fmaf(b[e], b[e], ss);
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = rsqrtf(ss / (float)HD + eps);
+    // norm, then round to the activation type before the rotation
+    float na[8], nb[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      na[2 * e] = T::to_f32(T::from_f32(f32_round(a[2 * e] * inv * T::to_f32(wa[e] & 0xFFFF))));
+      na[2 * e + 1] = T::to_f32(T::from_f32(f32_round(a[2 * e + 1] * inv * T::to_f32(wa[e] >> 16))));
+      nb[2 * e] = T::to_f32(T::from_f32(f32_round(b[2 * e] * inv * T::to_f32(wb[e] & 0xFFFF))));
+      nb[2 * e + 1] = T::to_f32(T::from_f32(f32_round(b[2 * e + 1] * inv * T::to_f32(wb[e] >> 16))));
+    }
+    u4 oa, ob;
+    if (neox) {
+      // pair p = 8 c + e: (na[e], nb[e])
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p0 = 8 * c + 2 * e, p1 = p0 + 1;
+        const float x0 = na[2 * e] * cs[p0] - nb[2 * e] * sn[p0];
+        const float x1 = na[2 * e + 1] * cs[p1] - nb[2 * e + 1] * sn[p1];
+        const float y0 = nb[2 * e] * cs[p0] + na[2 * e] * sn[p0];
+        const float y1 = nb[2 * e + 1] * cs[p1] + na[2 * e + 1] * sn[p1];
+        oa[e] = (uint32_t)T::from_f32(x0) | ((uint32_t)T::from_f32(x1) << 16);
+        ob[e] = (uint32_t)T::from_f32(y0) | ((uint32_t)T::from_f32(y1) << 16);
+      }
+    } else {
+      // pairs inside each chunk: chunk c holds pairs 4 c + e, chunk c + L pairs 4 (c + L) + e
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pa = 4 * c + e, pb = 4 * (c + L) + e;
+        const float xa = na[2 * e] * cs[pa] - na[2 * e + 1] * sn[pa];
+        const float ya = na[2 * e + 1] * cs[pa] + na[2 * e] * sn[pa];
+        const float xb = nb[2 * e] * cs[pb] - nb[2 * e + 1] * sn[pb];
+        const float yb = nb[2 * e + 1] * cs[pb] + nb[2 * e] * sn[pb];
+        oa[e] = (uint32_t)T::from_f32(xa) | ((uint32_t)T::from_f32(ya) << 16);
+        ob[e] = (uint32_t)T::from_f32(xb) | ((uint32_t)T::from_f32(yb) << 16);
+      }
+    }
+    if (h < h_end) {
+      uint16_t* v = head(h);
+      *reinterpret_cast<u4*>(v + 8 * c) = oa;
+      *reinterpret_cast<u4*>(v + HALF + 8 * c) = ob;
+    }
+  }
+}
+
 }  // namespace cek
 
 using namespace cek;
 
 extern "C" int cek_gelu_and_mul(void* out, const void* x, int64_t T, int64_t d,
                                 int64_t x_stride, int64_t out_stride, int io_dtype, void* stream) {
-  if (T < 0 || d <= 0 || T > 65535 || d > INT32_MAX / 2 || x_stride < 2 * d || out_stride < d) return CEK_ERR_INVALID;
+  if (T < 0 || d <= 0 || d > INT32_MAX / 2 || x_stride < 2 * d || out_stride < d) return CEK_ERR_INVALID;
   if (T == 0) return CEK_OK;
   if (!out || !x) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   const int vec = d % 8 == 0 && x_stride % 8 == 0 && out_stride % 8 == 0 && aligned(x, 16) && aligned(out, 16);
-  dim3 grid((unsigned)((d + 2047) / 2048), (unsigned)T);
+  // one workgroup row per token up to the grid's y limit; beyond it each
+  // workgroup row walks tokens with a stride of 65535
+  dim3 grid((unsigned)((d + 2047) / 2048), (unsigned)(T < 65535 ? T : 65535));
   uint16_t* o = static_cast<uint16_t*>(out);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
-  if (io_dtype == CEK_F16) gelu_and_mul_kernel<F16><<<grid, 256, 0, st>>>(o, xp, (int)d, x_stride, out_stride, vec);
-  else if (io_dtype == CEK_BF16) gelu_and_mul_kernel<BF16><<<grid, 256, 0, st>>>(o, xp, (int)d, x_stride, out_stride, vec);
+  if (io_dtype == CEK_F16) gelu_and_mul_kernel<F16><<<grid, 256, 0, st>>>(o, xp, T, (int)d, x_stride, out_stride, vec);
+  else if (io_dtype == CEK_BF16) gelu_and_mul_kernel<BF16><<<grid, 256, 0, st>>>(o, xp, T, (int)d, x_stride, out_stride, vec);
   else return CEK_ERR_INVALID;
   return check_launch();
 }
@@ -157,18 +277,51 @@ extern "C" int cek_qk_norm_rope(void* q, void* k, const void* qw, const void* kw
   if (T == 0 || n_q + n_k == 0) return CEK_OK;
   if (!positions || (n_q > 0 && (!q || !qw)) || (n_k > 0 && (!k || !kw))) return CEK_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
+  const int nh = (int)(n_q + n_k);
+  uint16_t* qp = static_cast<uint16_t*>(q);
+  uint16_t* kp = static_cast<uint16_t*>(k);
+  const uint16_t* qwp = static_cast<const uint16_t*>(qw);
+  const uint16_t* kwp = static_cast<const uint16_t*>(kw);
+  // 16-byte form: hd = 16 L with L a power of two from 2 to 32, 16-byte
+  // aligned row starts (row strides in 8-element units) and weights.
+  const int64_t lph = head_dim / 16;
+  const bool vec = head_dim % 16 == 0 && lph >= 2 && lph <= 32 && (lph & (lph - 1)) == 0 &&
+                   (n_q == 0 || (aligned(q, 16) && q_stride % 8 == 0 && aligned(qw, 16))) &&
+                   (n_k == 0 || (aligned(k, 16) && k_stride % 8 == 0 && aligned(kw, 16)));
+  if (vec) {
+    // Heads per workgroup: a multiple of one pass (4 waves x 64 / L heads);
+    // all of a token's heads once there are enough tokens to fill the GPU,
+    // else one pass, so a decode step's few tokens spread over workgroups.
+    const int pass = 4 * (int)(64 / lph);
+    const int hpw = T >= 64 ? (nh + pass - 1) / pass * pass : pass;
+    const dim3 grid((unsigned)T, (unsigned)((nh + hpw - 1) / hpw));
+#define CEK_ROPE_VEC(TY, LL)                                                                                  \
+  qk_norm_rope_vec_kernel<TY, LL><<<grid, 256, 0, st>>>(qp, kp, qwp, kwp, positions, (int)n_q, (int)n_k, q_stride, \
+                                                        k_stride, eps, theta, is_neox, hpw)
+#define CEK_ROPE_VEC_ALL(TY)                   \
+  do {                                         \
+    switch (lph) {                             \
+      case 2: CEK_ROPE_VEC(TY, 2); break;      \
+      case 4: CEK_ROPE_VEC(TY, 4); break;      \
+      case 8: CEK_ROPE_VEC(TY, 8); break;      \
+      case 16: CEK_ROPE_VEC(TY, 16); break;    \
+      default: CEK_ROPE_VEC(TY, 32); break;    \
+    }                                          \
+  } while (0)
+    if (io_dtype == CEK_F16) CEK_ROPE_VEC_ALL(F16);
+    else if (io_dtype == CEK_BF16) CEK_ROPE_VEC_ALL(BF16);
+    else return CEK_ERR_INVALID;
+#undef CEK_ROPE_VEC_ALL
+#undef CEK_ROPE_VEC
+    return check_launch();
+  }
   const int ppl = (int)((head_dim / 2 + 63) / 64);
   // Heads per workgroup (a multiple of the 4 waves): all of a token's heads
   // once there are enough tokens to fill the GPU; otherwise one head per wave,
   // so a decode step's few tokens still spread over many workgroups (each
   // rebuilds its token's cos/sin table).
-  const int nh = (int)(n_q + n_k);
   const int hpw = T >= 64 ? (nh + 3) / 4 * 4 : 4;
   const dim3 grid((unsigned)T, (unsigned)((nh + hpw - 1) / hpw));
-  uint16_t* qp = static_cast<uint16_t*>(q);
-  uint16_t* kp = static_cast<uint16_t*>(k);
-  const uint16_t* qwp = static_cast<const uint16_t*>(qw);
-  const uint16_t* kwp = static_cast<const uint16_t*>(kw);
 #define CEK_ROPE_LAUNCH(TY, P)                                                                              \
   qk_norm_rope_kernel<TY, P><<<grid, 256, 0, st>>>(qp, kp, qwp, kwp, positions, (int)n_q, (int)n_k, (int)head_dim, \
                                                    q_stride, k_stride, eps, theta, is_neox, hpw)

@@ -1021,10 +1021,11 @@ static void launch_norm_t(GemvSegs& sg, const NormArgs& na, int skind, int M, in
   else by_rows(std::integral_constant<int, 5>{});
 }
 
-static bool overlaps(const void* a, const void* b, int64_t bytes) {
+// Whether [a, a + a_bytes) and [b, b + b_bytes) share a byte.
+static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
   const char* pa = static_cast<const char*>(a);
   const char* pb = static_cast<const char*>(b);
-  return pa < pb + bytes && pb < pa + bytes;
+  return pa < pb + b_bytes && pb < pa + a_bytes;
 }
 
 // The fused launch covers M <= 4 rows, K in {3072, 4096, 5120}, e4m3
@@ -1049,8 +1050,15 @@ int launch_norm_gemv(const NormArgs& na, const void* w, const void* scale, int s
   if (!aligned(na.h, 16) || !aligned(na.r, 16) || !aligned(na.w, 16) || !aligned(na.r_out, 16) || !aligned(w, 16) ||
       (na.h_out && !aligned(na.h_out, 16)) || (quant && !aligned(na.q_out, 16)))
     return CEK_ERR_UNSUPPORTED;
-  if (overlaps(na.r_out, na.r, rb) || overlaps(na.r_out, na.h, rb) ||
-      (na.h_out && (overlaps(na.h_out, na.r, rb) || overlaps(na.h_out, na.h, rb))))
+  // Every workgroup reads h and r in its prologue while others already write
+  // y and workgroup 0 writes the side outputs: no output may share memory
+  // with an input.
+  const int64_t yb = M * (glu ? N / 2 : N) * 2;
+  auto hits_inputs = [&](const void* p, int64_t bytes) {
+    return p && (overlaps(p, bytes, na.r, rb) || overlaps(p, bytes, na.h, rb) || overlaps(p, bytes, na.w, K * 2));
+  };
+  if (hits_inputs(na.r_out, rb) || hits_inputs(na.h_out, rb) || hits_inputs(y, yb) ||
+      (quant && (hits_inputs(na.q_out, M * K) || hits_inputs(na.s_out, M * 4))))
     return CEK_ERR_UNSUPPORTED;
   GemvSegs sg{};
   sg.count = 1;

@@ -7,6 +7,8 @@
 // written in place and returned as the reference does; nothing synchronises.
 #include "torch_ops.h"
 
+#include <ATen/MemoryOverlap.h>
+
 #include <algorithm>
 #include <vector>
 
@@ -355,6 +357,12 @@ void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Ten
 // batches of up to four rows run as one launch; other shapes, and a
 // residual_out that aliases the inputs, run the norm op on a copy and then
 // the GEMV op (the same values).
+// The norm kernels update their residual argument in place: residual_out
+// takes residual's values first (nothing to copy when it is residual).
+static void seed_residual_out(at::Tensor& residual_out, const at::Tensor& residual) {
+  if (at::get_overlap_status(residual_out, residual) != at::MemOverlapStatus::Full) residual_out.copy_(residual);
+}
+
 static void check_norm_gemv_common(const at::Tensor& h, const at::Tensor& r, const at::Tensor& nw,
                                    const at::Tensor& r_out, const at::Tensor& w, const at::Tensor& ws,
                                    const at::Tensor& y, bool glu, const char* op, int64_t& M, int64_t& N,
@@ -405,7 +413,7 @@ void esimd_fused_add_rms_norm_gemv_fp8(at::Tensor hidden_states, at::Tensor resi
   }
   // two launches: the norm in place on copies, then the GEMV
   at::Tensor x = hidden_states.clone();
-  if (!residual_out.is_same(residual)) residual_out.copy_(residual);
+  seed_residual_out(residual_out, residual);
   check_rc(cek_fused_add_rms_norm(x.data_ptr(), residual_out.data_ptr(), weight.data_ptr(), M, K, (float)eps, io, st),
            op);
   if (gelu_and_mul) esimd_gemv_fp8_gelu_and_mul(x.view({M, K}), w, w_scale, output.view({M, N / 2}));
@@ -435,9 +443,14 @@ void esimd_fused_add_rms_norm_quant_gemv_fp8(at::Tensor hidden_states, at::Tenso
     check_rc(rc, op);
     return;
   }
-  // two launches: norm + quant (hidden only read), then the a8w8 product
-  if (!residual_out.is_same(residual)) residual_out.copy_(residual);
-  check_rc(cek_fused_add_rms_norm_quant_fp8(hidden_states.data_ptr(), residual_out.data_ptr(), weight.data_ptr(), M, K,
+  // two launches: norm + quant (hidden only read), then the a8w8 product.
+  // hidden is read after residual_out has been seeded with residual, so it
+  // is read from a copy when residual_out shares its memory.
+  const at::Tensor h = at::get_overlap_status(residual_out, hidden_states) == at::MemOverlapStatus::No
+                           ? hidden_states
+                           : hidden_states.clone();
+  seed_residual_out(residual_out, residual);
+  check_rc(cek_fused_add_rms_norm_quant_fp8(h.data_ptr(), residual_out.data_ptr(), weight.data_ptr(), M, K,
                                             (float)eps, io, q, qs, st),
            op);
   const auto* bp = static_cast<const uint8_t*>(b.data_ptr());

@@ -15,7 +15,7 @@ fallback: a missing HIP library is an error there.
 
 Pinning (what checks each oracle function against something other than
 itself) is listed per module in its docstring; the tests that perform the
-pins live in ``tests/test_oracle_*.py``.
+pins live in ``tests/test_oracle_fp8.py`` (codec) and ``tests/test_oracle_ops.py`` (ops).
 """
 
 from . import fp8, gemv, norm, act, gemm, layer  # noqa: F401

@@ -17,7 +17,7 @@ qk_norm_rope, per head of q and of k (head size hd):
         [a_i, b_i] = [v_i, v_{i+hd/2}] -> [a cos - b sin, b cos + a sin]
     GPT-J interleaved: the pair is (v_{2i}, v_{2i+1}).
 
-Pins (tests/test_oracle_act.py): gelu against
+Pins (tests/test_oracle_ops.py): gelu against
 ``torch.nn.functional.gelu(approximate='tanh')`` and its limits; RoPE
 against complex multiplication by exp(i*theta) (a different formulation),
 norm preservation per pair, identity at position 0, and relative-position

@@ -7,7 +7,7 @@ The reference has no a8w8 op.  Definition, fp32 accumulate:
 computed here as the fp32 dequantise-then-matmul of the codes, the same
 style as the reference's GEMM oracle (``tests/test_gemm_fp8.py:35-36``).
 
-Pins (tests/test_oracle_gemm.py): float64 brute force on tiny shapes;
+Pins (tests/test_oracle_ops.py): float64 brute force on tiny shapes;
 a8w8 with sa == 1 equals the fp16-activation GEMM oracle of
 ``oracle.gemv`` when A's codes are fed as fp16 activations; bilinearity in
 (sa, sb).

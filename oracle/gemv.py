@@ -13,7 +13,7 @@ with the scale applied after the K reduction, as the kernels do
 the reference kernels compute row 0 only (``fp8_GEMV_v2.h:62-75``) and the
 build treats all rows (a superset).
 
-Pins (tests/test_oracle_gemv.py): float64 brute-force triple loop on tiny
+Pins (tests/test_oracle_ops.py): float64 brute-force triple loop on tiny
 shapes; y is linear in the scale; zero weights give zero; pert == pern with a
 uniform scale; GEMM at M=1 == GEMV; decoding through ``oracle.fp8`` tables
 equals decoding through torch.

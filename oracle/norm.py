@@ -16,7 +16,7 @@ it and the oracle tests check both agree within the op tolerance.
 The fp8 extension (the reference has no op for it): quantise the fp16-rounded
 normed row per token with ``oracle.fp8.per_token_quant``.
 
-Pins (tests/test_oracle_norm.py): r' is f16(h+r) elementwise (checked
+Pins (tests/test_oracle_ops.py): r' is f16(h+r) elementwise (checked
 against numpy float16 addition), the normed output against a float64 loop and
 against ``torch.nn.functional.rms_norm``, scale invariance of the normed
 output, and the quant codes against ``oracle.fp8`` brute force.

@@ -28,12 +28,12 @@ def dev():
 
 
 def assert_close_fp(out, ref, what="", atol_frac=1e-2, rtol=2e-2):
-    """Tolerance of the op pack for floating-point outputs.
+    """Tolerance of the op pack for floating-point outputs (the bar BASELINE
+    states: max-abs error <= 1e-2 * max|ref| and rtol 2e-2).
 
-    Every element must satisfy |out - ref| <= atol + rtol * |ref| with
-    atol = atol_frac * max|ref|; in particular the max-abs error is at most
-    (atol_frac + rtol) * max|ref| and, for elements far below max|ref|, the
-    bound is dominated by atol = 1e-2 * max|ref|.
+    Two conditions, both asserted:
+      * max |out - ref| <= atol_frac * max|ref|   (the max-abs bound, alone);
+      * every element |out - ref| <= atol + rtol * |ref|, atol = atol_frac * max|ref|.
     """
     import torch
     out = torch.as_tensor(out).detach().cpu().double()
@@ -47,4 +47,5 @@ def assert_close_fp(out, ref, what="", atol_frac=1e-2, rtol=2e-2):
     maxerr = err.max().item() if err.numel() else 0.0
     assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of tolerance; max err {maxerr:.4g}, "
                            f"max|ref| {refmax:.4g}")
+    assert maxerr <= atol, f"{what}: max-abs error {maxerr:.4g} > {atol_frac:g} * max|ref| = {atol:.4g}"
     return maxerr, refmax

@@ -3,9 +3,11 @@
 esimd_gemm_fp8_pert: the reference's GEMM test grid (reference
 tests/test_gemm_fp8.py:13-23: M in {1..64} x 6 (N, K), e4m3/e5m2,
 fp16/bf16 IO, scale 0.05..0.15) plus prefill M.
-esimd_gemm_fp8_a8w8: BASELINE config 4 at M = 512 against the CPU oracle,
-and at M = 2048 against a float32 torch GPU matmul of the dequantised codes
-(the oracle's formula on the GPU; the CPU oracle at that size takes minutes).
+esimd_gemm_fp8_a8w8: every BASELINE config-4 shape (M in {512, 2048, 4096}
+x (K, N) in {(4096, 6144), (4096, 28672), (14336, 4096)}) against the CPU
+oracle (an fp32 CPU matmul of the dequantised codes: about a second per
+shape on the host's cores); tile and split-K edge cases against a float32
+torch GPU matmul of the same codes.
 """
 
 import sys
@@ -66,30 +68,30 @@ def _a8w8_inputs(M, K, N, seed):
     return q, sa, W8.view(torch.uint8), sb
 
 
+def _a8w8_inputs_config4(M, K, N, seed):
+    """Config-4 operands at full size: A per-token e4m3 from fp16 N(0, 1), B
+    per-channel e4m3 from N(0, 0.02) (the synthetic recipe).  A's codes come
+    from torch's CPU e4m3 conversion of x / s (RNE, the oracle's formula; the
+    numpy oracle codec is pinned to it and takes tens of seconds at this size)."""
+    x = synthetic.activations(M, K, seed=seed).float()
+    sa = torch.clamp(x.abs().amax(dim=1) / 448.0, min=1.0 / (448.0 * 512.0))
+    q = (x / sa[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+    W8, sb = synthetic.weight_fp8(N, K, seed=seed + 1)
+    return q, sa, W8.view(torch.uint8), sb
+
+
+@pytest.mark.parametrize("M", [512, 2048, 4096])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 28672), (14336, 4096)])
-def test_a8w8_config4_m512(ops, dev, K, N):
-    M = 512
-    _say(f"a8w8 M={M} K={K} N={N}")
-    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=K + N)
-    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+def test_a8w8_config4(ops, dev, M, K, N):
+    """BASELINE config 4, every (M, K, N), against the CPU oracle."""
+    _say(f"a8w8 config 4 M={M} K={K} N={N}")
+    q, sa, W8, sb = _a8w8_inputs_config4(M, K, N, seed=M + K + N)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
     ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev), y)
     torch.cuda.synchronize()
-    assert_close_fp(y.cpu(), ogemm.gemm_a8w8(q, sa, W8, sb), f"a8w8 K={K} N={N}")
-
-
-@pytest.mark.parametrize("K,N", [(4096, 6144), (14336, 4096)])
-def test_a8w8_m2048_vs_gpu_fp32(ops, dev, K, N):
-    M = 2048
-    _say(f"a8w8 M={M} K={K} N={N} vs fp32 torch")
-    q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=K)
-    qd, Wd = q.to(dev), W8.to(dev)
-    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
-    ops.esimd_gemm_fp8_a8w8(qd, sa.to(dev), Wd, sb.to(dev), y)
-    A = qd.view(torch.float8_e4m3fn).float()
-    B = Wd.view(torch.float8_e4m3fn).float()
-    ref = (A @ B.T) * sa.to(dev)[:, None] * sb.to(dev)[None, :]
-    torch.cuda.synchronize()
-    assert_close_fp(y.cpu(), ref.cpu(), f"a8w8 M=2048 K={K} N={N}")
+    out = y.cpu()
+    del y
+    assert_close_fp(out, ogemm.gemm_a8w8(q, sa, W8, sb), f"a8w8 M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 128, 16), (17, 48, 33), (64, 256, 64), (130, 1040, 250)])

@@ -84,17 +84,28 @@ def test_gemm_pert_skinny(ops, dev, M, K, N):
                                    (48, 4096, 9000)])
 def test_a8w8_skinny(ops, dev, M, K, N):
     """a8w8 M <= 64: LDS kernel with 1, 2 and 4 activation blocks (and the
-    tiled GEMM for M > 32, N > 8192)."""
+    tiled GEMM for M > 32, N > 8192).  The torch op gives the split-K plan
+    its workspace, which at M = 64 (64 x 128 tiles in K parts) replaces the
+    weight-streaming kernel; the C-ABI call without a workspace
+    (cek_gemm_fp8_a8w8) keeps the 4-block LDS kernel there, so both are run."""
+    from esimd_learning_amd import cabi
     _say(f"lds a8w8 M={M} K={K} N={N}")
+    lib = cabi.load()
     x = synthetic.activations(M, K, seed=M + 5)
     q, sa = onorm.per_token_quant(x)
     W8, sb = synthetic.weight_fp8(N, K, seed=K + 3)
     ref = ogemm.gemm_a8w8(q, sa, W8.view(torch.uint8), sb)
-    for out_dt in (torch.float16, torch.bfloat16):
+    qd, sad, Wd, sbd = q.to(dev), sa.to(dev), W8.view(torch.uint8).to(dev), sb.to(dev)
+    st = cabi.stream_ptr(torch.cuda.current_stream())
+    for code, out_dt in ((0, torch.float16), (1, torch.bfloat16)):
         y = torch.zeros(M, N, dtype=out_dt, device=dev)
-        ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.view(torch.uint8).to(dev), sb.to(dev), y)
+        ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y)
+        y_nows = torch.zeros(M, N, dtype=out_dt, device=dev)
+        assert lib.cek_gemm_fp8_a8w8(qd.data_ptr(), sad.data_ptr(), Wd.data_ptr(), sbd.data_ptr(), y_nows.data_ptr(),
+                                     M, N, K, code, st) == 0
         torch.cuda.synchronize()
         assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
+        assert_close_fp(y_nows.cpu(), ref, f"a8w8 no workspace M={M} K={K} N={N} {out_dt}")
 
 
 def test_fused_segments_lds(ops, dev):

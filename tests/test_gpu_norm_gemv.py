@@ -205,3 +205,66 @@ def test_norm_gemv_residual_in_place(ops, dev, quant):
     torch.cuda.synchronize()
     assert torch.equal(rd.cpu(), r_ref)
     assert_close_fp(y.cpu(), ref, f"in-place residual quant={quant}")
+
+
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("M,K", [(4, 3072), (6, 4096), (2, 2048)])
+def test_norm_gemv_residual_out_is_hidden(ops, dev, quant, M, K):
+    """residual_out aliasing hidden_states: the two-launch path seeds
+    residual_out with residual, so it must read hidden from a copy first
+    (M = 4 would be a fused shape, M = 6 and K = 2048 are two-launch shapes
+    by size)."""
+    N = 1040
+    dt = torch.float16
+    _say(f"norm+gemv residual_out=hidden M={M} K={K} quant={quant}")
+    h, r, g, W8, s = _inputs(M, K, N, dt, seed=9 + M + K)
+    hd = h.to(dev)
+    y = torch.zeros(M, N, dtype=dt, device=dev)
+    if quant:
+        q = torch.zeros(M, K, dtype=torch.uint8, device=dev)
+        qs = torch.zeros(M, dtype=torch.float32, device=dev)
+        ops.esimd_fused_add_rms_norm_quant_gemv_fp8(hd, r.to(dev), g.to(dev), EPS, hd, q, qs,
+                                                    W8.view(torch.uint8).to(dev), s.float().to(dev), y)
+        r_ref, q_ref, s_ref, _ = onorm.fused_add_rms_norm_quant(h, r, g, EPS)
+        ref = ogemm.gemm_a8w8(q_ref, s_ref, W8.view(torch.uint8), s.float())
+    else:
+        ops.esimd_fused_add_rms_norm_gemv_fp8(hd, r.to(dev), g.to(dev), EPS, hd, W8.to(dev), s.to(dev), y)
+        r_ref, normed = onorm.fused_add_rms_norm(h, r, g, EPS)
+        ref = ogemv.gemv_fp8_pern(normed.to(dt), W8, s)
+    torch.cuda.synchronize()
+    assert torch.equal(hd.cpu(), r_ref)
+    if quant:
+        _codes_near_oracle(q.cpu(), qs.cpu(), q_ref, s_ref, 2.0 ** -10)
+    assert_close_fp(y.cpu(), ref, f"residual_out=hidden M={M} K={K} quant={quant}")
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_norm_gemv_output_aliasing_input_falls_back(ops, dev, quant):
+    """An output that shares memory with an input (here y over the tail of
+    residual) would race in the fused launch: the op takes the two-launch
+    path and the values stay those of the unaliased call."""
+    M, K, N = 2, 4096, 2048
+    dt = torch.float16
+    _say(f"norm+gemv y aliasing residual quant={quant}")
+    h, r, g, W8, s = _inputs(M, K, N, dt, seed=21)
+    # residual [M, K] followed by y [M, N] in one buffer, y starting inside residual's last row
+    buf = torch.zeros(M * K + M * N, dtype=dt, device=dev)
+    rv = buf[: M * K].view(M, K)
+    rv.copy_(r.to(dev))
+    off = M * K - 1024
+    yv = buf[off: off + M * N].view(M, N)
+    r_out = torch.zeros(M, K, dtype=dt, device=dev)
+    if quant:
+        q = torch.zeros(M, K, dtype=torch.uint8, device=dev)
+        qs = torch.zeros(M, dtype=torch.float32, device=dev)
+        ops.esimd_fused_add_rms_norm_quant_gemv_fp8(h.to(dev), rv, g.to(dev), EPS, r_out, q, qs,
+                                                    W8.view(torch.uint8).to(dev), s.float().to(dev), yv)
+        r_ref, q_ref, s_ref, _ = onorm.fused_add_rms_norm_quant(h, r, g, EPS)
+        ref = ogemm.gemm_a8w8(q_ref, s_ref, W8.view(torch.uint8), s.float())
+    else:
+        ops.esimd_fused_add_rms_norm_gemv_fp8(h.to(dev), rv, g.to(dev), EPS, r_out, W8.to(dev), s.to(dev), yv)
+        r_ref, normed = onorm.fused_add_rms_norm(h, r, g, EPS)
+        ref = ogemv.gemv_fp8_pern(normed.to(dt), W8, s)
+    torch.cuda.synchronize()
+    assert torch.equal(r_out.cpu(), r_ref)
+    assert_close_fp(yv.cpu(), ref, f"y aliasing residual quant={quant}")

@@ -15,7 +15,7 @@ HEADER = PKG_DIR.parent / "include" / "cek.h"
 
 CEK_F16, CEK_BF16, CEK_F32 = 0, 1, 2
 CEK_E4M3, CEK_E5M2 = 0, 1
-CEK_OK, CEK_ERR_INVALID, CEK_ERR_UNSUPPORTED, CEK_ERR_HIP = 0, 1, 2, 3
+CEK_OK, CEK_ERR_INVALID, CEK_ERR_UNSUPPORTED, CEK_ERR_HIP, CEK_ERR_SCRATCH = 0, 1, 2, 3, 4
 
 _p, _i64, _i, _f = C.c_void_p, C.c_int64, C.c_int, C.c_float
 
@@ -34,6 +34,7 @@ SIGNATURES = {
     "cek_gemm_fp8_a8w8": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p]),
     "cek_gemm_fp8_a8w8_workspace_size": (_i64, [_i64, _i64, _i64]),
     "cek_gemm_fp8_a8w8_ws": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p, _i64, _p]),
+    "cek_gemm_fp8_a8w8_noalloc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p]),
     "cek_gelu_and_mul": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p]),
     "cek_gemv_fp8_gelu_and_mul": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_add_rms_norm_gemv_fp8": (_i, [_p, _p, _p, _f, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _i,

@@ -22,6 +22,7 @@ extern "C" const char* cek_error_string(int status) {
     case CEK_ERR_INVALID: return "invalid argument (size, pointer, alignment or enum value)";
     case CEK_ERR_UNSUPPORTED: return "unsupported configuration";
     case CEK_ERR_HIP: return "HIP runtime error (see cek_last_hip_error)";
+    case CEK_ERR_SCRATCH: return "request needs more than the library's static scratch buffer holds";
     default: return "unknown status";
   }
 }

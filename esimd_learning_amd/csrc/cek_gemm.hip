@@ -16,6 +16,9 @@
 // same register slots, so any K ordering the hardware uses inside an
 // instruction cancels out.  The accumulator of a 16 x 16 block holds
 // D[4 * (l >> 4) + v][l & 15] in element v of lane l.
+#include <atomic>
+#include <mutex>
+
 #include "cek_common.h"
 
 namespace cek {
@@ -1132,6 +1135,67 @@ extern "C" int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uin
 extern "C" int cek_gemm_fp8_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
                                  void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream) {
   return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, nullptr, 0, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Split-K scratch of cek_gemm_fp8_a8w8_noalloc: a file-scope device array,
+// one copy per GPU the library runs on, held until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is only a
+// handle of the symbol): each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current, and
+// only that address is used.  The split-K kernels write every partial sum
+// they later read, so the buffer needs no clearing between calls; calls that
+// overlap on one GPU (e.g. on two streams) share it and race.
+// ---------------------------------------------------------------------------
+namespace cek {
+
+constexpr int64_t kScratchBytes = (int64_t)32 << 20;  // 32 MiB: every BASELINE split-K plan fits
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the device `st` runs on (taken once per
+// device); CEK_OK or an error status.
+static int scratch_address(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return record_hip_error(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return CEK_ERR_UNSUPPORTED;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      int cur = -1;
+      e = hipGetDevice(&cur);
+      if (e != hipSuccess) return record_hip_error(e);
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return record_hip_error(e);
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      const hipError_t e2 = cur != dev ? hipSetDevice(cur) : hipSuccess;
+      if (e != hipSuccess) return record_hip_error(e);
+      if (e2 != hipSuccess) return record_hip_error(e2);
+      if (!p) return CEK_ERR_HIP;
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return CEK_OK;
+}
+
+}  // namespace cek
+
+extern "C" int cek_gemm_fp8_a8w8_noalloc(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
+                                         void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t need = cek::a8w8_workspace_bytes(M, N, K);
+  if (need > cek::kScratchBytes) return CEK_ERR_SCRATCH;
+  if (need == 0) return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, nullptr, 0, st);
+  void* ws = nullptr;
+  const int rc = cek::scratch_address(st, &ws);
+  if (rc != CEK_OK) return rc;
+  return cek::launch_a8w8(a, sa, b, sb, y, M, N, K, out_dtype, static_cast<float*>(ws), cek::kScratchBytes, st);
 }
 
 namespace cek {

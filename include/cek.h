@@ -6,7 +6,8 @@
  * counts; `stream` is a hipStream_t passed as void* (NULL = legacy default
  * stream).  Every entry point only enqueues work on `stream`: no host
  * synchronisation, no host read of device scales, no allocation.  Entry
- * points are stateless and re-entrant.  Return value: CEK_OK (0) or a
+ * points are stateless and re-entrant (cek_gemm_fp8_a8w8_noalloc aside: its
+ * calls share one static buffer per GPU).  Return value: CEK_OK (0) or a
  * CEK_ERR_* code; cek_error_string() names it.  Nothing throws across the
  * ABI.
  *
@@ -34,7 +35,8 @@ enum cek_status {
   CEK_OK = 0,
   CEK_ERR_INVALID = 1,      /* bad size, pointer, alignment or enum value */
   CEK_ERR_UNSUPPORTED = 2,  /* valid request this build has no kernel for */
-  CEK_ERR_HIP = 3           /* a HIP runtime call or launch failed */
+  CEK_ERR_HIP = 3,          /* a HIP runtime call or launch failed */
+  CEK_ERR_SCRATCH = 4       /* request needs more than the static scratch buffer holds */
 };
 
 const char* cek_error_string(int status);
@@ -149,6 +151,22 @@ int64_t cek_gemm_fp8_a8w8_workspace_size(int64_t M, int64_t N, int64_t K);
 int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
                          void* y, int64_t M, int64_t N, int64_t K, int out_dtype,
                          void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * NEW, and with no counterpart in the reference: the a8w8 GEMM for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * cek_gemm_fp8_a8w8_ws given the workspace its plan asks for, but the
+ * split-K partial sums go to a static device buffer inside the library
+ * (32 MiB, one per GPU, held until the process ends); the call allocates
+ * nothing.  Shapes whose plan needs more (cek_gemm_fp8_a8w8_workspace_size
+ * above 33554432 bytes) return CEK_ERR_SCRATCH; shapes that run unsplit use
+ * no scratch.  The first call on a device looks up the buffer's address on
+ * that device.  All calls on one GPU share the buffer: calls that overlap in
+ * time there (e.g. on two streams) race.
+ */
+int cek_gemm_fp8_a8w8_noalloc(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
+                              void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
 
 /*
  * NEW: out[t, i] = gelu_tanh(x[t, i]) * x[t, d + i], fp32 math.

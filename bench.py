@@ -21,7 +21,9 @@ Further legs (same JSON line): "gemm" (a8w8 at M = 2048,
 three projections), "gemm_pert" (the reference's esimd_gemm_fp8_pert, w8a16,
 same shapes), "decoder_layer" (config 5, one graph-replayed step),
 "gemv_shapes" (config 2, every M x shape), "norm_quant_gemv" (config 3,
-fused add+RMSNorm+quant then the fp8 GEMV/GEMM to N = 6144), and the device
+fused add+RMSNorm+quant then the fp8 GEMV/GEMM to N = 6144), "small_ops"
+(the norm, quant, gelu_and_mul and QK-norm+RoPE kernels at T = 4 and 64;
+--small-ops-only runs just this leg), and the device
 copy rate the headline is also quoted against (roofline.copy_GBps).
 roofline.read_ceiling_us is cek_hbm_read_probe (a read-only kernel) over
 the same rotating weight copies, timed the same way: the practical ceiling
@@ -29,7 +31,8 @@ of one pass over those bytes on this GPU, beside the 8 TB/s spec peak.
 
 cpu_baseline: the reference's torch CPU path restated in oracle/
 ((x.float() @ W8.to(fp16).float().T) * s) on this host's cores, timed on the
-same shape (2 warm-ups, median of 5).
+same shape (2 warm-ups, median of 5); sub-keys time the CPU path of the other
+legs (GEMV M = 16, norm+quant T = 64, a8w8 GEMM M = 2048, decoder step).
 """
 
 import argparse
@@ -276,24 +279,34 @@ def bench_norm_quant_gemv(ops, torch, reps=50, N=6144):
     return rows
 
 
-def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144):
+def bench_gemm(ops, torch, steps, warmup, M=2048, K=4096, N=6144, rotate=False):
+    """One a8w8 shape: `steps` launches in one graph, event-timed.  With
+    rotate, launch i reads weight copy i % C of C copies totalling > 2 GB
+    (weights from HBM, as a prefill streaming fresh layers sees them);
+    otherwise every launch re-reads one copy (Infinity Cache resident)."""
     from esimd_learning_amd import synthetic
     dev = "cuda:0"
-    log(f"gemm a8w8: M={M} K={K} N={N}")
+    log(f"gemm a8w8: M={M} K={K} N={N}" + (" (rotating weights)" if rotate else ""))
     x = synthetic.activations(M, K, seed=2).to(dev)
     q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
     sa = torch.empty(M, dtype=torch.float32, device=dev)
     ops.esimd_per_token_quant_fp8(x, q, sa)
     W8, sb = synthetic.weight_fp8(N, K, seed=3)
     Wd, sbd = W8.to(dev), sb.to(dev)
+    copies = max(2, math.ceil(ROTATE_BYTES / (N * K))) if rotate else 1
+    Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
     y = torch.empty(M, N, dtype=torch.float16, device=dev)
     stream = torch.cuda.Stream()
-    fn = lambda: ops.esimd_gemm_fp8_a8w8(q, sa, Wd, sbd, y)  # noqa: E731
+    fns = [(lambda W=W: ops.esimd_gemm_fp8_a8w8(q, sa, W, sbd, y)) for W in Ws]
+    fn = fns[0]
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             fn()
     torch.cuda.synchronize()
-    wall, ev_ms, _ = time_graph([fn] * steps, torch, stream, warm_s=WARM_S)
+    if rotate:
+        steps = max(steps, copies)
+    wall, ev_ms, _ = time_graph([fns[i % copies] for i in range(steps)], torch, stream, warm_s=WARM_S)
+    del Ws
     flops = 2.0 * M * N * K
     us = ev_ms * 1e3 / steps
     return {"config": f"a8w8 M={M} K={K} N={N}", "avg_launch_us": us,
@@ -320,14 +333,14 @@ def bench_gemm_all(ops, torch, steps, warmup, all_m=True):
         head["m_table"] = []
         for M in (512, 4096):
             for K, N in ((4096, 6144), (4096, 28672), (14336, 4096)):
-                r = bench_gemm(ops, torch, steps, warmup, M=M, K=K, N=N)
+                r = bench_gemm(ops, torch, steps, warmup, M=M, K=K, N=N, rotate=True)
                 flops = 2.0 * M * N * K
                 byts = M * K + N * K + 2 * M * N + 4 * M + 4 * N
                 roof_us = max(flops / (FP8_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9)) * 1e6
                 head["m_table"].append({"M": M, "K": K, "N": N, "avg_launch_us": round(r["avg_launch_us"], 2),
                                         "tflops": round(r["tflops"], 1), "roofline_us": round(roof_us, 2),
                                         "frac_of_roofline": round(roof_us / r["avg_launch_us"], 3),
-                                        "weights": "one copy, re-read across launches (Infinity Cache resident)"})
+                                        "weights": "rotating copies over > 2 GB (read from HBM)"})
     return head
 
 
@@ -357,6 +370,53 @@ def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
         rows.append({"config": f"w8a16 M={M} K={K} N={N}", "avg_launch_us": round(us, 2), "tflops": round(tf, 1),
                      "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
         del x, Wd, y
+    return rows
+
+
+def bench_small_ops(ops, torch, reps=200):
+    """The HBM/latency-bound small kernels at decode (T = 4, the config-5
+    shapes) and prefill (T = 64) sizes: add+RMSNorm, add+RMSNorm+quant,
+    per-token quant (H = 3072), gelu_and_mul (d = 24576) and QK-norm+RoPE
+    (16 q + 16 k heads x 256 in a [T, 12288] QKV buffer).  Each a graph of
+    `reps` launches over one set of buffers, event-timed; bytes are the
+    algorithmic bytes per launch (reads + writes)."""
+    from esimd_learning_amd import synthetic
+    dev = "cuda:0"
+    stream = torch.cuda.Stream()
+    H, d, hd, nq, nk = 3072, 24576, 256, 16, 16
+    rows = []
+    for T in (4, 64):
+        h = synthetic.activations(T, H, seed=T).to(dev)
+        r = synthetic.activations(T, H, seed=T + 1).to(dev)
+        w = synthetic.norm_weight(H, seed=H).to(dev)
+        q8 = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+        s8 = torch.empty(T, dtype=torch.float32, device=dev)
+        gu = synthetic.activations(T, 2 * d, seed=T + 2).to(dev)
+        act = torch.empty(T, d, dtype=torch.float16, device=dev)
+        qkv = synthetic.activations(T, (nq + 2 * nk) * hd, seed=T + 3).to(dev)
+        qw, kw = synthetic.norm_weight(hd, 1).to(dev), synthetic.norm_weight(hd, 2).to(dev)
+        pos = synthetic.positions(T, seed=T).to(dev)
+        legs = {
+            # in place: reads hidden and residual, writes both
+            "add_rmsnorm": (lambda: ops.esimd_fused_add_rms_norm_batched(h, r, w, 1e-6), 4 * T * H * 2 + H * 2),
+            "add_rmsnorm_quant": (lambda: ops.esimd_fused_add_rms_norm_quant_fp8(h, r, w, 1e-6, q8, s8),
+                                  3 * T * H * 2 + H * 2 + T * H + T * 4),
+            "per_token_quant": (lambda: ops.esimd_per_token_quant_fp8(h, q8, s8), T * H * 2 + T * H + T * 4),
+            "gelu_and_mul": (lambda: ops.esimd_gelu_and_mul(act, gu), T * 2 * d * 2 + T * d * 2),
+            "qk_norm_rope": (lambda: ops.esimd_qk_norm_rope(qkv[:, : nq * hd], qkv[:, nq * hd:(nq + nk) * hd], qw, kw,
+                                                            pos, 1e-6, 10000.0, True),
+                             2 * T * (nq + nk) * hd * 2 + 2 * hd * 2 + T * 8),
+        }
+        for name, (fn, nbytes) in legs.items():
+            with torch.cuda.stream(stream):
+                fn()
+            torch.cuda.synchronize()
+            # (the norms update the residual in place, so it grows by about
+            # one unit per call: a short warm keeps every value finite)
+            _, ms, _ = time_graph([fn] * reps, torch, stream, warm_s=0.02)
+            us = ms * 1e3 / reps
+            rows.append({"op": name, "T": T, "us": round(us, 2), "bytes": nbytes,
+                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)})
     return rows
 
 
@@ -430,47 +490,111 @@ def bench_layer(torch, steps, M=4, rounds=5):
     return out
 
 
+def _cpu_model():
+    """The host CPU's model name (lscpu, else /proc/cpuinfo) and socket/core counts."""
+    import subprocess
+    model, extra = "", ""
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {}
+        for line in txt.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                kv[k.strip()] = v.strip()
+        model = kv.get("Model name", "")
+        extra = ", ".join(f"{k} {kv[k]}" for k in ("Socket(s)", "Core(s) per socket", "Thread(s) per core",
+                                                   "CPU(s)") if k in kv)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not model:
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    return model, extra
+
+
+def _time_cpu(fn, reps, warm=2):
+    """Median wall time (s) of fn over reps calls after warm calls."""
+    ts = []
+    for i in range(warm + reps):
+        t0 = time.perf_counter()
+        fn()
+        if i >= warm:
+            ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def cpu_baseline(torch, M=1, K=4096, N=14336, reps=5):
+    """The reference's torch CPU path, restated in oracle/, on this host's
+    cores beside each GPU leg: the headline GEMV (value), plus the batched
+    GEMV at M = 16, add+RMSNorm+quant at T = 64, the a8w8 GEMM at M = 2048
+    and the decoder-layer step (sub-keys).  About 10-20 s in all."""
     from esimd_learning_amd import synthetic
+    from oracle import gemm as ogemm
     from oracle import gemv as ogemv
+    from oracle import layer as olayer
+    from oracle import norm as onorm
     torch.set_num_threads(os.cpu_count() or 1)
     W8, s = synthetic.weight_fp8(N, K, seed=0)
     x = synthetic.activations(M, K, seed=1)
-    ts = []
-    for i in range(2 + reps):
-        t0 = time.perf_counter()
-        ogemv.gemv_fp8_pern(x, W8, s)
-        if i >= 2:
-            ts.append(time.perf_counter() - t0)
-    ts.sort()
-    med = ts[len(ts) // 2]
+    med = _time_cpu(lambda: ogemv.gemv_fp8_pern(x, W8, s), reps)
     # the same with the weights dequantised once up front (matmul + scale only)
     Wf = W8.to(torch.float16).float()
     xf = x.float()
-    tm = []
-    for i in range(2 + reps):
-        t0 = time.perf_counter()
-        (xf @ Wf.T) * s.float()
-        if i >= 2:
-            tm.append(time.perf_counter() - t0)
-    tm.sort()
-    med_mm = tm[len(tm) // 2]
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": gemv_bytes(M, N, K) / med / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"oracle gemv_fp8_pern (dequant fp8->fp16->fp32 + fp32 matmul + scale) on CPU, "
-                      f"M={M} K={K} N={N}, median of {reps} after 2 warm-ups, {med * 1e3:.1f} ms/call; "
-                      f"os.cpu_count()={os.cpu_count()}; cpu '{model}'",
-            "matmul_only": {"value": gemv_bytes(M, N, K) / med_mm / 1e9, "unit": "GB/s",
-                            "ms_per_call": round(med_mm * 1e3, 2),
-                            "sample": "same shape with W dequantised once before timing (fp32 matmul + scale)"}}
+    med_mm = _time_cpu(lambda: (xf @ Wf.T) * s.float(), reps)
+    model, extra = _cpu_model()
+    out = {"value": gemv_bytes(M, N, K) / med / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+           "kind": "port",
+           "sample": f"oracle gemv_fp8_pern (dequant fp8->fp16->fp32 + fp32 matmul + scale) on CPU, "
+                     f"M={M} K={K} N={N}, median of {reps} after 2 warm-ups, {med * 1e3:.1f} ms/call; "
+                     f"os.cpu_count()={os.cpu_count()}; cpu '{model}' ({extra})",
+           "matmul_only": {"value": gemv_bytes(M, N, K) / med_mm / 1e9, "unit": "GB/s",
+                           "ms_per_call": round(med_mm * 1e3, 2),
+                           "sample": "same shape with W dequantised once before timing (fp32 matmul + scale)"}}
+    # config 2: the batched GEMV at M = 16 on the headline weights
+    x16 = synthetic.activations(16, K, seed=1)
+    t = _time_cpu(lambda: ogemv.gemv_fp8_pern(x16, W8, s), reps)
+    out["gemv_m16"] = {"value": round(gemv_bytes(16, N, K) / t / 1e9, 3), "unit": "GB/s",
+                       "ms_per_call": round(t * 1e3, 2), "gpu_leg": "gemv_shapes M=16 K=4096 N=14336",
+                       "sample": f"oracle gemv_fp8_pern, M=16 K={K} N={N}, median of {reps}"}
+    del Wf
+    # config 3: add+RMSNorm + per-token e4m3 quant, T = 64, H = 4096
+    T, H = 64, 4096
+    h = synthetic.activations(T, H, seed=T)
+    r = synthetic.activations(T, H, seed=T + 1)
+    w = synthetic.norm_weight(H, seed=H)
+    t = _time_cpu(lambda: onorm.fused_add_rms_norm_quant(h, r, w, 1e-6), reps)
+    out["norm_quant_t64"] = {"value": round(t * 1e6, 1), "unit": "us", "gpu_leg": "norm_quant_gemv T=64 H=4096 "
+                             "norm_quant_us", "sample": f"oracle fused_add_rms_norm_quant, T={T} H={H}, median of {reps}"}
+    # config 4: the a8w8 GEMM at the headline M = 2048, K = 4096, N = 6144
+    Mg, Kg, Ng, greps = 2048, 4096, 6144, 3
+    xa = synthetic.activations(Mg, Kg, seed=2).float()
+    sa = torch.clamp(xa.abs().amax(dim=1) / 448.0, min=1.0 / (448.0 * 512.0))
+    qa = (xa / sa[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+    Wg, sg = synthetic.weight_fp8(Ng, Kg, seed=3)
+    Wg = Wg.view(torch.uint8)
+    t = _time_cpu(lambda: ogemm.gemm_a8w8(qa, sa, Wg, sg), greps, warm=1)
+    out["gemm_a8w8_m2048"] = {"value": round(2.0 * Mg * Ng * Kg / t / 1e12, 3), "unit": "TFLOP/s",
+                              "ms_per_call": round(t * 1e3, 1), "gpu_leg": "gemm (a8w8 M=2048 K=4096 N=6144)",
+                              "sample": f"oracle gemm_a8w8 (fp32 dequantise of both code matrices + fp32 matmul "
+                                        f"+ scales), M={Mg} K={Kg} N={Ng}, median of {greps} after 1 warm-up"}
+    del xa, qa, Wg
+    # config 5: one decoder-layer step at M = 4
+    p = synthetic.gemma_layer(seed=10)
+    hl = synthetic.activations(4, p["hidden"], seed=20)
+    rl = synthetic.activations(4, p["hidden"], seed=21)
+    pos = synthetic.positions(4, seed=22)
+    lreps = 3
+    t = _time_cpu(lambda: olayer.decoder_step(p, hl, rl, pos), lreps, warm=1)
+    out["layer_m4"] = {"value": round(t * 1e3, 1), "unit": "ms/step", "gpu_leg": "decoder_layer us_per_step",
+                       "sample": f"oracle decoder_step (every GEMV dequantises its weights per call), M=4, "
+                                 f"median of {lreps} after 1 warm-up"}
+    return out
 
 
 def main():
@@ -483,6 +607,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--no-tables", action="store_true", help="skip the config-2 GEMV table and config-3 legs")
+    ap.add_argument("--small-ops-only", action="store_true",
+                    help="run only the small-kernel leg (norm, quant, gelu_and_mul, QK-norm+RoPE) and print it")
     ap.add_argument("--warm-s", type=float, default=None,
                     help=f"seconds of untimed graph replays before each headline timing (default {WARM_S})")
     ap.add_argument("--copy-ref", action="store_true",
@@ -508,6 +634,9 @@ def main():
         torch.cuda.synchronize()
         log(f"copy reference: 10 x {src.numel()} bytes")
         del src, dst
+    if a.small_ops_only:
+        print(json.dumps({"small_ops": bench_small_ops(ops, torch, reps=max(20, a.steps // 2))}), flush=True)
+        return
 
     g, (x, Wd, s, y) = bench_gemv(ops, torch, a.steps, a.warmup)
     log(f"gemv: read ceiling (one pass over the same weight bytes) {g['read_ceiling_us']:.2f} us")
@@ -559,6 +688,8 @@ def main():
         log("gemv table: " + ", ".join(f"M{r['M']}/{r['K']}x{r['N']}={r['us']}us" for r in out["gemv_shapes"]))
         out["norm_quant_gemv"] = bench_norm_quant_gemv(ops, torch)
         log("norm+quant -> gemv: " + ", ".join(f"T{r['T']}/H{r['H']}={r['pair_us']}us" for r in out["norm_quant_gemv"]))
+        out["small_ops"] = bench_small_ops(ops, torch)
+        log("small ops: " + ", ".join(f"{r['op']}/T{r['T']}={r['us']}us" for r in out["small_ops"]))
     if not a.no_gemm:
         out["gemm"] = bench_gemm_all(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")

@@ -148,27 +148,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
   const int c = lane % L;
   const int hbase = (int)blockIdx.y * heads_per_wg;
   const int h_end = min(nq + nk, hbase + heads_per_wg);
-  auto head = [&](int h) {
-    return h < nq ? q + (size_t)t * qs + (size_t)h * HD : k + (size_t)t * ks + (size_t)(h - nq) * HD;
-  };
-  // the pass's head of this lane, its two chunks and their weights
-  u4 va, vb, wa, wb;
-  auto load_head = [&](int h) {
-    if (h < h_end) {
-      const uint16_t* v = head(h);
-      const uint16_t* w = h < nq ? qw : kw;
-      va = load_u4(v + 8 * c);
-      vb = load_u4(v + HALF + 8 * c);
-      wa = load_u4(w + 8 * c);
-      wb = load_u4(w + HALF + 8 * c);
-    } else {
-      va = vb = wa = wb = u4{0u, 0u, 0u, 0u};
-    }
-  };
+  // the pass's head of this lane: its row pointer, two chunks and their weights
+  u4 va = u4{0u, 0u, 0u, 0u}, vb = va, wa = va, wb = va;
   const int h_first = hbase + wave * HPW + lane / L;
   // the first pass's loads go out before the fp64 cos/sin table, so their
   // latency overlaps its arithmetic (the barrier below waits for both)
-  load_head(h_first);
+  if (h_first < h_end) {
+    const uint16_t* v = h_first < nq ? q + (size_t)t * qs + (size_t)h_first * HD
+                                     : k + (size_t)t * ks + (size_t)(h_first - nq) * HD;
+    const uint16_t* w = h_first < nq ? qw : kw;
+    va = load_u4(v + 8 * c);
+    vb = load_u4(v + HALF + 8 * c);
+    wa = load_u4(w + 8 * c);
+    wb = load_u4(w + HALF + 8 * c);
+  }
   asm volatile("" ::: "memory");
   const double pos = (double)positions[t];
   const double lt = log2((double)theta);
@@ -182,7 +175,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
   __syncthreads();
 
   for (int h = h_first; h - lane / L - wave * HPW < h_end; h += 4 * HPW) {
-    if (h != h_first) load_head(h);
+    uint16_t* v = h < nq ? q + (size_t)t * qs + (size_t)h * HD : k + (size_t)t * ks + (size_t)(h - nq) * HD;
+    if (h != h_first) {
+      if (h < h_end) {
+        const uint16_t* w = h < nq ? qw : kw;
+        va = load_u4(v + 8 * c);
+        vb = load_u4(v + HALF + 8 * c);
+        wa = load_u4(w + 8 * c);
+        wb = load_u4(w + HALF + 8 * c);
+      } else {
+        va = vb = wa = wb = u4{0u, 0u, 0u, 0u};
+      }
+    }
     float a[8], b[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -236,7 +240,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
       }
     }
     if (h < h_end) {
-      uint16_t* v = head(h);
       *reinterpret_cast<u4*>(v + 8 * c) = oa;
       *reinterpret_cast<u4*>(v + HALF + 8 * c) = ob;
     }

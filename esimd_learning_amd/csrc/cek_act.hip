@@ -17,7 +17,7 @@
 //   group's heads; each wave owns whole heads of q and k: RMS over the head
 //   via a wave butterfly, weight multiply, rounding to the activation type,
 //   rotation in fp32, and store in place.
-#include "cek_common.h"
+#include "cek_rowops.h"
 
 namespace cek {
 
@@ -165,13 +165,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
   asm volatile("" ::: "memory");
   const double pos = (double)positions[t];
   const double lt = log2((double)theta);
-  for (int i = threadIdx.x; i < HALF; i += 256) {
-    const double inv_freq = exp2(-(double)(2 * i) / (double)HD * lt);
-    double sd, cd;
-    sincos(pos * inv_freq, &sd, &cd);
-    cs[i] = (float)cd;
-    sn[i] = (float)sd;
-  }
+  for (int i = threadIdx.x; i < HALF; i += 256) rope_angle(pos, i, HD, lt, cs[i], sn[i]);
   __syncthreads();
 
   for (int h = h_first; h - lane / L - wave * HPW < h_end; h += 4 * HPW) {
@@ -187,58 +181,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(
         va = vb = wa = wb = u4{0u, 0u, 0u, 0u};
       }
     }
-    float a[8], b[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      a[2 * e] = T::to_f32(va[e] & 0xFFFF);
-      a[2 * e + 1] = T::to_f32(va[e] >> 16);
-      b[2 * e] = T::to_f32(vb[e] & 0xFFFF);
-      b[2 * e + 1] = T::to_f32(vb[e] >> 16);
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ss = fmaf(a[e], a[e], ss);
-      ss = fmaf(b[e], b[e], ss);
-    }
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    const float inv = rsqrtf(ss / (float)HD + eps);
-    // norm, then round to the activation type before the rotation
-    float na[8], nb[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      na[2 * e] = T::to_f32(T::from_f32(f32_round(a[2 * e] * inv * T::to_f32(wa[e] & 0xFFFF))));
-      na[2 * e + 1] = T::to_f32(T::from_f32(f32_round(a[2 * e + 1] * inv * T::to_f32(wa[e] >> 16))));
-      nb[2 * e] = T::to_f32(T::from_f32(f32_round(b[2 * e] * inv * T::to_f32(wb[e] & 0xFFFF))));
-      nb[2 * e + 1] = T::to_f32(T::from_f32(f32_round(b[2 * e + 1] * inv * T::to_f32(wb[e] >> 16))));
-    }
     u4 oa, ob;
-    if (neox) {
-      // pair p = 8 c + e: (na[e], nb[e])
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int p0 = 8 * c + 2 * e, p1 = p0 + 1;
-        const float x0 = na[2 * e] * cs[p0] - nb[2 * e] * sn[p0];
-        const float x1 = na[2 * e + 1] * cs[p1] - nb[2 * e + 1] * sn[p1];
-        const float y0 = nb[2 * e] * cs[p0] + na[2 * e] * sn[p0];
-        const float y1 = nb[2 * e + 1] * cs[p1] + na[2 * e + 1] * sn[p1];
-        oa[e] = (uint32_t)T::from_f32(x0) | ((uint32_t)T::from_f32(x1) << 16);
-        ob[e] = (uint32_t)T::from_f32(y0) | ((uint32_t)T::from_f32(y1) << 16);
-      }
-    } else {
-      // pairs inside each chunk: chunk c holds pairs 4 c + e, chunk c + L pairs 4 (c + L) + e
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int pa = 4 * c + e, pb = 4 * (c + L) + e;
-        const float xa = na[2 * e] * cs[pa] - na[2 * e + 1] * sn[pa];
-        const float ya = na[2 * e + 1] * cs[pa] + na[2 * e] * sn[pa];
-        const float xb = nb[2 * e] * cs[pb] - nb[2 * e + 1] * sn[pb];
-        const float yb = nb[2 * e + 1] * cs[pb] + nb[2 * e] * sn[pb];
-        oa[e] = (uint32_t)T::from_f32(xa) | ((uint32_t)T::from_f32(ya) << 16);
-        ob[e] = (uint32_t)T::from_f32(xb) | ((uint32_t)T::from_f32(yb) << 16);
-      }
-    }
+    norm_rope_chunks<T, L>(va, vb, wa, wb, cs, sn, eps, neox != 0, c, oa, ob);
     if (h < h_end) {
       *reinterpret_cast<u4*>(v + 8 * c) = oa;
       *reinterpret_cast<u4*>(v + HALF + 8 * c) = ob;

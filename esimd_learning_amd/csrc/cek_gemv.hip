@@ -36,7 +36,7 @@
 //    for shapes the vector kernels do not take.
 #include <type_traits>
 
-#include "cek_common.h"
+#include "cek_rowops.h"
 
 namespace cek {
 
@@ -82,6 +82,20 @@ struct GemvSegs {
 
 // Inputs and side outputs of the add+RMSNorm (+ e4m3 quant) that
 // gemv_lds_kernel's NORM form computes in its prologue (unused otherwise).
+// Epilogue work on the GEMV's output done by the workgroup that finishes
+// last (TAIL != TAIL_NONE in gemv_lds_kernel); arrival counters zero before
+// the launch, and left zero by it.
+enum TailKind { TAIL_NONE = 0, TAIL_ROPE = 2 };
+struct TailArgs {
+  int* counters;          // ROPE: one per q / k head, TAIL_SLOT ints apart
+  const uint16_t* qw;     // ROPE: q head RMSNorm weight [hd]
+  const uint16_t* kw;     // ROPE: k head RMSNorm weight [hd]
+  const int64_t* pos;     // ROPE: positions [M]
+  int nq, nk;             // ROPE: heads q then k at output columns [0, (nq + nk) hd)
+  float eps, theta;
+  int neox;
+};
+
 struct NormArgs {
   const uint16_t* h;  // hidden [M, K]
   const uint16_t* r;  // residual [M, K] (read)
@@ -91,6 +105,7 @@ struct NormArgs {
   uint8_t* q_out;     // e4m3 codes [M, K] (quant form), workgroup 0
   float* s_out;       // per-row scales [M] (quant form), workgroup 0
   float eps;
+  TailArgs tail;      // epilogue arguments (TAIL forms only)
 };
 
 struct SegRef {
@@ -368,7 +383,10 @@ __device__ inline void lds_load_scales(uint32_t (&sc_n)[NT], float (&sc_m)[MB][4
     for (int v = 0; v < 4; ++v) sc_m[b][v] = (xs && wave == 0) ? xs[min(b * 16 + g * 4 + v, M - 1)] : 1.f;
 }
 
-template <int NT, int MB>
+// COH: the outputs are stored at device scope (global_store ... sc1: written
+// through to the level every XCD sees), for a tail epilogue that another
+// workgroup runs on them.
+template <int NT, int MB, bool COH = false>
 __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wave, int lane, int n0, int N,
                                         int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
                                         const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
@@ -398,7 +416,9 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
         const int m = b * 16 + g * 4 + v;  // D row = 4 * (lane >> 4) + v
         if (m >= M) continue;
         const float o = f32_round(c[v] * (xscaled ? sc * sc_m[b][v] : sc));
-        sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+        const uint16_t ob = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+        if constexpr (COH) __hip_atomic_store(sr.y + (size_t)m * N + n, ob, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else sr.y[(size_t)m * N + n] = ob;
       }
     }
   }
@@ -459,6 +479,89 @@ __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* r
   });
 }
 
+// Tail epilogue of gemv_lds_kernel (one 16-row tile per workgroup, one
+// segment, y [M, N] with row stride N).  Every thread of the workgroup calls
+// it after the tile's store, which wave 0 made at device scope (sc1 stores,
+// lds_reduce_store's COH form): once wave 0 has seen them complete, the
+// workgroup counts itself in on its head's counter.  The workgroup that
+// completes the count does the work over all of the head's tiles, reading
+// the other tiles' outputs with device-scope (sc1) loads, and puts the
+// counter back to zero.  Nobody waits, so no workgroup depends on another
+// being resident.
+//  * TAIL_ROPE (TP = L, head dim 16 L): the hd / 16 tiles of one q or k head
+//    h (columns [h hd, (h + 1) hd), h < nq + nk) count on slot h; then
+//    qk_norm_rope_vec_kernel's computation on that head for every row m < M,
+//    in place.
+// Measured on MI355X at the config-5 QKV shape (M = 4, K = 3072, N = 12288,
+// 32 q / k heads of 256): 10.9 us per launch against 8.6 us for the GEMV
+// alone and 2.7 us for the separate QK-norm+RoPE launch.  What did not pay:
+// a plain __threadfence (an L2 write-back) in every workgroup (15.6 us),
+// the 32 counters in one 128-byte line (13.8 us), an L2 invalidate and plain
+// loads in each head's last workgroup instead of sc1 loads (12.5 us); and
+// the same scheme for the add+RMSNorm after the o_proj GEMV (192 workgroups
+// into one norm over all outputs): 13.1 us against 5.2 + 2.5 us, since its
+// chain of device-scope round trips (stores, the count, the loads) sits on
+// the critical path of the launch's last workgroup.
+constexpr int TAIL_SLOT = 64;  // ints between counters (256 bytes)
+
+// 16 bytes read at device scope (two 8-byte sc1 loads): another XCD's
+// device-scope stores, not a stale line of this XCD's L2.
+__device__ inline u4 load_u4_dev(const uint16_t* p) {
+  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return u4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+
+// Counts the workgroup in on counters[slot]; true for the arrival that
+// completes `expect` (which then resets the counter).  Uniform per workgroup.
+__device__ inline bool tail_arrive(int* counters, int slot, int expect, int* flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool done = atomicAdd(counters + slot * TAIL_SLOT, 1) == expect - 1;
+    if (done) atomicExch(counters + slot * TAIL_SLOT, 0);  // all arrivals are in: ready for the next launch
+    *flag = done;
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
+template <typename T, int TAIL, int TP>
+__device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M, uint8_t* smem) {
+  static_assert(TAIL == TAIL_ROPE, "tail kinds");
+  __shared__ int flag;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (n0 / (16 * TP) >= ta.nq + ta.nk) return;  // v rows: no tail (uniform per workgroup)
+  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's device-scope stores are done
+
+  {
+    constexpr int L = TP, HD = 16 * L, HALF = 8 * L, HPW = 64 / L;  // rows per wave and pass
+    const int head = n0 / HD;
+    if (!tail_arrive(ta.counters, head, HD / 16, &flag)) return;
+    float* cs = reinterpret_cast<float*>(smem);  // [M][HALF]
+    float* sn = cs + M * HALF;
+    const uint16_t* w = head < ta.nq ? ta.qw : ta.kw;
+    const int c = lane % L;
+    const u4 wa = load_u4(w + 8 * c), wb = load_u4(w + HALF + 8 * c);
+    const double lt = log2((double)ta.theta);
+    for (int m0 = 0; m0 < M; m0 += 4 * HPW) {
+      const int m = m0 + wave * HPW + lane / L, mc = min(m, M - 1);
+      uint16_t* v = y + (size_t)mc * N + (size_t)head * HD;
+      // the row's loads first, the fp64 angles behind them
+      const u4 va = load_u4_dev(v + 8 * c), vb = load_u4_dev(v + HALF + 8 * c);
+      if (m0 == 0)
+        for (int i = tid; i < M * HALF; i += 256) rope_angle((double)ta.pos[i / HALF], i % HALF, HD, lt, cs[i], sn[i]);
+      __syncthreads();
+      u4 oa, ob;
+      norm_rope_chunks<T, L>(va, vb, wa, wb, cs + mc * HALF, sn + mc * HALF, ta.eps, ta.neox != 0, c, oa, ob);
+      if (m < M) {
+        *reinterpret_cast<u4*>(v + 8 * c) = oa;
+        *reinterpret_cast<u4*>(v + HALF + 8 * c) = ob;
+      }
+    }
+  }
+}
+
 // One kernel for both activation kinds.  XF8 = false: x is T (fp16/bf16), a
 // lane's 16-byte weight unit (16 K values) is decoded to two 8-value operands
 // of v_mfma_f32_16x16x32_{f16,bf16}.  XF8 = true: x holds e4m3 codes with
@@ -493,14 +596,21 @@ __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* r
 // while the first weight stages are in flight.  Workgroup 0 also writes the
 // side outputs (na.r_out, na.h_out or na.q_out / na.s_out); the other
 // workgroups read na.r meanwhile, so na.r_out must not alias it.
+//
+// TAIL (with TP, see gemv_tail): after the tile's store, the last workgroup
+// to finish (of all, or of one head's tiles) runs a fused epilogue on the
+// output: add+RMSNorm with a residual, or QK RMSNorm + RoPE per head.
 template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
-          bool GLU = false, bool NORM = false>
+          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M, NormArgs na) {
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 16), "activations go through LDS only for M <= 16");
   static_assert(!GLU || (TPW == 2 && NT == 1), "gate/up pairs are two 16-row tiles");
   static_assert(!NORM || (MX >= 1 && MX <= 4 && NT == 1), "fused norm: up to four rows");
+  static_assert(TAIL == TAIL_NONE || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && !XF8 &&
+                                      std::is_same<T, TO>::value),
+                "tails: one 16-row tile per workgroup, fp16 / bf16 activations");
   constexpr int K = STEPS * 1024;
   constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
@@ -816,8 +926,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     }
   }
   if constexpr (TPW == 1)
-    lds_reduce_store<NT, MB>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m, XF8,
-                             std::is_same<TO, BF16>::value);
+    lds_reduce_store<NT, MB, TAIL != TAIL_NONE>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m, XF8,
+                                                std::is_same<TO, BF16>::value);
+  if constexpr (TAIL != TAIL_NONE) gemv_tail<T, TAIL, TP>(na.tail, sr.y, nw, N, M, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1255,7 +1366,76 @@ int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* s
   return launch_glu<BF16, BF16, CEK_E5M2, false>(x, sg, skind, m, dd, k, st);
 }
 
+// GEMV with a fused epilogue (gemv_lds_kernel's TAIL forms): one 16-row
+// tile per workgroup, activations staged through LDS (M <= 4), prefetch
+// depth 3, e4m3 weights, K in {3, 4, 5} KiB values; tp = L (ROPE, head dim
+// 128 or 256).  CEK_ERR_UNSUPPORTED for
+// other shapes (the caller runs the GEMV, then the op).
+template <typename T, int TAIL, int TP>
+static void launch_tail_t(const void* x, GemvSegs& sg, int skind, int M, int K, const NormArgs& na, hipStream_t st) {
+  const dim3 grid((unsigned)seg_grid(sg, 16));
+#define CEK_TAIL(S)                                                                                                 \
+  gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, 3, S, 4, 1, false, false, TAIL, TP><<<grid, 256, 0, st>>>(x, sg, skind, \
+                                                                                                         M, na)
+  if (K == 3072) CEK_TAIL(3);
+  else if (K == 4096) CEK_TAIL(4);
+  else CEK_TAIL(5);
+#undef CEK_TAIL
+}
+
+int launch_gemv_tail(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N,
+                     int64_t K, int io_dtype, int fp8_fmt, int tail, int tp, const NormArgs& na, hipStream_t st) {
+  if (M < 0 || N < 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
+  if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
+  if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
+  if (skind < 0 || skind == SK_F32_SCALAR) return CEK_ERR_INVALID;
+  if (M == 0 || N == 0) return CEK_OK;
+  if (!x || !w || !scale || !y || !na.tail.counters) return CEK_ERR_INVALID;
+  if (N * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
+  if (M > 4 || (K != 3072 && K != 4096 && K != 5120) || fp8_fmt != CEK_E4M3 || N % 16 != 0) return CEK_ERR_UNSUPPORTED;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16)) return CEK_ERR_UNSUPPORTED;
+  // the output is re-read by the tail: it must not share memory with the inputs
+  if (overlaps(y, M * N * 2, x, M * K * 2) || overlaps(y, M * N * 2, w, N * K)) return CEK_ERR_UNSUPPORTED;
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = static_cast<const uint8_t*>(w);
+  sg.s[0] = scale;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)N;
+  const int m = (int)M, k = (int)K;
+  const bool f16 = io_dtype == CEK_F16;
+  (void)tail;
+  if (tp == 8) { if (f16) launch_tail_t<F16, TAIL_ROPE, 8>(x, sg, skind, m, k, na, st); else launch_tail_t<BF16, TAIL_ROPE, 8>(x, sg, skind, m, k, na, st); }
+  else { if (f16) launch_tail_t<F16, TAIL_ROPE, 16>(x, sg, skind, m, k, na, st); else launch_tail_t<BF16, TAIL_ROPE, 16>(x, sg, skind, m, k, na, st); }
+  return check_launch();
+}
+
 }  // namespace cek
+
+extern "C" int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, void* y,
+                                         const void* q_weight, const void* k_weight, const int64_t* positions,
+                                         int64_t n_q, int64_t n_k, int64_t head_dim, float eps, float theta,
+                                         int is_neox, int* counters, int64_t M, int64_t N, int64_t K, int io_dtype,
+                                         int fp8_fmt, int scale_dtype, void* stream) {
+  if (M < 0 || N < 0 || n_q < 0 || n_k < 0 || head_dim <= 0 || !(theta > 0.f)) return CEK_ERR_INVALID;
+  if ((n_q + n_k) * head_dim > N) return CEK_ERR_INVALID;
+  if (M > 0 && N > 0 && (!positions || (n_q > 0 && !q_weight) || (n_k > 0 && !k_weight))) return CEK_ERR_INVALID;
+  if (head_dim != 128 && head_dim != 256) return M == 0 || N == 0 ? CEK_OK : CEK_ERR_UNSUPPORTED;
+  if (N % 8 != 0 || (n_q > 0 && !cek::aligned(q_weight, 16)) || (n_k > 0 && !cek::aligned(k_weight, 16)))
+    return M == 0 || N == 0 ? CEK_OK : CEK_ERR_UNSUPPORTED;
+  cek::NormArgs na{};
+  na.tail.counters = counters;
+  na.tail.qw = static_cast<const uint16_t*>(q_weight);
+  na.tail.kw = static_cast<const uint16_t*>(k_weight);
+  na.tail.pos = positions;
+  na.tail.nq = (int)n_q;
+  na.tail.nk = (int)n_k;
+  na.tail.eps = eps;
+  na.tail.theta = theta;
+  na.tail.neox = is_neox != 0;
+  return cek::launch_gemv_tail(x, w, scale, cek::scale_kind(scale_dtype), y, M, N, K, io_dtype, fp8_fmt,
+                               cek::TAIL_ROPE, (int)(head_dim / 16), na, (hipStream_t)stream);
+}
 
 extern "C" int cek_add_rms_norm_gemv_fp8(const void* hidden, const void* residual, const void* norm_weight, float eps,
                                          void* residual_out, void* hidden_out, uint8_t* q_out, float* q_scale,

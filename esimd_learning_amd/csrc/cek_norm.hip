@@ -14,22 +14,14 @@
 // per_token_quant_kernel does, with the same launch shape and reduction
 // order as the plain norm kernel.  The fused result is therefore bit-identical
 // to the unfused pair (norm kernel, then quant kernel).
-#include "cek_common.h"
+#include "cek_rowops.h"
 
 namespace cek {
 
 constexpr int NORM_THREADS = 256;
 
 // Workgroup-wide sum / max for NORM_THREADS threads (4 waves).
-__device__ inline float block_sum(float v, float* sh) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) sh[wave] = v;
-  __syncthreads();
-  float t = sh[0] + sh[1] + sh[2] + sh[3];
-  __syncthreads();
-  return t;
-}
+__device__ inline float block_sum(float v, float* sh) { return wg4_sum(v, sh); }
 __device__ inline float block_max(float v, float* sh) {
   v = wave_max(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -59,17 +51,7 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(
   for (int j = 0; j < UPT; ++j) {
     const int u = threadIdx.x + j * NORM_THREADS;
     if (u < units) {
-      u4 hv = load_u4(hr + u * 8);
-      u4 xv = load_u4(rr + u * 8);
-      u4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a0 = T::to_f32(hv[e] & 0xFFFF) + T::to_f32(xv[e] & 0xFFFF);
-        float a1 = T::to_f32(hv[e] >> 16) + T::to_f32(xv[e] >> 16);
-        ss = fmaf(a0, a0, ss);
-        ss = fmaf(a1, a1, ss);
-        o[e] = (uint32_t)T::from_f32(a0) | ((uint32_t)T::from_f32(a1) << 16);
-      }
+      const u4 o = addnorm_pass1<T>(load_u4(hr + u * 8), load_u4(rr + u * 8), ss);
       rv[j] = o;
       *reinterpret_cast<u4*>(rr + u * 8) = o;
     }
@@ -83,18 +65,15 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(
   for (int j = 0; j < UPT; ++j) {
     const int u = threadIdx.x + j * NORM_THREADS;
     if (u < units) {
-      u4 wv = load_u4(weight + u * 8);
-      u4 o;
+      const u4 o = addnorm_pass2<T>(rv[j], load_u4(weight + u * 8), inv);
+      if (QUANT) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float n0 = f32_round(T::to_f32(rv[j][e] & 0xFFFF) * inv * T::to_f32(wv[e] & 0xFFFF));
-        float n1 = f32_round(T::to_f32(rv[j][e] >> 16) * inv * T::to_f32(wv[e] >> 16));
-        uint16_t b0 = T::from_f32(n0), b1 = T::from_f32(n1);
-        if (QUANT) amax = fmaxf(amax, fmaxf(fabsf(T::to_f32(b0)), fabsf(T::to_f32(b1))));
-        o[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+        for (int e = 0; e < 4; ++e)
+          amax = fmaxf(amax, fmaxf(fabsf(T::to_f32(o[e] & 0xFFFF)), fabsf(T::to_f32(o[e] >> 16))));
+        nv[j] = o;
+      } else {
+        *reinterpret_cast<u4*>(hr + u * 8) = o;
       }
-      if (QUANT) nv[j] = o;
-      else *reinterpret_cast<u4*>(hr + u * 8) = o;
     }
   }
   if (!QUANT) return;

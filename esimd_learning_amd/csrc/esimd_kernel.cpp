@@ -468,3 +468,74 @@ void esimd_fused_add_rms_norm_quant_gemv_fp8(at::Tensor hidden_states, at::Tenso
   }
   check_rc(rc, op);
 }
+
+// ---- GEMV with the consuming op fused into its last workgroup ----
+// counters: int32 on the device, zero before the first call, left zero by
+// every call (64 * (1 + ceil(N / 256)) for add+RMSNorm, 64 * (n_q + n_k)
+// for QK-norm+RoPE: counters 256 bytes apart); calls that may overlap in
+// time need their own.  Shapes the fused launch does not take
+// run the GEMV op, then the norm / RoPE op (the same values).
+static void check_counters(const at::Tensor& c, const at::Tensor& ref, int64_t need, const char* op) {
+  TORCH_CHECK(c.scalar_type() == at::ScalarType::Int, op, ": counters must be int32");
+  check_device(c, ref, op, "counters");
+  check_contig(c, op, "counters");
+  TORCH_CHECK(c.numel() >= need, op, ": counters must hold ", need, " elements");
+}
+
+static int scale_code_of(const at::Tensor& scale, int64_t N, const char* op) {
+  const auto st = scale.scalar_type();
+  TORCH_CHECK(st == at::ScalarType::Half || st == at::ScalarType::BFloat16 || st == at::ScalarType::Float, op,
+              ": weight_scale must be fp16, bf16 or fp32");
+  TORCH_CHECK(scale.numel() >= N, op, ": weight_scale must hold N elements");
+  return st == at::ScalarType::Float ? CEK_F32 : (st == at::ScalarType::Half ? CEK_F16 : CEK_BF16);
+}
+
+void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                                 at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
+                                 int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters) {
+  const char* op = "esimd_gemv_fp8_qk_norm_rope";
+  check_gemv_io(input, output, op);
+  check_fp8_weight(weight, op);
+  for (const auto* t : {&weight_scale, &output, &q_weight, &k_weight, &positions})
+    check_device(*t, input, op, "operand");
+  check_contig(input, op, "input");
+  check_contig(weight, op, "weight");
+  check_contig(weight_scale, op, "weight_scale");
+  check_contig(output, op, "output");
+  check_contig(q_weight, op, "q_weight");
+  check_contig(k_weight, op, "k_weight");
+  check_contig(positions, op, "positions");
+  TORCH_CHECK(weight.dim() == 2 && weight.size(0) > 0 && weight.size(1) > 0, op, ": weight must be [N, K]");
+  const int64_t N = weight.size(0), K = weight.size(1);
+  TORCH_CHECK(input.size(-1) == K, op, ": input must be [M, K]");
+  const int64_t M = input.numel() / K;
+  TORCH_CHECK(output.numel() == M * N, op, ": output must be [M, N]");
+  TORCH_CHECK(q_weight.scalar_type() == input.scalar_type() && k_weight.scalar_type() == input.scalar_type(), op,
+              ": q_weight and k_weight must have the input's dtype");
+  TORCH_CHECK(positions.scalar_type() == at::ScalarType::Long && positions.numel() == M, op,
+              ": positions must be int64 [M]");
+  const int64_t hd = q_weight.numel();
+  TORCH_CHECK(k_weight.numel() == hd && hd > 0 && hd % 2 == 0 && hd <= 512, op,
+              ": q_weight and k_weight must both have head_dim (even, <= 512) elements");
+  TORCH_CHECK(n_q >= 0 && n_k >= 0 && (n_q + n_k) * hd <= N, op, ": the q and k heads must fit in the output row");
+  check_counters(counters, input, 64 * (n_q + n_k), op);
+  const int scale_code = scale_code_of(weight_scale, N, op);
+  c10::OptionalDeviceGuard guard(input.device());
+  void* st = current_stream(input);
+  const int io = io_code(input.scalar_type());
+  const int rc = cek_gemv_fp8_qk_norm_rope(
+      input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(), output.data_ptr(), q_weight.data_ptr(),
+      k_weight.data_ptr(), static_cast<const int64_t*>(positions.data_ptr()), n_q, n_k, hd, (float)eps, (float)theta,
+      is_neox ? 1 : 0, static_cast<int*>(counters.data_ptr()), M, N, K, io, fp8_code(weight), scale_code, st);
+  if (rc != CEK_ERR_UNSUPPORTED) {
+    check_rc(rc, op);
+    return;
+  }
+  run_gemv(input, weight, weight_scale, output, N, K, false, op);
+  if (n_q + n_k == 0) return;
+  auto* y = static_cast<char*>(output.data_ptr());
+  check_rc(cek_qk_norm_rope(y, y + n_q * hd * output.element_size(), q_weight.data_ptr(), k_weight.data_ptr(),
+                            static_cast<const int64_t*>(positions.data_ptr()), M, n_q, n_k, hd, N, N, (float)eps,
+                            (float)theta, is_neox ? 1 : 0, io, st),
+           op);
+}

@@ -57,6 +57,11 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
   m.def("esimd_qk_norm_rope(Tensor(a!) q, Tensor(b!) k, Tensor q_weight, Tensor k_weight, "
         "Tensor positions, float eps, float theta, bool is_neox) -> ()");
   m.impl("esimd_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_qk_norm_rope);
+
+  m.def("esimd_gemv_fp8_qk_norm_rope(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "
+        "Tensor q_weight, Tensor k_weight, Tensor positions, int n_q, int n_k, float eps, float theta, "
+        "bool is_neox, Tensor(b!) counters) -> ()");
+  m.impl("esimd_gemv_fp8_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope);
 }
 
 PyMODINIT_FUNC PyInit_custom_esimd_kernels() {

@@ -53,6 +53,12 @@ void esimd_gemv_fp8_gelu_and_mul(at::Tensor input, at::Tensor weight, at::Tensor
 void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Tensor k_weight,
                         at::Tensor positions, double eps, double theta, bool is_neox);
 
+// The QKV GEMV with QK RMSNorm + RoPE on its q and k columns fused into
+// the last workgroup of each head.
+void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                                 at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
+                                 int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters);
+
 at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
                                at::Tensor output);
 

@@ -21,16 +21,25 @@ receives r2 as before.  It is off by default: every workgroup of the GEMV
 then normalises the rows itself, which at M = 4 over the 768 and 1536
 workgroups of QKV and gate/up costs more than the norm launch it saves.
 
+With ``fuse_tails`` (the default; fp16/bf16 hand-offs, no ``fuse_norm``)
+QK-norm+RoPE runs in the QKV GEMV (esimd_gemv_fp8_qk_norm_rope: per head,
+the workgroup that finishes the head's rows last) -- one launch fewer per
+step, the same values bit for bit.  Its arrival counters are allocated
+(zeroed) once here and left zero by every call.
+
 With ``act_fp8=True`` the two norm -> GEMV hand-offs carry e4m3 activations
 instead of fp16: esimd_fused_add_rms_norm_quant_fp8 writes per-token codes
 and scales, and esimd_gemm_fp8_a8w8 (esimd_gemm_fp8_a8w8_gelu_and_mul for
 gate/up) consumes them (the hidden input is then
 only read, not overwritten with the normed value).  Needs e4m3 weights.
 
-All intermediate buffers are allocated once in the constructor, so a step
-enqueues only kernels: it can be captured in a HIP graph (``capture``) and
-replayed, which removes host launch overhead from the latency-bound small
-kernels between the GEMVs.
+The intermediate buffers and counters are allocated once in the
+constructor, so at decode sizes a step enqueues only kernels: it can be
+captured in a HIP graph (``capture``) and replayed, which removes host launch
+overhead from the latency-bound small kernels between the GEMVs.  (One
+exception: with ``act_fp8`` at M = 64 the a8w8 op splits K and takes its
+fp32 workspace from PyTorch's caching allocator on every call -- inside a
+captured graph, from the graph's memory pool.)
 """
 
 import torch
@@ -38,7 +47,7 @@ import torch
 
 class GemmaDecodeLayer:
     def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False, fuse_glu=True,
-                 fuse_norm=False):
+                 fuse_norm=False, fuse_tails=True):
         from . import ops as _load_ops
         self.ops = _load_ops()
         p = params
@@ -64,6 +73,8 @@ class GemmaDecodeLayer:
         self.fuse_glu = fuse_glu
         self.fuse_norm = fuse_norm and M <= 4   # the fused launch covers up to four rows
         self.r_mid = mk(self.hidden)            # r1 between the two fused norms
+        self.fuse_tails = fuse_tails and not act_fp8 and not self.fuse_norm
+        self.cnt_rope = self.ops.gemv_tail_counters(self.nq, self.nk, device)
         if act_fp8:
             if self.Wqkv.dtype != torch.float8_e4m3fn or self.Wgu.dtype != torch.float8_e4m3fn:
                 raise ValueError("act_fp8 needs e4m3 weights")
@@ -86,9 +97,14 @@ class GemmaDecodeLayer:
             o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wqkv8, self.sqkv32, self.qkv)
         else:
             o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, self.eps)
-            o.esimd_gemv_fp8_pern(hidden, self.Wqkv, self.sqkv, self.qkv, self.Wqkv.shape[0], self.hidden)
-        o.esimd_qk_norm_rope(self.qkv[:, : nq * hd], self.qkv[:, nq * hd:(nq + nk) * hd], self.qw, self.kw,
-                             positions, self.eps, self.theta, True)
+            if self.fuse_tails:
+                o.esimd_gemv_fp8_qk_norm_rope(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
+                                              nq, nk, self.eps, self.theta, True, self.cnt_rope)
+            else:
+                o.esimd_gemv_fp8_pern(hidden, self.Wqkv, self.sqkv, self.qkv, self.Wqkv.shape[0], self.hidden)
+        if not self.fuse_tails:
+            o.esimd_qk_norm_rope(self.qkv[:, : nq * hd], self.qkv[:, nq * hd:(nq + nk) * hd], self.qw, self.kw,
+                                 positions, self.eps, self.theta, True)
         self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
         o.esimd_gemv_fp8_pern(self.attn, self.Wo, self.so, self.o, self.hidden, nq * hd)
         if self.act_fp8:

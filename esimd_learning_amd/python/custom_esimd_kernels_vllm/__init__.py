@@ -26,6 +26,8 @@ from custom_esimd_kernels_vllm.ops import (  # noqa: F401
     esimd_fused_add_rms_norm_gemv_fp8,
     esimd_fused_add_rms_norm_quant_gemv_fp8,
     esimd_qk_norm_rope,
+    esimd_gemv_fp8_qk_norm_rope,
+    gemv_tail_counters,
     esimd_gemm_fp8_a8w8,
     esimd_gemm_fp8_a8w8_gelu_and_mul,
 )

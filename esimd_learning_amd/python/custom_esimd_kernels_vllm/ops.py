@@ -146,6 +146,26 @@ def esimd_qk_norm_rope(
     _ops.esimd_qk_norm_rope(q, k, q_weight, k_weight, positions, eps, theta, is_neox)
 
 
+def gemv_tail_counters(n_q, n_k, device) -> torch.Tensor:
+    """Zeroed arrival counters for esimd_gemv_fp8_qk_norm_rope (64 per head)."""
+    return torch.zeros(64 * (n_q + n_k), dtype=torch.int32, device=device)
+
+
+def esimd_gemv_fp8_qk_norm_rope(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
+    q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor, n_q: int, n_k: int,
+    eps: float, theta: float = 10000.0, is_neox: bool = True, counters: torch.Tensor = None,
+) -> None:
+    """The QKV GEMV (esimd_gemv_fp8_pern into output [M, N]) followed by
+    esimd_qk_norm_rope on its q columns [0, n_q hd) and k columns
+    [n_q hd, (n_q + n_k) hd), in one launch for decode batches.  counters:
+    int32 device tensor of >= 64 * (n_q + n_k) elements
+    (``gemv_tail_counters``), zero before the first call and left zero by
+    each."""
+    _ops.esimd_gemv_fp8_qk_norm_rope(input, weight, weight_scale, output, q_weight, k_weight, positions, n_q, n_k,
+                                     eps, theta, is_neox, counters)
+
+
 def esimd_gemm_fp8_a8w8(
     a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
     output: torch.Tensor,

@@ -218,6 +218,27 @@ int cek_gemv_fp8_gelu_and_mul(const void* x, const float* x_scale, const void* w
                               int scale_dtype, void* stream);
 
 /*
+ * NEW: the fused QKV GEMV with the per-head QK RMSNorm + RoPE fused in (no
+ * counterpart in the reference: it is esimd_gemv_fp8_pern over the QKV
+ * weight, csrc/xpu/esimd_kernel.sycl:22-53, followed by cek_qk_norm_rope on
+ * the q and k columns of its output):
+ *   y = GEMV(x, w, scale) [M, N]; then, in place, cek_qk_norm_rope on
+ *   q = y[:, 0 : n_q hd] and k = y[:, n_q hd : (n_q + n_k) hd] (row stride N)
+ * with the same values bit for bit.  For each q / k head the workgroup that
+ * finishes the head's rows last does its norm and rotation; `counters`
+ * (64 * (n_q + n_k) ints: one counter per head, 256 bytes apart) must be
+ * zero before the first call and are left zero -- calls that may overlap in
+ * time need their own.  Covers M <= 4,
+ * K in {3072, 4096, 5120}, N % 16 == 0, head_dim 128 or 256, e4m3 weights,
+ * 16-byte aligned operands; CEK_ERR_UNSUPPORTED otherwise (run the GEMV,
+ * then cek_qk_norm_rope).
+ */
+int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, void* y, const void* q_weight,
+                              const void* k_weight, const int64_t* positions, int64_t n_q, int64_t n_k,
+                              int64_t head_dim, float eps, float theta, int is_neox, int* counters, int64_t M,
+                              int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+
+/*
  * NEW: per-head RMSNorm (weight qw / kw of length head_dim, Gemma w+1) then
  * rotary embedding, in place on q [T, n_q * head_dim] and
  * k [T, n_k * head_dim] (row strides q_stride / k_stride elements, so both

@@ -72,6 +72,31 @@ def test_decoder_step_graph_replays(ops, dev, act_fp8, fuse_norm, dims):
         torch.randn(1000, device=dev).sum().item()   # unrelated eager work between replays
 
 
+def test_decoder_step_tails_equal_separate_ops(ops, dev):
+    """QK-norm+RoPE in the QKV GEMV's last workgroup of each head (the default
+    step) gives the step the separate launch gives, bit for bit; and the step
+    matches the oracle."""
+    M, dims = 4, CONFIG5
+    p = synthetic.gemma_layer(seed=13, **dims)
+    res = []
+    for tails in (True, False):
+        layer = GemmaDecodeLayer(p, M, dev, fuse_tails=tails)
+        assert layer.fuse_tails == tails
+        h = synthetic.activations(M, dims["hidden"], seed=50)
+        r = synthetic.activations(M, dims["hidden"], seed=51)
+        pos = synthetic.positions(M, seed=52)
+        hd, rd = h.to(dev), r.to(dev)
+        out = layer.step(hd, rd, pos.to(dev)).clone()
+        res.append((out, rd.clone(), layer.qkv.clone(), layer.o.clone()))
+        del layer
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    ref_out, ref_r, _ = olayer.decoder_step(p, h, r, pos)
+    assert_close_fp(res[0][1].cpu(), ref_r.float(), "residual after the layer")
+    assert_close_fp(res[0][0].cpu(), ref_out, "layer output")
+
+
 @pytest.mark.parametrize("act_fp8", [False, True])
 def test_decoder_step_fused_equals_unfused(ops, dev, act_fp8):
     """The fused launches (norm into the GEMV prologue, gelu into the gate/up

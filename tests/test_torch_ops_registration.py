@@ -43,7 +43,7 @@ def test_new_ops_registered(pkg):
                  "esimd_qk_norm_rope", "esimd_gemm_fp8_a8w8", "esimd_gemv_fp8_pern_fused",
                  "esimd_gemv_fp8_pert_fused", "esimd_gemv_fp8_gelu_and_mul",
                  "esimd_gemm_fp8_a8w8_gelu_and_mul", "esimd_fused_add_rms_norm_gemv_fp8",
-                 "esimd_fused_add_rms_norm_quant_gemv_fp8"):
+                 "esimd_fused_add_rms_norm_quant_gemv_fp8", "esimd_gemv_fp8_qk_norm_rope"):
         op = getattr(torch.ops.custom_esimd_kernels_vllm, name).default
         assert "!" in str(op._schema)     # written tensors carry alias annotations
 

@@ -193,6 +193,35 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
+// Weight scale kinds of the GEMV / GEMM kernels: per output channel (fp16,
+// bf16 or fp32 [N]) or one fp32 value for the whole tensor.
+enum ScaleKind { SK_F16 = 0, SK_BF16 = 1, SK_F32 = 2, SK_F32_SCALAR = 3 };
+
+__device__ inline float load_scale(const void* s, int kind, int n) {
+  switch (kind) {
+    case SK_F16: return F16::to_f32(reinterpret_cast<const uint16_t*>(s)[n]);
+    case SK_BF16: return BF16::to_f32(reinterpret_cast<const uint16_t*>(s)[n]);
+    case SK_F32: return reinterpret_cast<const float*>(s)[n];
+    default: return *reinterpret_cast<const float*>(s);
+  }
+}
+
+// The same in two halves, for kernels that load the scale long before they
+// use it: the load alone (raw bits, no conversion, so nothing waits for it
+// until scale_value) and the conversion.
+__device__ inline uint32_t load_scale_bits(const void* s, int kind, int n) {
+  uint32_t b;
+  if (kind == SK_F16 || kind == SK_BF16) b = reinterpret_cast<const uint16_t*>(s)[n];
+  else if (kind == SK_F32) b = reinterpret_cast<const uint32_t*>(s)[n];
+  else b = *reinterpret_cast<const uint32_t*>(s);
+  return b;
+}
+__device__ inline float scale_value(uint32_t b, int kind) {
+  if (kind == SK_F16) return F16::to_f32((uint16_t)b);
+  if (kind == SK_BF16) return BF16::to_f32((uint16_t)b);
+  return __uint_as_float(b);
+}
+
 __device__ inline u4 load_u4(const void* p) { return *reinterpret_cast<const u4*>(p); }
 // Streaming (non-temporal) 16-byte load for data read exactly once.
 __device__ inline u4 load_u4_stream(const void* p) {

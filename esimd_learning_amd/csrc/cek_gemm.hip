@@ -165,11 +165,14 @@ __device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
 // With SL (scales in LDS), rs and cs point at LDS copies of the tile's BM row
 // and BN column scales (loaded by the kernel's prologue, outside smem's first
 // BM * BN * 2 bytes) instead of the global vectors.
+// With wskind >= 0 the column scale is the weight scale ws of that kind
+// (ScaleKind: per channel fp16 / bf16 / fp32, or one fp32 value), in place
+// of cs * s0.
 template <typename T, int BM, int BN, int WM, int WN, int NT = 256, bool SL = false>
 __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], uint8_t* smem, int wm, int wn,
                                   int lane, int m0, int n0, int M, int N, const float* rs, const float* cs,
                                   float s0, uint16_t* Y, int mlo = 0,
-                                  int nlo = 0) {
+                                  int nlo = 0, const void* ws = nullptr, int wskind = -1) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
   constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
   static_assert(CPR % 8 == 0, "the chunk swizzle stays inside aligned groups of 8");
@@ -190,7 +193,8 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int c = wn * TN + j * 16 + r16;
-    const float cv = (SL ? cs[c] : (cs ? cs[min(n0 + c, N - 1)] : 1.f)) * s0;
+    const float cv = wskind >= 0 ? load_scale(ws, wskind, min(n0 + c, N - 1))
+                                 : (SL ? cs[c] : (cs ? cs[min(n0 + c, N - 1)] : 1.f)) * s0;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -620,7 +624,7 @@ __device__ inline void w8a16_issue_off(uint8_t* smem, int stage, int kb, int wav
 
 template <typename T, int FMT, int BM, int BN, int OCC, int WM = 2, int WN = 2>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ scale, int skind,
     uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
   constexpr int BK = 64;
   constexpr int NW = WM * WN;
@@ -686,7 +690,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
   }
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
-  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, *scale, Y);
+  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, 1.f, Y, 0, 0, scale,
+                                         skind);
 }
 
 // ---------------------------------------------------------------------------
@@ -752,7 +757,7 @@ struct W8Pipe {
 
 template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN, int LW>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ scale, int skind,
     uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
   using P = W8Pipe<T, FMT, BM, BN, WM, WN, LW>;
   constexpr int BK = P::BK, NW = P::NW, TM = P::TM, TN = P::TN, FM = P::FM, FN = P::FN, STAGE = P::STAGE;
@@ -811,7 +816,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
   if (kt < KT) P::step(kt, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0, b1);
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
-  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, *scale, Y);
+  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, 1.f, Y, 0, 0, scale,
+                                         skind);
 }
 
 // ---------------------------------------------------------------------------
@@ -828,7 +834,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
 template <typename T, int FMT, int U>
 __global__ __launch_bounds__(256) void gemm_w8a16_tinyn_kernel(const uint16_t* __restrict__ X,
                                                                const uint8_t* __restrict__ W,
-                                                               const float* __restrict__ scale,
+                                                               const void* __restrict__ scale, int skind,
                                                                uint16_t* __restrict__ Y, int M, int N, int K) {
   __shared__ f4 red[3][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -862,10 +868,12 @@ __global__ __launch_bounds__(256) void gemm_w8a16_tinyn_kernel(const uint16_t* _
     }
   }
   if (wave > 0) red[wave - 1][lane] = acc;
+  // the column's weight scale, loaded by every lane before the branches
+  // below (columns >= N read column N - 1 and are never stored)
+  const float sc = load_scale(scale, skind, min(r16, N - 1));
   __syncthreads();
   if (wave != 0) return;
   const f4 c = acc + red[0][lane] + red[1][lane] + red[2][lane];
-  const float sc = *scale;
   const int n = r16;  // D column = lane & 15
   if (n >= N) return;
 #pragma unroll
@@ -882,7 +890,7 @@ __global__ __launch_bounds__(256) void gemm_w8a16_tinyn_kernel(const uint16_t* _
 
 template <typename T, int FMT>
 __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const float* __restrict__ scale,
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ scale, int skind,
     uint16_t* __restrict__ Y, int M, int N, int K) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m0 = blockIdx.y * 64 + (wave >> 1) * 32;
@@ -919,7 +927,9 @@ __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
         acc[i][j] = mfma16x16x32<T>(xb[i], wh[j], acc[i][j]);
       }
   }
-  const float sc = *scale;
+  float sc[2];  // the columns' weight scales, loaded before any branch (column N - 1 past N)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) sc[j] = load_scale(scale, skind, min(n0 + j * 16 + r16, N - 1));
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + j * 16 + r16;
@@ -929,7 +939,7 @@ __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = m0 + i * 16 + g * 4 + v;
-        if (m < M) Y[(size_t)m * N + n] = T::from_f32(acc[i][j][v] * sc);
+        if (m < M) Y[(size_t)m * N + n] = T::from_f32(acc[i][j][v] * sc[j]);
       }
   }
 }
@@ -945,22 +955,27 @@ using namespace cek;
 #define CEK_A8W8_LAYOUT 1
 #endif
 
-extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scale, void* y,
-                                 int64_t M, int64_t N, int64_t K,
-                                 int io_dtype, int fp8_fmt, void* stream) {
+namespace cek {
+
+// w8a16 product for any M with a weight scale of kind skind (ScaleKind):
+// M <= 16 the GEMV kernels, N <= 16 the activation-streaming kernel,
+// 16 < M <= 32 the LDS-staged GEMV where it has an instantiation, else the
+// tiled MFMA GEMM (or the generic kernels for unaligned shapes).
+int launch_w8a16(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N, int64_t K,
+                 int io_dtype, int fp8_fmt, hipStream_t st) {
   if (M < 0 || N < 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
   if (M == 0 || N == 0) return CEK_OK;
   if (!x || !w || !scale || !y) return CEK_ERR_INVALID;
   if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
   if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
-  hipStream_t st = (hipStream_t)stream;
-  if (M <= 16) return launch_gemv(x, w, scale, 3 /* f32 scalar */, y, M, N, K, io_dtype, fp8_fmt, st);
+  if (skind < SK_F16 || skind > SK_F32_SCALAR) return CEK_ERR_INVALID;
+  if (M <= 16) return launch_gemv(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, st);
   if (N <= 16 && K % 64 == 0 && aligned(x, 16) && aligned(w, 16) && M <= (int64_t)INT32_MAX - 16) {
     const dim3 grid((unsigned)((M + 15) / 16));
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     uint16_t* yp = static_cast<uint16_t*>(y);
-#define CEK_TINYN(TY, F) gemm_w8a16_tinyn_kernel<TY, F, 4><<<grid, 256, 0, st>>>(xp, wp, scale, yp, (int)M, (int)N, (int)K)
+#define CEK_TINYN(TY, F) gemm_w8a16_tinyn_kernel<TY, F, 4><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, (int)M, (int)N, (int)K)
     if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_TINYN(F16, CEK_E4M3);
     else if (io_dtype == CEK_F16) CEK_TINYN(F16, CEK_E5M2);
     else if (fp8_fmt == CEK_E4M3) CEK_TINYN(BF16, CEK_E4M3);
@@ -969,11 +984,11 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
     return check_launch();
   }
   if (M <= 32 && aligned(x, 16) && aligned(w, 16)) {
-    const int rc = launch_gemv_wide(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
+    const int rc = launch_gemv_wide(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, st);
     if (rc != CEK_ERR_UNSUPPORTED) return rc;
   }
   if (K % 64 != 0 || !aligned(x, 16) || !aligned(w, 16) || M > 65535 * 64)
-    return launch_gemv_generic(x, w, scale, 3, y, M, N, K, io_dtype, fp8_fmt, st);
+    return launch_gemv_generic(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, st);
   {
     // Tiles: 128 x 128 with 4 waves and two workgroups per CU, or the
     // register-pipelined 8-wave kernel (2 x 4 waves, four loader waves) at
@@ -1006,13 +1021,13 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   do {                                                                                                         \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                    \
     gemm_w8a16_lds_kernel<TY, F, BM, BN, OCC, WM, WN>                                                          \
-        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn);              \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, skind, yp, M, N, K, tm, tn);       \
   } while (0)
 #define CEK_W8A16_PIPE(TY, F, BM, BN, OCC, WM, WN)                                                                 \
   do {                                                                                                         \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                    \
     gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN, CEK_W8A16_LW>                                                         \
-        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, yp, M, N, K, tm, tn);              \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, skind, yp, M, N, K, tm, tn);       \
   } while (0)
 #define CEK_W8A16(TY, F)                                          \
   do {                                                            \
@@ -1034,11 +1049,19 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint8_t* wp = static_cast<const uint8_t*>(w);
   uint16_t* yp = static_cast<uint16_t*>(y);
-  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) gemm_w8a16_simple_kernel<F16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, wp, scale, yp, M, N, K);
-  else if (io_dtype == CEK_F16) gemm_w8a16_simple_kernel<F16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, wp, scale, yp, M, N, K);
-  else if (fp8_fmt == CEK_E4M3) gemm_w8a16_simple_kernel<BF16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, wp, scale, yp, M, N, K);
-  else gemm_w8a16_simple_kernel<BF16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, wp, scale, yp, M, N, K);
+  if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) gemm_w8a16_simple_kernel<F16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+  else if (io_dtype == CEK_F16) gemm_w8a16_simple_kernel<F16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+  else if (fp8_fmt == CEK_E4M3) gemm_w8a16_simple_kernel<BF16, CEK_E4M3><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
+  else gemm_w8a16_simple_kernel<BF16, CEK_E5M2><<<grid, 256, 0, st>>>(xp, wp, scale, skind, yp, M, N, K);
   return check_launch();
+}
+
+}  // namespace cek
+
+extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scale, void* y,
+                                 int64_t M, int64_t N, int64_t K,
+                                 int io_dtype, int fp8_fmt, void* stream) {
+  return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 
 namespace cek {

@@ -40,32 +40,9 @@
 
 namespace cek {
 
-enum ScaleKind { SK_F16 = 0, SK_BF16 = 1, SK_F32 = 2, SK_F32_SCALAR = 3 };
 
-__device__ inline float load_scale(const void* s, int kind, int n) {
-  switch (kind) {
-    case SK_F16: return F16::to_f32(reinterpret_cast<const uint16_t*>(s)[n]);
-    case SK_BF16: return BF16::to_f32(reinterpret_cast<const uint16_t*>(s)[n]);
-    case SK_F32: return reinterpret_cast<const float*>(s)[n];
-    default: return *reinterpret_cast<const float*>(s);
-  }
-}
-
-// The same in two halves, for kernels that load the scale long before they
-// use it: the load alone (raw bits, no conversion, so nothing waits for it
-// until scale_value) and the conversion.
-__device__ inline uint32_t load_scale_bits(const void* s, int kind, int n) {
-  uint32_t b;
-  if (kind == SK_F16 || kind == SK_BF16) b = reinterpret_cast<const uint16_t*>(s)[n];
-  else if (kind == SK_F32) b = reinterpret_cast<const uint32_t*>(s)[n];
-  else b = *reinterpret_cast<const uint32_t*>(s);
-  return b;
-}
-__device__ inline float scale_value(uint32_t b, int kind) {
-  if (kind == SK_F16) return F16::to_f32((uint16_t)b);
-  if (kind == SK_BF16) return BF16::to_f32((uint16_t)b);
-  return __uint_as_float(b);
-}
+int launch_w8a16(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N, int64_t K,
+                 int io_dtype, int fp8_fmt, hipStream_t st);  // cek_gemm.hip
 
 constexpr int MAX_SEGS = 8;
 
@@ -940,9 +917,11 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint16_t* __res
   const SegRef sr = find_seg(sg, blockIdx.x);
   const int lane = threadIdx.x & 63;
   const int n = sr.group * 4 + (threadIdx.x >> 6);
+  // the row's weight scale before any branch (a wave past the last row reads
+  // the last row's and returns)
+  const float sc = load_scale(sr.s, skind, min(n, sr.n - 1));
   if (n >= sr.n) return;
   const uint8_t* wr = sr.w + (size_t)n * K;
-  const float sc = load_scale(sr.s, skind, n);
   for (int m = 0; m < M; ++m) {
     const uint16_t* xr = x + (size_t)m * K;
     float acc = 0.f;
@@ -1455,17 +1434,22 @@ extern "C" int cek_gemv_fp8_gelu_and_mul(const void* x, const float* x_scale, co
                               (hipStream_t)stream);
 }
 
+// More than 16 rows: the w8a16 GEMM dispatch (cek_gemm.hip), which streams
+// the weights once for all rows instead of once per 16-row slab.
 extern "C" int cek_gemv_fp8_pern(const void* x, const void* w, const void* scale, void* y,
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
   const int skind = cek::scale_kind(scale_dtype);
   if (skind < 0) return CEK_ERR_INVALID;
+  if (M > 16) return cek::launch_w8a16(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
   return cek::launch_gemv(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 
 extern "C" int cek_gemv_fp8_pert(const void* x, const void* w, const float* scale, void* y,
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, void* stream) {
+  if (M > 16)
+    return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
   return cek::launch_gemv(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 

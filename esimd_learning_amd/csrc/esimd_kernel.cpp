@@ -60,18 +60,14 @@ static void run_gemv(const at::Tensor& input, const at::Tensor& weight, const at
   void* st = current_stream(input);
   const int io = io_code(input.scalar_type());
   const int fmt = fp8_code(weight);
-  const size_t esz = input.element_size();
-  // The kernels take up to 16 rows per launch; larger M is split into slabs.
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
-    const int64_t mb = std::min<int64_t>(16, M - m0);
-    const char* x = static_cast<const char*>(input.data_ptr()) + m0 * K * esz;
-    char* y = static_cast<char*>(output.data_ptr()) + m0 * N * esz;
-    int rc = per_tensor
-                 ? cek_gemv_fp8_pert(x, weight.data_ptr(), static_cast<const float*>(scale.data_ptr()), y, mb, N, K,
-                                     io, fmt, st)
-                 : cek_gemv_fp8_pern(x, weight.data_ptr(), scale.data_ptr(), y, mb, N, K, io, fmt, scale_code, st);
-    check_rc(rc, op);
-  }
+  // Up to 16 rows the decode GEMV kernels; more rows the w8a16 GEMM, which
+  // streams the weights once for all of them.
+  const int rc = per_tensor ? cek_gemv_fp8_pert(input.data_ptr(), weight.data_ptr(),
+                                                static_cast<const float*>(scale.data_ptr()), output.data_ptr(), M, N,
+                                                K, io, fmt, st)
+                            : cek_gemv_fp8_pern(input.data_ptr(), weight.data_ptr(), scale.data_ptr(),
+                                                output.data_ptr(), M, N, K, io, fmt, scale_code, st);
+  check_rc(rc, op);
 }
 
 at::Tensor esimd_gemv_fp8_pern(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
@@ -257,9 +253,9 @@ void esimd_gelu_and_mul(at::Tensor out, at::Tensor input) {
 
 // Gate/up GEMV over a merged [2d, K] weight with gelu_and_mul fused into its
 // epilogue: output[m, i] = gelu_tanh(g[m, i]) * u[m, i], g and u the GEMV's
-// rounded outputs of rows i and d + i.  Slabs of up to 16 rows go to the
-// fused kernel; shapes it does not cover run the GEMV into a workspace and
-// then gelu_and_mul (the same values).
+// rounded outputs of rows i and d + i.  Up to 16 rows go to the fused
+// kernel; shapes it does not cover, and more rows, run the GEMV into a
+// workspace and then gelu_and_mul (the same values).
 void esimd_gemv_fp8_gelu_and_mul(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output) {
   const char* op = "esimd_gemv_fp8_gelu_and_mul";
   check_gemv_io(input, output, op);
@@ -287,6 +283,15 @@ void esimd_gemv_fp8_gelu_and_mul(at::Tensor input, at::Tensor weight, at::Tensor
   const int io = io_code(input.scalar_type());
   const int fmt = fp8_code(weight);
   const size_t esz = input.element_size();
+  if (M > 16) {
+    // the GEMV over all rows at once (weights streamed once), then gelu_and_mul
+    at::Tensor gu = at::empty({M, 2 * d}, input.options());
+    check_rc(cek_gemv_fp8_pern(input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(), gu.data_ptr(), M, 2 * d,
+                               K, io, fmt, scale_code, st),
+             op);
+    check_rc(cek_gelu_and_mul(output.data_ptr(), gu.data_ptr(), M, d, 2 * d, d, io, st), op);
+    return;
+  }
   at::Tensor gu;  // workspace of the unfused path, [16, 2d]
   for (int64_t m0 = 0; m0 < M; m0 += 16) {
     const int64_t mb = std::min<int64_t>(16, M - m0);

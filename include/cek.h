@@ -46,10 +46,12 @@ const char* cek_last_hip_error(void);
 int cek_version(void);
 
 /*
- * fp8-weight GEMV with per-output-channel scale, M <= 16 rows.
+ * fp8-weight GEMV with per-output-channel scale.
  *   y[m, n] = Out( (sum_k f32(x[m, k]) * dq(w[n, k])) * f32(scale[n]) )
  * x [M, K] io_dtype (F16|BF16), w [N, K] fp8 row-major (K contiguous),
- * scale [N] of scale_dtype (F16|BF16|F32), y [M, N] io_dtype.
+ * scale [N] of scale_dtype (F16|BF16|F32), y [M, N] io_dtype.  M <= 16 runs
+ * the decode GEMV kernels; larger M the w8a16 GEMM of cek_gemm_fp8_pert
+ * with this scale (the weights are streamed once for all rows).
  * Replaces esimd_gemv_fp8_pern, csrc/xpu/esimd_kernel.sycl:22-53 ->
  * GEMV_fp8_pern_host, csrc/xpu/esimd_kernels/fp8_GEMV_v2.h:127-191 (which
  * computes row 0 only; here every row m < M).

@@ -27,7 +27,7 @@ int main(void) {
 
   expect(cek_version() / 10000, 0, "major version");
   expect(strcmp(cek_error_string(CEK_OK), cek_error_string(CEK_ERR_INVALID)) != 0, 1, "distinct status strings");
-  expect(cek_gemv_fp8_pern(p, p, p, p, 17, 8, 64, CEK_F16, CEK_E4M3, CEK_F32, NULL), CEK_ERR_INVALID, "gemv M > 16");
+  expect(cek_gemv_fp8_pern(p, p, p, p, -1, 8, 64, CEK_F16, CEK_E4M3, CEK_F32, NULL), CEK_ERR_INVALID, "gemv M < 0");
   expect(cek_gemv_fp8_pern(NULL, NULL, NULL, NULL, 0, 8, 64, CEK_F16, CEK_E4M3, CEK_F32, NULL), CEK_OK, "gemv M = 0");
   expect(cek_gemv_fp8_pert(p, p, NULL, p, 1, 8, 0, CEK_BF16, CEK_E5M2, NULL), CEK_ERR_INVALID, "gemv K = 0");
   expect(cek_gemv_fp8_pern_multi(p, 0, ws, ss, ys, ns, 1, 64, CEK_F16, CEK_E4M3, CEK_F32, NULL), CEK_ERR_INVALID,

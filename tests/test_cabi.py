@@ -61,7 +61,8 @@ def test_host_rejects_invalid_arguments():
     lib = cabi.load()
     p = C.c_void_p(16)   # never dereferenced: every call below fails validation first
     E = cabi.CEK_ERR_INVALID
-    assert lib.cek_gemv_fp8_pern(p, p, p, p, 17, 8, 64, 0, 0, 2, None) == E          # M > 16
+    assert lib.cek_gemv_fp8_pern(p, p, p, p, -1, 8, 64, 0, 0, 2, None) == E          # M < 0
+    assert lib.cek_gemv_fp8_pern(p, p, p, p, 17, 8, 64, 0, 0, 9, None) == E          # scale dtype, M > 16
     assert lib.cek_gemv_fp8_pern(p, p, p, p, 1, 8, 64, 0, 0, 7, None) == E           # scale dtype
     assert lib.cek_gemv_fp8_pert(p, p, p, p, 1, 8, 0, 0, 0, None) == E               # K = 0
     assert lib.cek_gemv_fp8_pert(None, p, p, p, 1, 8, 64, 0, 0, None) == E           # null x

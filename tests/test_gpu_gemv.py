@@ -151,14 +151,27 @@ def test_gemv_misaligned_input(ops, dev):
     assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, W8, s), "misaligned")
 
 
-def test_gemv_many_rows_sliced(ops, dev):
-    # M > 16 through the GEMV op: processed in 16-row slabs
-    N, K, M = 512, 1024, 37
-    _say("gemv M=37 slabs")
-    W8, s = synthetic.weight_fp8(N, K, seed=11)
-    x = synthetic.activations(M, K, seed=12)
-    y = _run_pern(ops, x, W8, s, dev)
-    assert_close_fp(y, ogemv.gemv_fp8_pern(x, W8, s), "M=37")
+@pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("io", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", [(17, 2048, 3000), (37, 1024, 512), (64, 4096, 4096), (300, 2048, 6000),
+                                   (100, 640, 100), (40, 1000, 72), (50, 2048, 12)])
+def test_gemv_many_rows(ops, dev, M, K, N, io, sdt):
+    """M > 16 through the GEMV ops: the w8a16 GEMM dispatch with the
+    per-channel scale (LDS GEMV up to 32 rows, tiled MFMA GEMM, tiny-N kernel
+    for N <= 16, generic kernel for K % 64 != 0), weights streamed once; also
+    the per-tensor op."""
+    _say(f"gemv many rows M={M} K={K} N={N} {io} scale {sdt}")
+    W8, s = synthetic.weight_fp8(N, K, seed=M + N)
+    s = s.to(sdt)
+    x = synthetic.activations(M, K, seed=M, dtype=io)
+    y = torch.full((M, N), float("nan"), dtype=io, device=dev)
+    ops.esimd_gemv_fp8_pern(x.to(dev), W8.to(dev), s.to(dev), y, N, K)
+    sv = torch.tensor(0.013)
+    yt = torch.full((M, N), float("nan"), dtype=io, device=dev)
+    ops.esimd_gemv_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), yt)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, W8, s), f"pern M={M}")
+    assert_close_fp(yt.cpu(), ogemv.gemv_fp8_pert(x, W8, sv), f"pert M={M}")
 
 
 def test_gemv_reference_row0_semantics(ops, dev):

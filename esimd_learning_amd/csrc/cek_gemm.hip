@@ -344,6 +344,24 @@ __device__ inline void barrier_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// The same leaving min(steps, MAXS) later steps' loads in flight (PER loads
+// per step and wave, issued in step order): the count is an immediate, so a
+// uniform branch picks it.  Waves with fewer loads out pass at once.
+template <int MAXS, int PER>
+__device__ inline void barrier_upto(int steps) {
+  static_assert(MAXS <= 3 && MAXS * PER <= 63, "vmcnt immediate");
+  if constexpr (MAXS >= 3) {
+    if (steps >= 3) { barrier_vmcnt<3 * PER>(); return; }
+  }
+  if constexpr (MAXS >= 2) {
+    if (steps >= 2) { barrier_vmcnt<2 * PER>(); return; }
+  }
+  if constexpr (MAXS >= 1) {
+    if (steps >= 1) { barrier_vmcnt<PER>(); return; }
+  }
+  barrier_vmcnt<0>();
+}
+
 // Direct-to-LDS loads of one K step (128 bytes) of CH 1 KB row chunks into a
 // slot: chunks j = w + STRIDE i (rows 8 j .. 8 j + 7) of loader w.
 template <int CH, int STRIDE>
@@ -369,8 +387,12 @@ __device__ inline void a8w8_issue_off(uint8_t* slot, int kb, int w, const uint8_
 #endif
 }
 
-template <int BM, int BN, int WM, int WN, int LW>
-__device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uint8_t* sBr, bool loader, int wave,
+// One K step kt from ring slot c (the next step's slot cn).  Its barrier
+// (before the last MFMA group) waits for step kt + 1's loads, leaves up to
+// RING - 2 later steps' in flight, and refills slot c -- fully read by then --
+// with step kt + RING.
+template <int BM, int BN, int WM, int WN, int LW, int RING>
+__device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, int c, int cn, uint8_t* sAr, uint8_t* sBr, bool loader, int wave,
                                                int wm, int wn, int r16, int p0, int p1, const uint8_t* A, const uint8_t* B,
                                                int K, uint32_t ga, uint32_t gb,
                                                f4 (&acc)[PipeCfg<BM, BN, WM, WN>::FM][PipeCfg<BM, BN, WM, WN>::FN],
@@ -379,20 +401,19 @@ __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uin
   using C = PipeCfg<BM, BN, WM, WN>;
   using L = LoadSplit<BM, BN, LW>;
   constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
-  const int c = kt & 1;
   const uint8_t* sA = sAr + c * C::ASLOT + (wm * TM + r16) * BK;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     if (i + 1 < FM) {
       a[(i + 1) & 1] = lds_frag(sA + (i + 1) * 16 * BK, p0, p1);
     } else if (kt + 1 < KT) {
-      barrier_vmcnt<0>();
-      if (loader && kt + 2 < KT) {
-        a8w8_issue_off<L::BL, LW>(sBr + c * C::BSLOT, (kt + 2) * BK, wave, B, K, gb);
-        a8w8_issue_off<L::AL, LW>(sAr + c * C::ASLOT, (kt + 2) * BK, wave, A, K, ga);
+      barrier_upto<RING - 2, L::AL + L::BL>(KT - 2 - kt);
+      if (loader && kt + RING < KT) {
+        a8w8_issue_off<L::BL, LW>(sBr + c * C::BSLOT, (kt + RING) * BK, wave, B, K, gb);
+        a8w8_issue_off<L::AL, LW>(sAr + c * C::ASLOT, (kt + RING) * BK, wave, A, K, ga);
       }
-      const uint8_t* nA = sAr + (c ^ 1) * C::ASLOT + (wm * TM + r16) * BK;
-      const uint8_t* nB = sBr + (c ^ 1) * C::BSLOT + (wn * TN + r16) * BK;
+      const uint8_t* nA = sAr + cn * C::ASLOT + (wm * TM + r16) * BK;
+      const uint8_t* nB = sBr + cn * C::BSLOT + (wn * TN + r16) * BK;
 #pragma unroll
       for (int j = 0; j < FN; ++j) bn[j] = lds_frag(nB + j * 16 * BK, p0, p1);
       a[0] = lds_frag(nA, p0, p1);
@@ -409,7 +430,8 @@ __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, uint8_t* sAr, uin
 // ((K / SPLIT) % 128 == 0) and stores its unscaled fp32 sums to part
 // P[b % SPLIT] of the [SPLIT][M][N] workspace P; gemm_splitk_finalize then
 // adds the parts in order, scales and converts.
-template <typename T, int BM, int BN, int WM, int WN, int OCC, int LW, int SPLIT = 1>
+// RING: slots of the A and B rings (loads run RING - 1 steps ahead).
+template <typename T, int BM, int BN, int WM, int WN, int OCC, int LW, int SPLIT = 1, int RING = 2>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sa,
     const uint8_t* __restrict__ B, const float* __restrict__ sb,
@@ -419,14 +441,15 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NW = C::NW;
   constexpr int AL = L::AL, BL = L::BL;
   static_assert(LW >= 1 && LW <= NW, "loader waves");
-  constexpr int RINGS = 2 * C::ASLOT + 2 * C::BSLOT;
+  static_assert(RING >= 2 && RING <= 4, "ring slots");
+  constexpr int RINGS = RING * (C::ASLOT + C::BSLOT);
   constexpr int SMEM = RINGS > BM * BN * 2 ? RINGS : BM * BN * 2;
   static_assert(BM + BN <= 64 * NW, "one scale per thread");
   // the A ring and the B ring (or the output tile), then the tile's row and
   // column scales
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + (BM + BN) * 4];
   uint8_t* sAr = smem;
-  uint8_t* sBr = smem + 2 * C::ASLOT;
+  uint8_t* sBr = smem + RING * C::ASLOT;
   float* sc = reinterpret_cast<float*>(smem + SMEM);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -471,18 +494,18 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK / SPLIT;
-  // Prologue: steps 0 and 1, then wait for step 0 (a loader's step 1 loads,
-  // issued last, may fly; a non-loader has at most its older scale load out).
+  // Prologue: steps 0 .. RING - 1 into their slots, then wait for step 0 (a
+  // loader's later steps, issued after it, may fly; a non-loader has at most
+  // its older scale load out).
   if (loader) {
-    a8w8_issue_off<BL, LW>(sBr, 0, wave, B, K, gb);
-    a8w8_issue_off<AL, LW>(sAr, 0, wave, A, K, ga);
-    if (KT > 1) {
-      a8w8_issue_off<BL, LW>(sBr + C::BSLOT, BK, wave, B, K, gb);
-      a8w8_issue_off<AL, LW>(sAr + C::ASLOT, BK, wave, A, K, ga);
-    }
+#pragma unroll
+    for (int s = 0; s < RING; ++s)
+      if (s == 0 || s < KT) {
+        a8w8_issue_off<BL, LW>(sBr + s * C::BSLOT, s * BK, wave, B, K, gb);
+        a8w8_issue_off<AL, LW>(sAr + s * C::ASLOT, s * BK, wave, A, K, ga);
+      }
   }
-  if (KT > 1) barrier_vmcnt<AL + BL>();
-  else barrier_vmcnt<0>();
+  barrier_upto<RING - 1, AL + BL>(KT - 1);
   i8 a[2], b0[FN], b1[FN];
   {
     const uint8_t* sA = sAr + (wm * TM + r16) * BK;
@@ -491,16 +514,22 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     for (int j = 0; j < FN; ++j) b0[j] = lds_frag(sB + j * 16 * BK, p0, p1);
     a[0] = lds_frag(sA, p0, p1);
   }
-  int kt = 0;
+  int kt = 0, c = 0;
+  auto nxt = [](int v) { return v + 1 == RING ? 0 : v + 1; };
   for (; kt + 1 < KT; kt += 2) {
-    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b0, b1);
-    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt + 1, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b1, b0);
+    const int c1 = RING == 2 ? 1 : nxt(c), c2 = RING == 2 ? 0 : nxt(c1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW, RING>(kt, KT, RING == 2 ? 0 : c, c1, sAr, sBr, loader, wave, wm, wn, r16, p0,
+                                             p1, A, B, K, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW, RING>(kt + 1, KT, c1, c2, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B,
+                                             K, ga, gb, acc, a, b1, b0);
+    c = c2;
   }
   if (kt < KT)
-    a8w8_pipe_step<BM, BN, WM, WN, LW>(kt, KT, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW, RING>(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), sAr, sBr, loader, wave,
+                                             wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b0, b1);
   // every wave's loads (a non-loader's scale load included) are complete
-  // here: each step's barrier waited for vmcnt(0), and with KT == 1 the
-  // prologue's did
+  // here: step KT - 2's barrier (the last) waited for vmcnt(0), and with
+  // KT == 1 the prologue's did
   static_assert(SMEM >= BM * BN * 2, "output tile must fit");
   if constexpr (SPLIT > 1) {
     // fp32 partial sums in D layout: lane l holds column l & 15, rows
@@ -1066,31 +1095,85 @@ extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scal
 
 namespace cek {
 
-// Tiled a8w8 configurations: tile, measured rate at full occupancy (MI355X,
-// BASELINE prefill shapes, TFLOP/s) and workgroup slots over 256 CUs (the
-// 8-wave tiles fit one workgroup per CU, the 4-wave ones two):
-//  * 64 x 128 for few, small tiles;
-//  * 128 x 128, 4 waves, two workgroups per CU so that one's MFMAs cover
-//    the other's LDS reads and barrier waits;
-//  * 256 x 192, 8 waves (2 x 4, four loader waves);
-//  * 256 x 256, 8 waves (2 x 4, wave tile 128 x 64, two waves per SIMD,
-//    four loader waves): the least load and LDS traffic per MFMA.
-struct A8w8Opt { int bm, bn; double rate; int slots; };
-constexpr A8w8Opt kA8w8Opts[4] = {{64, 128, 1750, 512}, {128, 128, 2250, 512}, {256, 192, 2480, 256}, {256, 256, 2650, 256}};
+// Tiled a8w8 configurations.  Rate: measured TFLOP/s at full occupancy
+// (cache-resident operands; the model for M < 128 and matrices above 4 GB).
+// Slots: workgroups over 256 CUs at once.  t0 / step: the round model fitted
+// to the nine config-4 shapes with operands streamed from HBM (us per round:
+// t0 + step per 128-deep K step of one workgroup; every launch below timed
+// on MI355X).
+//  0  64 x 128, 4 waves (2 x 2), two workgroups per CU, 2 ring slots;
+//  1  128 x 128, 4 waves, two per CU (one's MFMAs cover the other's LDS
+//     reads and barrier waits), 2 slots;
+//  2  256 x 192, 8 waves (2 x 4, four loader waves), 2 slots;
+//  3  256 x 256, 8 waves (wave tile 128 x 64, two waves per SIMD): the least
+//     load and LDS traffic per MFMA, 2 slots (128 KB of LDS);
+//  4  128 x 128, 8 waves (2 x 4, four loader waves), 3 slots: loads two
+//     steps ahead, one workgroup per CU;
+//  5  128 x 256, 8 waves, 3 slots;
+//  6  256 x 128, 8 waves, 3 slots.
+// The 3-slot tiles are for weights streamed from HBM, whose latency one step
+// of lead does not cover on a small tile (M = 512, K = 4096, N = 6144: 64 x
+// 128 in 2 slots 32.0 us, 128 x 128 8-wave in 3 slots 21.5 us).
+struct A8w8Opt { int bm, bn; double rate; int slots; double t0, step; };
+constexpr int kA8w8Cfgs = 7;
+constexpr A8w8Opt kA8w8Opts[kA8w8Cfgs] = {
+    {64, 128, 1750, 512, 0.0, 0.686},   {128, 128, 2250, 512, 1.56, 1.085}, {256, 192, 2480, 256, 0.0, 1.461},
+    {256, 256, 2650, 256, 0.0, 1.760},  {128, 128, 0, 256, 2.87, 0.560},    {128, 256, 0, 256, 3.65, 0.914},
+    {256, 128, 0, 256, 2.99, 0.957}};
+constexpr bool a8w8_splits(int c) { return c == 1 || c == 5 || c == 6; }
 
 struct A8w8Plan { int cfg, split; };
 
-// Estimated time of each configuration: its rounds of workgroups at the
-// full-occupancy rate (a partial round costs a full one), for the 4-wave
-// tiles also with K split in 2 or 4 parts (each part a workgroup) plus the
-// fp32 partials' traffic and the finalize launch.  Split only when allowed
-// (a workspace is there), on the pipelined path, and 10% faster than the
-// best unsplit plan.  Unsplit, this picks the fastest measured tile, or one
-// within 2% of it, on all nine config-4 shapes; split, the fastest of the
-// four split forms at M = 512, K = 14336 (128 x 128 in 4 parts: 44 us
-// against 65 us unsplit), and no split where splitting measured slower
-// (M = 512, K = 4096; M = 1024).
+// Round model (us) of configuration c with K in sp parts: U workgroups over
+// S slots run floor(U / S) full rounds and, for a last round of fill f,
+// 0.6 + 0.4 f of one (its workgroups share HBM and L2 with fewer others); a
+// round takes t0 + step per K step of a part.  Split adds the finalize: the
+// parts read and the output written at ~5 TB/s, plus a launch.
+static double a8w8_round_us(const A8w8Opt& o, int64_t M, int64_t N, int64_t K, int sp) {
+  const int64_t units = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn) * sp;
+  const int64_t full = units / o.slots;
+  const double f = (double)(units - full * o.slots) / (double)o.slots;
+  const double rounds = (double)full + (f > 0.0 ? 0.6 + 0.4 * f : 0.0);
+  double t = rounds * (o.t0 + (double)(K / 128 / sp) * o.step);
+  if (sp > 1) t += ((double)sp * M * N * 4.0 + (double)M * N * 2.0) / 5.0e6 + 1.5;
+  return t;
+}
+
+// M >= 128 on the pipelined path: the fastest configuration by the round
+// model, split in 2, 4 or 8 parts (at least 1024 K values each) where
+// allowed.  Fitted on the nine config-4 shapes (weights from HBM), it picks
+// the measured fastest on all nine, with cache-resident operands too; on
+// twelve other shapes (M = 128 .. 3000, K = 2048 .. 14336, ragged N) within
+// 6% of the fastest of thirteen measured forms.
+static A8w8Plan plan_a8w8_rounds(int64_t M, int64_t N, int64_t K, bool allow_split) {
+  A8w8Plan best{1, 1};
+  double tbest = -1.0;
+  for (int c = 0; c < kA8w8Cfgs; ++c) {
+    const A8w8Opt& o = kA8w8Opts[c];
+    if (M < o.bm || N < o.bn) continue;
+    for (int sp : {1, 2, 4, 8}) {
+      if (sp > 1 && (!allow_split || !a8w8_splits(c) || (K / 128) % sp || K / sp < 1024)) continue;
+      const double t = a8w8_round_us(o, M, N, K, sp);
+      if (tbest < 0 || t < tbest) {
+        tbest = t;
+        best = A8w8Plan{c, sp};
+      }
+    }
+  }
+  return best;
+}
+
+// Below 128 rows or columns (only the 64 x 128 tile fits), or with matrices
+// above 4 GB (the clamped-load kernel, configurations 0-3): each configuration's
+// rounds of workgroups at its full-occupancy rate (a partial round costs a
+// full one), the 64 x 128 tile also split in 2, 4 or 8 parts plus the fp32
+// partials' traffic and the finalize launch; split only when allowed, on the
+// pipelined path, and 10% faster than the best unsplit plan.  At M = 64
+// (config 3's prefill-sized decode) the split plans measured 1.2-1.8x faster
+// than the weight-streaming kernels, and 8 parts of 512 K values slower than
+// 4 (M = 64, K = 4096: 13.8 against 11.2 us).
 static A8w8Plan plan_a8w8(int64_t M, int64_t N, int64_t K, bool pipe_ok, bool allow_split) {
+  if (pipe_ok && M >= 128 && N >= 128) return plan_a8w8_rounds(M, N, K, allow_split);
   A8w8Plan best{0, 1};
   double tbest = -1.0;
   for (int c = 0; c < 4; ++c) {
@@ -1109,9 +1192,6 @@ static A8w8Plan plan_a8w8(int64_t M, int64_t N, int64_t K, bool pipe_ok, bool al
     const A8w8Opt& o = kA8w8Opts[c];
     if (!pipe_ok || M < o.bm || N < o.bn) continue;
     for (int sp : {2, 4, 8}) {
-      // at least 1024 K values per part: a part's prologue and partial-sum
-      // epilogue do not shrink with its K range (measured at M = 64, K = 4096:
-      // 4 parts 11.2 us, 8 parts 13.8 us)
       if ((K / 128) % sp || K / sp < 1024) continue;
       const int64_t units = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn) * sp;
       const int64_t rounds = (units + o.slots - 1) / o.slots;
@@ -1248,9 +1328,11 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     // Tile (and split-K) choice: plan_a8w8.  Every configuration runs
     // gemm_a8w8_pipe_kernel (register-pipelined fragment reads,
     // single-offset addressing) when the matrices are below 4 GB and hold at
-    // least one tile in each dimension; otherwise gemm_a8w8_lds_kernel with
-    // the same tile (its loads clamp rows).  Split K needs a workspace of
-    // a8w8_workspace_bytes; without one the unsplit plan runs.
+    // least one tile in each dimension; otherwise configurations 0-3 run
+    // gemm_a8w8_lds_kernel with the same tile (its loads clamp rows), and
+    // the plan only picks 4-6 where the pipelined kernel applies.  Split K
+    // needs a workspace of a8w8_workspace_bytes; without one the unsplit
+    // plan runs.
     const bool off32 = a8w8_off32(M, N, K);
     const int64_t need = a8w8_workspace_bytes(M, N, K);
     const A8w8Plan plan = plan_a8w8(M, N, K, off32, need > 0 && ws && ws_bytes >= need);
@@ -1262,43 +1344,50 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     gemm_a8w8_lds_kernel<TY, BM, BN, WM, WN, CEK_A8W8_LAYOUT, OCC>                                    \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
-#define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, LW)                                                      \
+#define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, LW, RING)                                                \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW>                                                \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, 1, RING>                                       \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, nullptr, M, N, K, tm, tn); \
   } while (0)
-#define CEK_A8W8_SPLIT(TY, BM, BN, OCC, LW, SP)                                                          \
+#define CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, SP, RING)                                          \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_pipe_kernel<TY, BM, BN, 2, 2, OCC, LW, SP>                                              \
-        <<<dim3((unsigned)(tm * tn * SP)), 256, 0, st>>>(a, sa, b, sb, yp, ws, M, N, K, tm, tn);      \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, SP, RING>                                      \
+        <<<dim3((unsigned)(tm * tn * SP)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, ws, M, N, K, tm, tn); \
     gemm_splitk_finalize<TY, SP><<<dim3((unsigned)((N + 2047) / 2048), (unsigned)(M < 65535 ? M : 65535)), \
                                    256, 0, st>>>(ws, sa, sb, yp, (int)M, (int)N);                       \
+  } while (0)
+#define CEK_A8W8_SPLITS(TY, BM, BN, WM, WN, OCC, LW, RING)                                             \
+  do {                                                                                                \
+    if (plan.split == 2) CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, 2, RING);                        \
+    else if (plan.split == 4) CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, 4, RING);                   \
+    else CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, 8, RING);                                        \
   } while (0)
 #define CEK_A8W8_ALL(TY)                                                               \
   do {                                                                                 \
     if (plan.split > 1) {                                                              \
-      if (cfg == 1) {                                                                  \
-        if (plan.split == 2) CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 2);                    \
-        else if (plan.split == 4) CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 4);               \
-        else CEK_A8W8_SPLIT(TY, 128, 128, 2, 4, 8);                                    \
-      } else {                                                                         \
-        if (plan.split == 2) CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 2);                     \
-        else if (plan.split == 4) CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 4);                \
-        else CEK_A8W8_SPLIT(TY, 64, 128, 2, 2, 8);                                     \
-      }                                                                                \
+      if (cfg == 6) CEK_A8W8_SPLITS(TY, 256, 128, 2, 4, 1, 4, 3);                      \
+      else if (cfg == 5) CEK_A8W8_SPLITS(TY, 128, 256, 2, 4, 1, 4, 3);                 \
+      else if (cfg == 1) CEK_A8W8_SPLITS(TY, 128, 128, 2, 2, 2, 4, 2);                 \
+      else CEK_A8W8_SPLITS(TY, 64, 128, 2, 2, 2, 2, 2);                                \
+    } else if (cfg == 6) {                                                             \
+      CEK_A8W8_PIPE(TY, 256, 128, 2, 4, 1, 4, 3);                                      \
+    } else if (cfg == 5) {                                                             \
+      CEK_A8W8_PIPE(TY, 128, 256, 2, 4, 1, 4, 3);                                      \
+    } else if (cfg == 4) {                                                             \
+      CEK_A8W8_PIPE(TY, 128, 128, 2, 4, 1, 4, 3);                                      \
     } else if (cfg == 3) {                                                             \
-      if (pipe) CEK_A8W8_PIPE(TY, 256, 256, 2, 4, 1, 4);                               \
+      if (pipe) CEK_A8W8_PIPE(TY, 256, 256, 2, 4, 1, 4, 2);                            \
       else CEK_A8W8(TY, 256, 256, 4, 2, 1);                                            \
     } else if (cfg == 2) {                                                             \
-      if (pipe) CEK_A8W8_PIPE(TY, 256, 192, 2, 4, 1, 4);                               \
+      if (pipe) CEK_A8W8_PIPE(TY, 256, 192, 2, 4, 1, 4, 2);                            \
       else CEK_A8W8(TY, 256, 192, 2, 4, 1);                                            \
     } else if (cfg == 1) {                                                             \
-      if (pipe) CEK_A8W8_PIPE(TY, 128, 128, 2, 2, 2, 4);                               \
+      if (pipe) CEK_A8W8_PIPE(TY, 128, 128, 2, 2, 2, 4, 2);                            \
       else CEK_A8W8(TY, 128, 128, 2, 2, 2);                                            \
     } else {                                                                           \
-      if (pipe) CEK_A8W8_PIPE(TY, 64, 128, 2, 2, 2, 2);                                \
+      if (pipe) CEK_A8W8_PIPE(TY, 64, 128, 2, 2, 2, 2, 2);                             \
       else CEK_A8W8(TY, 64, 128, 2, 2, 2);                                             \
     }                                                                                  \
   } while (0)
@@ -1307,6 +1396,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
 #undef CEK_A8W8
 #undef CEK_A8W8_PIPE
 #undef CEK_A8W8_SPLIT
+#undef CEK_A8W8_SPLITS
 #undef CEK_A8W8_ALL
     return check_launch();
   }

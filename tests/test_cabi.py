@@ -125,8 +125,8 @@ def test_host_rejects_invalid_arguments():
     assert lib.cek_gemm_fp8_a8w8_ws(p, p, p, p, p, 512, 4096, 14336, 0, C.c_void_p(18), 64, None) == E  # misaligned
     # the no-allocation a8w8 entry point refuses plans beyond its 32 MiB
     # static scratch buffer before any HIP call
-    assert lib.cek_gemm_fp8_a8w8_workspace_size(768, 3072, 24576) > (32 << 20)
-    assert lib.cek_gemm_fp8_a8w8_noalloc(p, p, p, p, p, 768, 3072, 24576, 0, None) == cabi.CEK_ERR_SCRATCH
+    assert lib.cek_gemm_fp8_a8w8_workspace_size(768, 6144, 24576) > (32 << 20)
+    assert lib.cek_gemm_fp8_a8w8_noalloc(p, p, p, p, p, 768, 6144, 24576, 0, None) == cabi.CEK_ERR_SCRATCH
     assert b"scratch" in lib.cek_error_string(cabi.CEK_ERR_SCRATCH)
     # empty problems are no-ops that succeed without touching memory
     assert lib.cek_gemv_fp8_pern(None, None, None, None, 0, 8, 64, 0, 0, 2, None) == cabi.CEK_OK

@@ -197,6 +197,38 @@ def test_a8w8_split_k(ops, dev, M, K, N):
     assert_close_fp(yb.cpu(), ref, f"a8w8 split bf16 M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("M,K,N,parts", [(225, 4096, 339, 4), (516, 2048, 7302, 0), (710, 2048, 5403, 0),
+                                         (516, 16384, 3293, 2), (516, 8192, 1605, 4), (225, 16384, 339, 8),
+                                         (3232, 16384, 550, 2), (1583, 8192, 550, 4), (419, 16384, 339, 8)])
+def test_a8w8_round_model_tiles(ops, dev, M, K, N, parts):
+    """Shapes (ragged in M and N) on which the round-model plan for M >= 128
+    picks each 8-wave, 3-slot tile (128 x 128, 128 x 256, 256 x 128) unsplit
+    or split in 2, 4 or 8 parts (`parts`, 0: unsplit; the op allocates the
+    workspace), and without a workspace (the bare C-ABI call) the unsplit
+    plan, which at 225 x 339 is the 8-wave 128 x 128 tile.  Both against the
+    CPU oracle; two calls of the op agree bit for bit."""
+    from esimd_learning_amd import cabi
+    _say(f"a8w8 round-model tiles M={M} K={K} N={N} parts={parts}")
+    lib = cabi.load()
+    need = lib.cek_gemm_fp8_a8w8_workspace_size(M, N, K)
+    assert need == (parts * M * N * 4 if parts else 0), need
+    q, sa, W8, sb = _a8w8_inputs_config4(M, K, N, seed=M + K + N)
+    qd, Wd, sad, sbd = q.to(dev), W8.to(dev), sa.to(dev), sb.to(dev)
+    y1 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    y2 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y1)
+    ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y2)
+    y3 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    st = cabi.stream_ptr(torch.cuda.current_stream())
+    assert lib.cek_gemm_fp8_a8w8(qd.data_ptr(), sad.data_ptr(), Wd.data_ptr(), sbd.data_ptr(), y3.data_ptr(),
+                                 M, N, K, 1, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    ref = ogemm.gemm_a8w8(q, sa, W8, sb)
+    assert_close_fp(y1.cpu(), ref, f"a8w8 op M={M} K={K} N={N}")
+    assert_close_fp(y3.cpu(), ref, f"a8w8 unsplit bf16 M={M} K={K} N={N}")
+
+
 def test_a8w8_split_k_graph_replays(ops, dev):
     """The split-K op captured in a HIP graph (its workspace then comes from
     the graph's memory pool): three replays, with eager work on the same

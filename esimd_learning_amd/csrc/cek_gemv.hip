@@ -577,8 +577,19 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
 // TAIL (with TP, see gemv_tail): after the tile's store, the last workgroup
 // to finish (of all, or of one head's tiles) runs a fused epilogue on the
 // output: add+RMSNorm with a residual, or QK RMSNorm + RoPE per head.
+//
+// ROT: tile t (16-row block index t16 of its first row) reads its K chunks
+// in the order t16 mod STEPS, t16 mod STEPS + 1, ... (wrapping), so that
+// tiles streaming at the same time read different 1 KB columns of their rows
+// instead of all the same one (HBM channels then share the load: M = 4,
+// K = 3072, N = 12288: 9.2 -> 8.4 us; K = 4096, N = 4096: 6.5 -> 5.8 us).
+// It changes the order of the K sums of every tile, so all forms that must
+// agree bit for bit (plain, GLU, NORM, TAIL, multi-matrix) take it under the
+// same rule: fp16 / bf16 activations and M <= 4 (launch_lds_steps).  The
+// runtime chunk offsets cost VALU address arithmetic, which made the
+// multi-tile and M > 4 forms 1-5% slower with it.
 template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
-          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0>
+          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0, bool ROT = false>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M, NormArgs na) {
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
@@ -616,6 +627,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   const int nw = sr.group * ROWS * (GLU ? 1 : TPW);  // first row of the workgroup
   // first row of tile t
   auto tile_row = [&](int t) { return GLU ? nw + t * half : nw + ROWS * t; };
+  // K chunk (1 KB of each row) that stage i reads
+  auto kchunk = [&](int i) {
+    const int s = i % STEPS;
+    if constexpr (!ROT) {
+      return s;
+    } else {
+      const int r = (tile_row(i / STEPS) >> 4) % STEPS;
+      return s + r >= STEPS ? s + r - STEPS : s + r;
+    }
+  };
   uint32_t sc_n[NT];
   float sc_m[MB][4];
   lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 && !NORM ? sg.xs : nullptr);
@@ -648,7 +669,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   u4 wr[S][LW];
   u4 xr[S][MX > 0 ? XU : QN][MX > 0 ? 1 : MB][MX > 0 ? 1 : 2];
   auto issue = [&](int i, u4 (&ws)[LW], u4 (&xs)[MX > 0 ? XU : QN][MX > 0 ? 1 : MB][MX > 0 ? 1 : 2]) {
-    const int k0 = (i % STEPS) << 10;
+    const int k0 = kchunk(i) << 10;
 #pragma unroll
     for (int j = 0; j < LW; ++j) ws[j] = load_u4_stream(wrow(i / STEPS, j) + k0);  // 1 KB of one row per instruction
     asm volatile("" ::: "memory");  // same issue order in every step (weights, then activations)
@@ -823,7 +844,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     // wave finished before the barrier of step i - 1).  Lane l's unit lands
     // at slot l, i.e. unit v of row r at slot v ^ (r & 15).
     uint8_t* sw = smem + (i & 1) * STAGE;
-    uint8_t* sx = smem + 2 * STAGE + (NORM ? i % STEPS : i & 1) * XSTAGE;
+    uint8_t* sx = smem + 2 * STAGE + (NORM ? kchunk(i) : i & 1) * XSTAGE;
 #pragma unroll
     for (int jj = 0; jj < LW; ++jj) *reinterpret_cast<u4*>(sw + (wave + 4 * jj) * 1024 + 16 * lane) = wr[i % S][jj];
     if constexpr (MX > 0 && !NORM) {
@@ -954,20 +975,20 @@ template <typename T, typename TO, int FMT, bool XF8, int S>
 static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int N, hipStream_t st) {
 #define CEK_LDS(NT, MB, D) \
   gemv_lds_kernel<T, TO, FMT, XF8, NT, MB, D, S><<<dim3(seg_grid(sg, 16 * (NT))), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
-#define CEK_LDS_T(NT, D, MX, TPW)                                                                          \
-  gemv_lds_kernel<T, TO, FMT, XF8, NT, 1, D, S, MX, TPW><<<dim3(seg_grid(sg, 16 * (NT) * (TPW))), 256, 0, st>>>( \
-      x, sg, skind, M, NormArgs{})
+#define CEK_LDS_T(NT, D, MX, TPW, ROT)                                                                         \
+  gemv_lds_kernel<T, TO, FMT, XF8, NT, 1, D, S, MX, TPW, false, false, TAIL_NONE, 0, ROT>                     \
+      <<<dim3(seg_grid(sg, 16 * (NT) * (TPW))), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
   constexpr bool SHORT = S >= 3 && S <= 5;
   constexpr bool MULTI = S == 4 || S == 5;  // multi-tile workgroups (K = 4096, 5120)
-#define CEK_LDS_TPW(NT, D, MX)                       \
-  do {                                               \
-    if constexpr (MULTI) {                           \
-      if (tpw == 4) CEK_LDS_T(NT, D, MX, 4);         \
-      else if (tpw == 2) CEK_LDS_T(NT, D, MX, 2);    \
-      else CEK_LDS_T(NT, D, MX, 1);                  \
-    } else {                                         \
-      CEK_LDS_T(NT, D, MX, 1);                       \
-    }                                                \
+#define CEK_LDS_TPW(NT, D, MX, ROT)                       \
+  do {                                                    \
+    if constexpr (MULTI) {                                \
+      if (tpw == 4) CEK_LDS_T(NT, D, MX, 4, ROT);         \
+      else if (tpw == 2) CEK_LDS_T(NT, D, MX, 2, ROT);    \
+      else CEK_LDS_T(NT, D, MX, 1, ROT);                  \
+    } else {                                              \
+      CEK_LDS_T(NT, D, MX, 1, ROT);                       \
+    }                                                     \
   } while (0)
   // K = 4096 or 5120 (4-5 stages per 16-row tile): consecutive tiles per
   // workgroup, as many as keep >= 224 workgroups (measured on MI355X: 4
@@ -980,8 +1001,8 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
     // of just the M rows); for long K only up to 12288 rows (5-20% faster
     // there, slower for wider matrices).
     if (M <= 8 && (SHORT || N <= 12288)) {
-      if (M <= 4) CEK_LDS_TPW(1, (S >= 3 ? 3 : 2), 4);
-      else CEK_LDS_TPW(1, 2, 8);
+      if (M <= 4) CEK_LDS_TPW(1, (S >= 3 ? 3 : 2), 4, true);
+      else CEK_LDS_TPW(1, 2, 8, false);
       return true;
     }
   }
@@ -990,7 +1011,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
     // activation rows staged through LDS (measured on MI355X at N = 4096:
     // 19.7 -> 18.5 us; at K = 4096 staging 9-16 rows was 3-33% slower)
     if (M > 8 && M <= 16 && N <= 4096) {
-      CEK_LDS_T(1, 2, 16, 1);
+      CEK_LDS_T(1, 2, 16, 1, false);
       return true;
     }
   }
@@ -998,10 +1019,14 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
     if constexpr (SHORT) {
       // Two 16-row tiles per workgroup halve the activation re-reads once
       // there are enough rows to keep >= 192 workgroups.
+      // (fp16 / bf16 M <= 4 took the staged form above)
       if (N >= 6144 && (XF8 ? M > 8 : M >= 8)) CEK_LDS(2, 1, 2);
-      else CEK_LDS_TPW(1, 3, 0);
+      else CEK_LDS_TPW(1, 3, 0, false);
     } else if constexpr (XF8 && S >= 3) {
       CEK_LDS(1, 1, 3);
+    } else if constexpr (!XF8) {
+      if (M <= 4) CEK_LDS_T(1, 2, 0, 1, true);  // fp16 / bf16 M <= 4 rotate in every form
+      else CEK_LDS(1, 1, 2);
     } else {
       CEK_LDS(1, 1, 2);
     }
@@ -1046,19 +1071,20 @@ static void launch_glu_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   const int grid = (d + 15) / 16;
   sg.gstart[0] = 0;
   for (int i = 1; i <= MAX_SEGS; ++i) sg.gstart[i] = grid;
-#define CEK_GLU(D, MX) \
-  gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, 2, true><<<dim3(grid), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
+#define CEK_GLU(D, MX, ROT)                                                                   \
+  gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, 2, true, false, TAIL_NONE, 0, ROT><<<dim3(grid), 256, 0, st>>>( \
+      x, sg, skind, M, NormArgs{})
   if constexpr (!XF8) {
     if (M <= 4) {
-      CEK_GLU(3, 4);
+      CEK_GLU(3, 4, true);
       return;
     }
     if (M <= 8) {
-      CEK_GLU(2, 8);
+      CEK_GLU(2, 8, false);
       return;
     }
   }
-  CEK_GLU(3, 0);
+  CEK_GLU(3, 0, false);
 #undef CEK_GLU
 }
 
@@ -1083,19 +1109,19 @@ static void launch_norm_steps(GemvSegs& sg, const NormArgs& na, int skind, int M
     const int grid = (N / 2 + 15) / 16;
     sg.gstart[0] = 0;
     for (int i = 1; i <= MAX_SEGS; ++i) sg.gstart[i] = grid;
-    gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 2, true, true><<<dim3(grid), 256, 0, st>>>(
-        nullptr, sg, skind, M, na);
+    gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 2, true, true, TAIL_NONE, 0, !XF8>
+        <<<dim3(grid), 256, 0, st>>>(nullptr, sg, skind, M, na);
     return;
   }
   if constexpr (S == 4 || S == 5) {
     if ((N + 15) / 16 >= 384) {
-      gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 2, false, true><<<dim3(seg_grid(sg, 32)), 256, 0, st>>>(
-          nullptr, sg, skind, M, na);
+      gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 2, false, true, TAIL_NONE, 0, !XF8>
+          <<<dim3(seg_grid(sg, 32)), 256, 0, st>>>(nullptr, sg, skind, M, na);
       return;
     }
   }
-  gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 1, false, true><<<dim3(seg_grid(sg, 16)), 256, 0, st>>>(
-      nullptr, sg, skind, M, na);
+  gemv_lds_kernel<T, TO, CEK_E4M3, XF8, 1, 1, 3, S, MX, 1, false, true, TAIL_NONE, 0, !XF8>
+      <<<dim3(seg_grid(sg, 16)), 256, 0, st>>>(nullptr, sg, skind, M, na);
 }
 
 template <typename T, typename TO, bool XF8>
@@ -1353,9 +1379,9 @@ int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* s
 template <typename T, int TAIL, int TP>
 static void launch_tail_t(const void* x, GemvSegs& sg, int skind, int M, int K, const NormArgs& na, hipStream_t st) {
   const dim3 grid((unsigned)seg_grid(sg, 16));
-#define CEK_TAIL(S)                                                                                                 \
-  gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, 3, S, 4, 1, false, false, TAIL, TP><<<grid, 256, 0, st>>>(x, sg, skind, \
-                                                                                                         M, na)
+#define CEK_TAIL(S)                                                                                  \
+  gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, 3, S, 4, 1, false, false, TAIL, TP, true><<<grid, 256, 0, st>>>( \
+      x, sg, skind, M, na)
   if (K == 3072) CEK_TAIL(3);
   else if (K == 4096) CEK_TAIL(4);
   else CEK_TAIL(5);

@@ -432,26 +432,39 @@ LAYER_VARIANTS = {"us_per_step": dict(),
                   "norm_fused_us_per_step": dict(fuse_norm=True)}
 
 
-def bench_layer(torch, steps, M=4, rounds=5):
-    """one Gemma-style decoder-layer decode step, HIP-graph
-    replayed.  Every variant of LAYER_VARIANTS is captured first, then the
-    variants are timed in turn, `rounds` times round-robin (so that all see
-    the same clock state), and each reports its median round; plus the read
-    probe over the step's four weight matrices (the one-pass floor)."""
+LAYERS = 8  # decoder layers per captured forward, each with its own weight copy (2.2 GB: read from HBM)
+
+
+def bench_layer(torch, steps, M=4, rounds=5, layers=LAYERS):
+    """the Gemma-style decoder-layer decode step, as a
+    multi-layer model runs it: `layers` chained layers (each layer's output
+    the next one's hidden state, each with its own copy of the weights, so
+    that every step reads its 277 MB from HBM) captured in one HIP graph; a
+    step is the graph's time / `layers`.  Every variant of LAYER_VARIANTS is
+    captured first, then the variants are timed in turn, `rounds` times
+    round-robin (so that all see the same clock state), and each reports its
+    median round.  Also: the default step captured alone and its graph
+    replayed back to back (`single_step_graphs_us`: each replay adds the
+    graph-to-graph launch gap), and the read probe over the layers' weight
+    matrices in one graph the same way (the one-pass floor of a step's
+    GEMVs)."""
     from esimd_learning_amd import synthetic
-    from esimd_learning_amd.layer import GemmaDecodeLayer
+    from esimd_learning_amd.layer import GemmaDecodeLayer, capture_forward, forward
     dev = "cuda:0"
     p = synthetic.gemma_layer(seed=10)
+    p0 = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in p.items()}
+    psets = [p0] + [{k: (v.clone() if torch.is_tensor(v) else v) for k, v in p0.items()} for _ in range(layers - 1)]
     h = synthetic.activations(M, p["hidden"], seed=20).to(dev)
     r = synthetic.activations(M, p["hidden"], seed=21).to(dev)
     pos = synthetic.positions(M, seed=22).to(dev)
-    graphs, layers = {}, {}
+    reps = max(1, -(-steps // layers))
+    graphs, stacks = {}, {}
     for key, kw in LAYER_VARIANTS.items():
-        layer = GemmaDecodeLayer(p, M, dev, **kw)
-        layer.step(h, r, pos)
+        stack = [GemmaDecodeLayer(ps, M, dev, **kw) for ps in psets]
+        forward(stack, h, r, pos)
         torch.cuda.synchronize()
-        graphs[key] = layer.capture(h, r, pos)
-        layers[key] = layer
+        graphs[key] = capture_forward(stack, h, r, pos)
+        stacks[key] = stack
     t_end = time.perf_counter() + WARM_S
     while time.perf_counter() < t_end:
         for g in graphs.values():
@@ -462,24 +475,36 @@ def bench_layer(torch, steps, M=4, rounds=5):
         for key, g in graphs.items():
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            for _ in range(steps):
+            for _ in range(reps):
                 g.replay()
             e1.record()
             torch.cuda.synchronize()
-            times[key].append(e0.elapsed_time(e1) * 1e3 / steps)
+            times[key].append(e0.elapsed_time(e1) * 1e3 / (reps * layers))
     med = {key: sorted(v)[len(v) // 2] for key, v in times.items()}
-    layer = layers["us_per_step"]
-    wb = layer.weight_bytes()
-    # the four weight matrices read once each by cek_hbm_read_probe, captured
-    # and replayed the same way: the one-pass read floor of a step's GEMVs
+    # the default step alone in a graph, replayed back to back
+    one = stacks["us_per_step"][0]
+    g1 = one.capture(h, r, pos)
+    for _ in range(10):
+        g1.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g1.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    single_us = e0.elapsed_time(e1) * 1e3 / steps
+    wb = one.weight_bytes()
+    # the layers' weight matrices read once each by cek_hbm_read_probe, in
+    # one graph the same way: the one-pass read floor of a step's GEMVs
     from esimd_learning_amd import cabi
     lib = cabi.load()
-    mats = [layer.Wqkv, layer.Wo, layer.Wgu, layer.Wd]
+    mats = [w for ly in stacks["us_per_step"] for w in (ly.Wqkv, ly.Wo, ly.Wgu, ly.Wd)]
     stream = torch.cuda.Stream()
     pfns = [(lambda w=w: cabi.check(lib.cek_hbm_read_probe(w.data_ptr(), w.numel(), None, cabi.stream_ptr(stream))))
-            for w in mats] * steps
+            for w in mats] * reps
     _, pev_ms, _ = time_graph(pfns, torch, stream, warm_s=WARM_S / 2)
-    floor_us = pev_ms * 1e3 / steps
+    floor_us = pev_ms * 1e3 / (reps * layers)
     us = med["us_per_step"]
     out = {"config": "Gemma-style decoder layer decode step, M=4, hidden 3072, 16q/16kv x 256, MLP 24576 "
                      "(attention stood in by a copy of q)",
@@ -488,8 +513,9 @@ def bench_layer(torch, steps, M=4, rounds=5):
     for key in LAYER_VARIANTS:
         if key != "us_per_step":
             out[key] = round(med[key], 2)
-    out["timing"] = (f"one HIP graph per variant, {steps} replays back to back, variants timed round-robin "
-                     f"{rounds} times, median round")
+    out["single_step_graphs_us"] = round(single_us, 2)
+    out["timing"] = (f"{layers} chained layers (own weight copies) per HIP graph, {reps} replays back to back, "
+                     f"per step = time / {reps * layers}; variants timed round-robin {rounds} times, median round")
     return out
 
 

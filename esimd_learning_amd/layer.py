@@ -163,3 +163,26 @@ class GemmaDecodeLayer:
     def replay(self):
         self.graph.replay()
         return self.out
+
+
+def forward(layers, hidden, residual, positions):
+    """A decode forward over `layers` in sequence: each layer's output buffer
+    is the next layer's hidden state (which that layer's first norm
+    overwrites), and the residual stream is updated in place by every layer.
+    Returns the last layer's output buffer."""
+    h = hidden
+    for layer in layers:
+        h = layer.step(h, residual, positions)
+    return h
+
+
+def capture_forward(layers, hidden, residual, positions, stream=None):
+    """forward() over `layers` captured in one HIP graph, as a serving loop
+    captures a model's whole decode step (no launch gap between layers)."""
+    s = stream or torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        forward(layers, hidden, residual, positions)
+    torch.cuda.current_stream().wait_stream(s)
+    return g

@@ -114,3 +114,34 @@ def test_decoder_step_fused_equals_unfused(ops, dev, act_fp8):
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+def test_forward_chains_layers(ops, dev):
+    """forward() over two layers (different weights) equals the two steps run
+    by hand, the first layer's output feeding the second; capture_forward()
+    replays equal the eager forward bit for bit (inputs refreshed before each
+    replay, eager work between replays)."""
+    from esimd_learning_amd.layer import capture_forward, forward
+    M, dims = 4, SMALL
+    stack = [GemmaDecodeLayer(synthetic.gemma_layer(seed=s, **dims), M, dev) for s in (14, 15)]
+    h0 = synthetic.activations(M, dims["hidden"], seed=60).to(dev)
+    r0 = synthetic.activations(M, dims["hidden"], seed=61).to(dev)
+    pos = synthetic.positions(M, seed=62).to(dev)
+    h, r = h0.clone(), r0.clone()
+    ref = stack[1].step(stack[0].step(h, r, pos), r, pos).clone()
+    ref_r = r.clone()
+    h, r = h0.clone(), r0.clone()
+    out = forward(stack, h, r, pos)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == stack[1].out.data_ptr()
+    assert torch.equal(out, ref) and torch.equal(r, ref_r)
+    hb, rb = h0.clone(), r0.clone()
+    g = capture_forward(stack, hb, rb, pos)
+    for _ in range(3):
+        hb.copy_(h0)
+        rb.copy_(r0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(stack[1].out, ref)
+        assert torch.equal(rb, ref_r)
+        torch.randn(1000, device=dev).sum().item()

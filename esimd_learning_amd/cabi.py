@@ -28,6 +28,8 @@ SIGNATURES = {
     "cek_gemv_fp8_pern_multi": (_i, [_p, _i, _p, _p, _p, _p, _i64, _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_pert_multi": (_i, [_p, _i, _p, _p, _p, _p, _i64, _i64, _i, _i, _p]),
     "cek_gemm_fp8_pert": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _p]),
+    "cek_gemm_fp8_pert_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "cek_gemm_fp8_pert_ws": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _p, _i64, _p]),
     "cek_fused_add_rms_norm": (_i, [_p, _p, _p, _i64, _i64, _f, _i, _p]),
     "cek_fused_add_rms_norm_quant_fp8": (_i, [_p, _p, _p, _i64, _i64, _f, _i, _p, _p, _p]),
     "cek_per_token_quant_fp8": (_i, [_p, _i64, _i64, _i, _p, _p, _p]),

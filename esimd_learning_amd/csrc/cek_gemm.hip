@@ -605,6 +605,55 @@ __global__ __launch_bounds__(256) void gemm_splitk_finalize(const float* __restr
   }
 }
 
+// The same for the w8a16 split K: Y[m, n] = Out(w_scale[n] * (P[0][m, n] +
+// P[1][m, n] + ...)), the weight scale of kind skind (ScaleKind; per channel
+// or one value), the parts added in order.
+template <typename T, int SPLIT>
+__global__ __launch_bounds__(256) void gemm_splitk_finalize_w(const float* __restrict__ P, const void* __restrict__ ws,
+                                                              int skind, uint16_t* __restrict__ Y, int M, int N) {
+  const size_t total = (size_t)M * N;
+  const int n = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
+  if (n >= N) return;
+  const bool vec = (N & 7) == 0 && ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(Y)) & 15) == 0;
+  float cs[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) cs[e] = load_scale(ws, skind, min(n + e, N - 1));
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const size_t i = (size_t)m * N + n;
+    if (vec) {
+      f4 s0 = *reinterpret_cast<const f4*>(P + i), s1 = *reinterpret_cast<const f4*>(P + i + 4);
+#pragma unroll
+      for (int q = 1; q < SPLIT; ++q) {
+        const f4 p0 = *reinterpret_cast<const f4*>(P + q * total + i);
+        const f4 p1 = *reinterpret_cast<const f4*>(P + q * total + i + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s0[e] += p0[e];
+          s1[e] += p1[e];
+        }
+      }
+      u4 o;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t lo0 = T::from_f32(f32_round(s0[2 * e] * cs[2 * e]));
+        const uint32_t hi0 = T::from_f32(f32_round(s0[2 * e + 1] * cs[2 * e + 1]));
+        const uint32_t lo1 = T::from_f32(f32_round(s1[2 * e] * cs[4 + 2 * e]));
+        const uint32_t hi1 = T::from_f32(f32_round(s1[2 * e + 1] * cs[4 + 2 * e + 1]));
+        o[e] = lo0 | (hi0 << 16);
+        o[2 + e] = lo1 | (hi1 << 16);
+      }
+      *reinterpret_cast<u4*>(Y + i) = o;
+    } else {
+      for (int e = 0; e < 8 && n + e < N; ++e) {
+        float s = P[i + e];
+#pragma unroll
+        for (int q = 1; q < SPLIT; ++q) s += P[q * total + i + e];
+        Y[i + e] = T::from_f32(f32_round(s * cs[e]));
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // w8a16, LDS-tiled: block tile BM x BN, K step 64, four waves 2 x 2.
 // LDS stage: A as BM rows of 128 bytes (64 activations, eight 16-byte chunks,
@@ -730,12 +779,13 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
 // of FN MFMA block updates (two 16 x 16 x 32 MFMAs each); group i + 1's A
 // fragment is read while group i's MFMAs run, and the step's one barrier
 // sits before the last group, after which the loader waves (the first LW)
-// issue the loads of step k + 2 into the stage step k used and every wave
+// issue the loads of step k + RING into the stage step k used and every wave
 // reads and decodes step k + 1's B fragments and first A fragment behind the
-// last group's MFMAs.  Loader waves as in gemm_a8w8_pipe_kernel.
+// last group's MFMAs.  Loader waves and ring slots (RING stages, loads
+// RING - 1 steps ahead) as in gemm_a8w8_pipe_kernel.
 // Requires K % 64 == 0, FM even, 16-byte aligned X and W.
 // ---------------------------------------------------------------------------
-template <typename T, int FMT, int BM, int BN, int WM, int WN, int LW>
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int LW, int RING = 2>
 struct W8Pipe {
   static constexpr int BK = 64;
   static constexpr int NW = WM * WN;
@@ -758,19 +808,23 @@ struct W8Pipe {
     for (int j = 0; j < FN; ++j) decode16<T, FMT>(*reinterpret_cast<const u4*>(sB + j * 16 * 64 + pb * 16), b[j][0], b[j][1]);
   }
 
-  __device__ static __forceinline__ void step(int kt, int KT, uint8_t* smem, bool loader, int wave, int wm, int wn, int r16,
-                                              int pa0, int pa1, int pb, const uint8_t* Xb, const uint8_t* W,
-                                              const uint32_t (&ga)[ACH], const uint32_t (&gb)[BCH], f4 (&acc)[FM][FN], u4 (&a)[2][2],
-                                              const u4 (&bc)[FN][2], u4 (&bn)[FN][2]) {
-    const uint8_t* sA = smem + (kt & 1) * STAGE + (wm * TM + r16) * 128;
+  // step kt from ring slot c (the next step's slot cn)
+  __device__ static __forceinline__ void step(int kt, int KT, int c, int cn, uint8_t* smem, bool loader, int wave, int wm,
+                                              int wn, int r16, int pa0, int pa1, int pb, const uint8_t* Xb,
+                                              const uint8_t* W, const uint32_t (&ga)[ACH], const uint32_t (&gb)[BCH],
+                                              f4 (&acc)[FM][FN], u4 (&a)[2][2], const u4 (&bc)[FN][2],
+                                              u4 (&bn)[FN][2]) {
+    const uint8_t* sA = smem + c * STAGE + (wm * TM + r16) * 128;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       if (i + 1 < FM) {
         read_a(sA + (i + 1) * 16 * 128, pa0, pa1, a[(i + 1) & 1]);
       } else if (kt + 1 < KT) {
-        barrier_vmcnt<0>();  // step k + 1 has landed; step k's stage is free
-        if (loader && kt + 2 < KT) w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, kt & 1, (kt + 2) * BK, wave, Xb, W, ga, gb);
-        const uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
+        // step k + 1 has landed (later steps' loads may fly); slot c is free
+        barrier_upto<RING - 2, ACH + BCH>(KT - 2 - kt);
+        if (loader && kt + RING < KT)
+          w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, c, (kt + RING) * BK, wave, Xb, W, ga, gb);
+        const uint8_t* nxt = smem + cn * STAGE;
         read_b(nxt + BM * 128 + (wn * TN + r16) * 64, pb, bn);
         read_a(nxt + (wm * TM + r16) * 128, pa0, pa1, a[0]);
       }
@@ -784,20 +838,27 @@ struct W8Pipe {
   }
 };
 
-template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN, int LW>
+// SPLIT > 1 (split K): workgroup b computes tile b / SPLIT over the K range
+// of part b % SPLIT ((K / SPLIT) % 64 == 0) and stores its unscaled fp32
+// sums to part P[b % SPLIT] of the [SPLIT][M][N] workspace P;
+// gemm_splitk_finalize_w then adds the parts in order and scales.
+template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN, int LW, int SPLIT = 1, int RING = 2>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ scale, int skind,
-    uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
-  using P = W8Pipe<T, FMT, BM, BN, WM, WN, LW>;
+    uint16_t* __restrict__ Y, float* __restrict__ Pw, int M, int N, int K, int tiles_m, int tiles_n) {
+  using P = W8Pipe<T, FMT, BM, BN, WM, WN, LW, RING>;
   constexpr int BK = P::BK, NW = P::NW, TM = P::TM, TN = P::TN, FM = P::FM, FN = P::FN, STAGE = P::STAGE;
   constexpr int ACH = P::ACH, BCH = P::BCH;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2];
+  static_assert(RING >= 2 && RING <= 4, "ring slots");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING * STAGE > BM * BN * 2 ? RING * STAGE : BM * BN * 2];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const bool loader = wave < LW;
+  const int part = SPLIT > 1 ? (int)blockIdx.x % SPLIT : 0;
+  const uint32_t kpart = (uint32_t)(part * (K / SPLIT));  // first K value of this part
   int tm, tn;
-  tile_of<BM, BN, 8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_of<BM, BN, 8>(SPLIT > 1 ? blockIdx.x / SPLIT : blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const uint8_t* Xb = reinterpret_cast<const uint8_t*>(X);
 
@@ -808,12 +869,12 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
     const int row = (wave + LW * i) * 8 + (lane >> 3);
-    ga[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ swzA(row)) * 16);
+    ga[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K * 2u + 2u * kpart + (uint32_t)(((lane & 7) ^ swzA(row)) * 16);
   }
 #pragma unroll
   for (int i = 0; i < BCH; ++i) {
     const int row = (wave + LW * i) * 16 + (lane >> 2);
-    gb[i] = (uint32_t)min(n0 + row, N - 1) * (uint32_t)K + (uint32_t)(((lane & 3) ^ swzB(row)) * 16);
+    gb[i] = (uint32_t)min(n0 + row, N - 1) * (uint32_t)K + kpart + (uint32_t)(((lane & 3) ^ swzB(row)) * 16);
   }
   const int r16 = lane & 15, g = lane >> 4;
   const int pa0 = (2 * g) ^ swzA(r16), pa1 = (2 * g + 1) ^ swzA(r16), pb = g ^ swzB(r16);
@@ -824,29 +885,52 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int KT = K / BK;
+  const int KT = K / BK / SPLIT;
+  // prologue: steps 0 .. RING - 1 into their slots, then wait for step 0
   if (loader) {
-    w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, 0, 0, wave, Xb, W, ga, gb);
-    if (KT > 1) w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, 1, BK, wave, Xb, W, ga, gb);
+#pragma unroll
+    for (int s = 0; s < RING; ++s)
+      if (s == 0 || s < KT) w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, s, s * BK, wave, Xb, W, ga, gb);
   }
-  if (KT > 1) {
-    barrier_vmcnt<ACH + BCH>();
-  } else {
-    barrier_vmcnt<0>();
-  }
+  barrier_upto<RING - 1, ACH + BCH>(KT - 1);
   u4 a[2][2], b0[FN][2], b1[FN][2];
   P::read_b(smem + BM * 128 + (wn * TN + r16) * 64, pb, b0);
   P::read_a(smem + (wm * TM + r16) * 128, pa0, pa1, a[0]);
-  int kt = 0;
+  int kt = 0, c = 0;
+  auto nxt = [](int v) { return v + 1 == RING ? 0 : v + 1; };
   for (; kt + 1 < KT; kt += 2) {
-    P::step(kt, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0, b1);
-    P::step(kt + 1, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b1, b0);
+    const int c1 = RING == 2 ? 1 : nxt(c), c2 = RING == 2 ? 0 : nxt(c1);
+    P::step(kt, KT, RING == 2 ? 0 : c, c1, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0,
+            b1);
+    P::step(kt + 1, KT, c1, c2, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b1, b0);
+    c = c2;
   }
-  if (kt < KT) P::step(kt, KT, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0, b1);
+  if (kt < KT)
+    P::step(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W,
+            ga, gb, acc, a, b0, b1);
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
-  store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, 1.f, Y, 0, 0, scale,
-                                         skind);
+  if constexpr (SPLIT > 1) {
+    // fp32 partial sums in D layout: lane l holds column l & 15, rows
+    // 4 (l >> 4) + v of each 16 x 16 block (rows and columns past the
+    // matrix are clamped copies, not stored)
+    float* Pp = Pw + (size_t)part * M * N;
+    const int g4 = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * TN + j * 16 + r16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = m0 + wm * TM + i * 16 + g4 + v;
+          if (m < M && n < N) Pp[(size_t)m * N + n] = acc[i][j][v];
+        }
+      }
+  } else {
+    store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, 1.f, Y, 0, 0,
+                                           scale, skind);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -990,8 +1074,63 @@ namespace cek {
 // M <= 16 the GEMV kernels, N <= 16 the activation-streaming kernel,
 // 16 < M <= 32 the LDS-staged GEMV where it has an instantiation, else the
 // tiled MFMA GEMM (or the generic kernels for unaligned shapes).
+// Tiled w8a16 configurations of the round model (M, N >= 128, matrices
+// below 4 GB): the 8-wave register-pipelined kernel (2 x 4 waves, four
+// loader waves) with its ring slots, and t0 / step of the round model (us
+// per round: t0 + step per 64-deep K step of one workgroup), fitted to the
+// nine config-4 shapes with operands streamed from HBM (MI355X):
+//  0  256 x 128, 3 slots;   1  256 x 192, 3 slots;   2  256 x 256, 2 slots;
+//  3  128 x 256, 3 slots;   4  128 x 128, 3 slots (split K only).
+// Unsplit: 0-3; split in 2, 4 or 8 parts (K values per part >= 1024): 0 and
+// 3, and 4 in 4 or 8 parts.  On the nine config-4 shapes (HBM and
+// cache-resident) and ten others (M = 128 .. 3000) the plan's pick measured
+// within 7% of the fastest of sixteen forms (M = 512, K = 14336: 171 -> 68 us
+// split in 4; M = 512, K = 4096, N = 6144: 52 -> 36 us).
+struct W8Opt { int bm, bn; double t0, step; };
+constexpr W8Opt kW8Opts[5] = {{256, 128, 0.49, 0.972}, {256, 192, 6.84, 1.166}, {256, 256, 0.0, 1.595},
+                              {128, 256, 2.05, 0.904}, {128, 128, 0.0, 0.491}};
+struct W8Plan { int cfg, split; };
+
+static bool w8_off32(int64_t M, int64_t N, int64_t K) {
+  return (uint64_t)M * (uint64_t)K * 2 < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
+}
+
+// cfg -1: the shape is outside the round model (the score-based choice of
+// launch_w8a16 applies)
+static W8Plan plan_w8a16(int64_t M, int64_t N, int64_t K, bool allow_split) {
+  W8Plan best{-1, 1};
+  if (M < 128 || N < 128 || K % 64 != 0 || !w8_off32(M, N, K)) return best;
+  double tbest = -1.0;
+  for (int c = 0; c < 5; ++c) {
+    const W8Opt& o = kW8Opts[c];
+    if (M < o.bm || N < o.bn) continue;
+    for (int sp : {1, 2, 4, 8}) {
+      const bool ok = sp == 1 ? c != 4 : (allow_split && (c == 0 || c == 3 || (c == 4 && sp >= 4)));
+      if (!ok || (K / 64) % sp || (sp > 1 && K / sp < 1024)) continue;
+      const int64_t units = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn) * sp;
+      const int64_t full = units / 256;
+      const double f = (double)(units - full * 256) / 256.0;
+      const double rounds = (double)full + (f > 0.0 ? 0.6 + 0.4 * f : 0.0);
+      double t = rounds * (o.t0 + (double)(K / 64 / sp) * o.step);
+      if (sp > 1) t += ((double)sp * M * N * 4.0 + (double)M * N * 2.0) / 5.0e6 + 1.5;
+      if (tbest < 0 || t < tbest) {
+        tbest = t;
+        best = W8Plan{c, sp};
+      }
+    }
+  }
+  return best;
+}
+
+// Bytes of fp32 partials the w8a16 split-K plan needs for (M, N, K) (0: unsplit).
+static int64_t w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 32 || N <= 16 || M > 65535 * 64 || N > INT32_MAX || K > INT32_MAX || K <= 0) return 0;
+  const W8Plan p = plan_w8a16(M, N, K, true);
+  return p.split > 1 ? (int64_t)p.split * M * N * 4 : 0;
+}
+
 int launch_w8a16(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N, int64_t K,
-                 int io_dtype, int fp8_fmt, hipStream_t st) {
+                 int io_dtype, int fp8_fmt, float* ws, int64_t ws_bytes, hipStream_t st) {
   if (M < 0 || N < 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
   if (M == 0 || N == 0) return CEK_OK;
   if (!x || !w || !scale || !y) return CEK_ERR_INVALID;
@@ -1019,6 +1158,55 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
   if (K % 64 != 0 || !aligned(x, 16) || !aligned(w, 16) || M > 65535 * 64)
     return launch_gemv_generic(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, st);
   {
+    const int64_t need = w8a16_workspace_bytes(M, N, K);
+    const W8Plan plan = plan_w8a16(M, N, K, need > 0 && ws && ws_bytes >= need);
+    if (plan.cfg >= 0) {
+      const uint16_t* xp = static_cast<const uint16_t*>(x);
+      const uint8_t* wp = static_cast<const uint8_t*>(w);
+      uint16_t* yp = static_cast<uint16_t*>(y);
+#define CEK_W8P(TY, F, BM, BN, SP, RING)                                                                         \
+  do {                                                                                                          \
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                     \
+    gemm_w8a16_pipe_kernel<TY, F, BM, BN, 1, 2, 4, 4, SP, RING>                                                 \
+        <<<dim3((unsigned)(tm * tn * SP)), 512, 0, st>>>(xp, wp, scale, skind, yp, ws, M, N, K, tm, tn);         \
+    if (SP > 1)                                                                                                 \
+      gemm_splitk_finalize_w<TY, SP><<<dim3((unsigned)((N + 2047) / 2048), (unsigned)(M < 65535 ? M : 65535)),  \
+                                        256, 0, st>>>(ws, scale, skind, yp, (int)M, (int)N);                     \
+  } while (0)
+#define CEK_W8P_SPLITS(TY, F, BM, BN)                        \
+  do {                                                       \
+    if (plan.split == 2) CEK_W8P(TY, F, BM, BN, 2, 3);       \
+    else if (plan.split == 4) CEK_W8P(TY, F, BM, BN, 4, 3);  \
+    else CEK_W8P(TY, F, BM, BN, 8, 3);                       \
+  } while (0)
+#define CEK_W8P_ALL(TY, F)                                                 \
+  do {                                                                     \
+    if (plan.split > 1) {                                                  \
+      if (plan.cfg == 0) CEK_W8P_SPLITS(TY, F, 256, 128);                  \
+      else if (plan.cfg == 3) CEK_W8P_SPLITS(TY, F, 128, 256);             \
+      else if (plan.split == 4) CEK_W8P(TY, F, 128, 128, 4, 3);            \
+      else CEK_W8P(TY, F, 128, 128, 8, 3);                                 \
+    } else if (plan.cfg == 0) {                                            \
+      CEK_W8P(TY, F, 256, 128, 1, 3);                                      \
+    } else if (plan.cfg == 1) {                                            \
+      CEK_W8P(TY, F, 256, 192, 1, 3);                                      \
+    } else if (plan.cfg == 2) {                                            \
+      CEK_W8P(TY, F, 256, 256, 1, 2);                                      \
+    } else {                                                               \
+      CEK_W8P(TY, F, 128, 256, 1, 3);                                      \
+    }                                                                      \
+  } while (0)
+      if (io_dtype == CEK_F16 && fp8_fmt == CEK_E4M3) CEK_W8P_ALL(F16, CEK_E4M3);
+      else if (io_dtype == CEK_F16) CEK_W8P_ALL(F16, CEK_E5M2);
+      else if (fp8_fmt == CEK_E4M3) CEK_W8P_ALL(BF16, CEK_E4M3);
+      else CEK_W8P_ALL(BF16, CEK_E5M2);
+#undef CEK_W8P_ALL
+#undef CEK_W8P_SPLITS
+#undef CEK_W8P
+      return check_launch();
+    }
+  }
+  {
     // Tiles: 128 x 128 with 4 waves and two workgroups per CU, or the
     // register-pipelined 8-wave kernel (2 x 4 waves, four loader waves) at
     // 256 x 128, 256 x 192 or 256 x 256 -- each configuration's measured rate
@@ -1033,7 +1221,7 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
       return rate * (double)(M * N) / ((double)(rounds * slots) * bm * bn);
     };
     // the pipelined kernel addresses X and W by 32-bit byte offsets
-    const bool off32 = (uint64_t)M * (uint64_t)K * 2 < (1ull << 32) && (uint64_t)N * (uint64_t)K < (1ull << 32);
+    const bool off32 = w8_off32(M, N, K);
     const double s128 = score(128, 128, 1150, 512);
     const double s192 = off32 ? score(256, 192, 1250, 256) : -1.0;
     const double s256 = off32 ? score(256, 256, 1400, 256) : -1.0;
@@ -1056,7 +1244,7 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
   do {                                                                                                         \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                    \
     gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN, CEK_W8A16_LW>                                                         \
-        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, skind, yp, M, N, K, tm, tn);       \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, skind, yp, nullptr, M, N, K, tm, tn); \
   } while (0)
 #define CEK_W8A16(TY, F)                                          \
   do {                                                            \
@@ -1090,7 +1278,20 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
 extern "C" int cek_gemm_fp8_pert(const void* x, const void* w, const float* scale, void* y,
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, void* stream) {
-  return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
+  return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, nullptr, 0,
+                           (hipStream_t)stream);
+}
+
+extern "C" int64_t cek_gemm_fp8_pert_workspace_size(int64_t M, int64_t N, int64_t K) {
+  return cek::w8a16_workspace_bytes(M, N, K);
+}
+
+extern "C" int cek_gemm_fp8_pert_ws(const void* x, const void* w, const float* scale, void* y, int64_t M, int64_t N,
+                                    int64_t K, int io_dtype, int fp8_fmt, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !cek::aligned(workspace, 4)))) return CEK_ERR_INVALID;
+  return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt,
+                           static_cast<float*>(workspace), workspace_bytes, (hipStream_t)stream);
 }
 
 namespace cek {

@@ -42,7 +42,7 @@ namespace cek {
 
 
 int launch_w8a16(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N, int64_t K,
-                 int io_dtype, int fp8_fmt, hipStream_t st);  // cek_gemm.hip
+                 int io_dtype, int fp8_fmt, float* ws, int64_t ws_bytes, hipStream_t st);  // cek_gemm.hip
 
 constexpr int MAX_SEGS = 8;
 
@@ -1467,7 +1467,7 @@ extern "C" int cek_gemv_fp8_pern(const void* x, const void* w, const void* scale
                                  int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
   const int skind = cek::scale_kind(scale_dtype);
   if (skind < 0) return CEK_ERR_INVALID;
-  if (M > 16) return cek::launch_w8a16(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
+  if (M > 16) return cek::launch_w8a16(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, nullptr, 0, (hipStream_t)stream);
   return cek::launch_gemv(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 
@@ -1475,7 +1475,8 @@ extern "C" int cek_gemv_fp8_pert(const void* x, const void* w, const float* scal
                                  int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, void* stream) {
   if (M > 16)
-    return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
+    return cek::launch_w8a16(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, nullptr, 0,
+                             (hipStream_t)stream);
   return cek::launch_gemv(x, w, scale, cek::SK_F32_SCALAR, y, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 

@@ -34,10 +34,21 @@ at::Tensor esimd_gemm_fp8_pert(at::Tensor input, at::Tensor weight, at::Tensor w
   const int64_t M = input.numel() / K;
   TORCH_CHECK(output.numel() >= M * N, op, ": output must hold M*N elements");
   c10::OptionalDeviceGuard guard(input.device());
-  check_rc(cek_gemm_fp8_pert(input.data_ptr(), weight.data_ptr(), static_cast<const float*>(weight_scale.data_ptr()),
-                             output.data_ptr(), M, N, K, io_code(input.scalar_type()), fp8_code(weight),
-                             current_stream(input)),
-           op);
+  const auto* sp = static_cast<const float*>(weight_scale.data_ptr());
+  // shapes with too few tiles split K: fp32 partials in a workspace from the
+  // caching allocator (no kernel runs to allocate or clear it)
+  const int64_t need = cek_gemm_fp8_pert_workspace_size(M, N, K);
+  if (need > 0) {
+    at::Tensor ws = at::empty({(need + 3) / 4}, weight_scale.options());
+    check_rc(cek_gemm_fp8_pert_ws(input.data_ptr(), weight.data_ptr(), sp, output.data_ptr(), M, N, K,
+                                  io_code(input.scalar_type()), fp8_code(weight), ws.data_ptr(), need,
+                                  current_stream(input)),
+             op);
+  } else {
+    check_rc(cek_gemm_fp8_pert(input.data_ptr(), weight.data_ptr(), sp, output.data_ptr(), M, N, K,
+                               io_code(input.scalar_type()), fp8_code(weight), current_stream(input)),
+             op);
+  }
   return output;
 }
 

@@ -100,6 +100,22 @@ int cek_gemm_fp8_pert(const void* x, const void* w, const float* scale, void* y,
                       int io_dtype, int fp8_fmt, void* stream);
 
 /*
+ * The same product with a caller-provided workspace, which lets shapes with
+ * too few output tiles (e.g. M = 512, K = 14336) split K into parts: fp32
+ * partial sums in the workspace, then a second launch that adds them in
+ * order and scales (deterministic).  cek_gemm_fp8_pert_workspace_size gives
+ * the bytes the plan needs for (M, N, K), 0 when it runs unsplit; with a
+ * smaller workspace (or none) the call runs unsplit, like cek_gemm_fp8_pert.
+ * The workspace needs no initialisation and must be 4-byte aligned
+ * (CEK_ERR_INVALID otherwise).  Extends esimd_gemm_fp8_pert (same
+ * reference entry as cek_gemm_fp8_pert): the reference has no split K.
+ */
+int64_t cek_gemm_fp8_pert_workspace_size(int64_t M, int64_t N, int64_t K);
+int cek_gemm_fp8_pert_ws(const void* x, const void* w, const float* scale, void* y,
+                         int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Batched fused residual add + RMSNorm, in place:
  *   residual = f16(hidden + residual);
  *   hidden   = f16(residual * rsqrt(mean((hidden+residual)^2) + eps) * weight)

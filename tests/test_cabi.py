@@ -123,6 +123,14 @@ def test_host_rejects_invalid_arguments():
     assert lib.cek_gemm_fp8_a8w8_ws(p, p, p, p, p, 512, 4096, 14336, 0, None, 64, None) == E
     assert lib.cek_gemm_fp8_a8w8_ws(p, p, p, p, p, 512, 4096, 14336, 0, p, -1, None) == E
     assert lib.cek_gemm_fp8_a8w8_ws(p, p, p, p, p, 512, 4096, 14336, 0, C.c_void_p(18), 64, None) == E  # misaligned
+    # the w8a16 GEMM's split-K workspace: the same contract
+    assert lib.cek_gemm_fp8_pert_workspace_size(2048, 6144, 4096) == 0
+    ws = lib.cek_gemm_fp8_pert_workspace_size(512, 4096, 14336)
+    assert ws > 0 and ws % (512 * 4096 * 4) == 0
+    assert lib.cek_gemm_fp8_pert_workspace_size(64, 4096, 14336) == 0  # below the round model: unsplit
+    assert lib.cek_gemm_fp8_pert_ws(p, p, p, p, 512, 4096, 14336, 0, 0, None, 64, None) == E
+    assert lib.cek_gemm_fp8_pert_ws(p, p, p, p, 512, 4096, 14336, 0, 0, p, -1, None) == E
+    assert lib.cek_gemm_fp8_pert_ws(p, p, p, p, 512, 4096, 14336, 0, 0, C.c_void_p(18), 64, None) == E
     # the no-allocation a8w8 entry point refuses plans beyond its 32 MiB
     # static scratch buffer before any HIP call
     assert lib.cek_gemm_fp8_a8w8_workspace_size(768, 6144, 24576) > (32 << 20)

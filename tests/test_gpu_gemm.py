@@ -61,6 +61,53 @@ def test_gemm_pert_prefill(ops, dev, M, K, N):
     assert_close_fp(y.cpu(), ogemv.gemm_fp8_pert(x, W8, sv), f"prefill M={M}")
 
 
+@pytest.mark.parametrize("M,K,N,parts,io,fmt", [
+    (276, 2048, 130, 2, torch.float16, torch.float8_e4m3fn),     # 256 x 128, 2 parts
+    (1736, 16384, 847, 4, torch.bfloat16, torch.float8_e4m3fn),  # 256 x 128, 4 parts
+    (2977, 2048, 1325, 0, torch.float16, torch.float8_e5m2),     # 256 x 128
+    (1444, 2048, 5388, 0, torch.float16, torch.float8_e4m3fn),   # 256 x 192
+    (1298, 2048, 8256, 0, torch.bfloat16, torch.float8_e5m2),    # 256 x 256
+    (787, 128, 8256, 0, torch.float16, torch.float8_e4m3fn),     # 256 x 256, one K step
+    (641, 2048, 5388, 0, torch.float16, torch.float8_e4m3fn),    # 128 x 256
+    (130, 128, 369, 0, torch.bfloat16, torch.float8_e4m3fn),     # 128 x 256, one K step
+    (130, 2048, 369, 2, torch.float16, torch.float8_e4m3fn),     # 128 x 256, 2 parts
+    (130, 8192, 6344, 4, torch.float16, torch.float8_e5m2),      # 128 x 256, 4 parts
+    (1000, 8192, 1000, 4, torch.float16, torch.float8_e4m3fn),   # 128 x 128, 4 parts
+    (130, 130, 4096, 0, torch.float16, torch.float8_e4m3fn),     # K = 130: not a multiple of 64
+    (130, 4096, 130, 4, torch.float16, torch.float8_e4m3fn),     # 128 x 128, 4 parts
+    (130, 8192, 130, 8, torch.bfloat16, torch.float8_e4m3fn),    # 128 x 128, 8 parts
+])
+def test_gemm_pert_round_model(ops, dev, M, K, N, parts, io, fmt):
+    """Ragged shapes (M and N not multiples of the tile) on which the w8a16
+    round-model plan (M, N >= 128) picks each register-pipelined tile,
+    unsplit or split in `parts` (0: unsplit; the op allocates the
+    workspace); the bare C-ABI call (no workspace) runs the unsplit plan.
+    Both against the CPU oracle; two calls of the op agree bit for bit."""
+    from esimd_learning_amd import cabi
+    _say(f"gemm pert round model M={M} K={K} N={N} parts={parts} {io} {fmt}")
+    lib = cabi.load()
+    assert lib.cek_gemm_fp8_pert_workspace_size(M, N, K) == (parts * M * N * 4 if parts else 0)
+    g = torch.Generator().manual_seed(M + K + N)
+    W8 = (torch.randn(N, K, generator=g) * 0.05).to(fmt)
+    x = (torch.randn(M, K, generator=g) * 0.5).to(io)
+    sv = torch.tensor(0.02)
+    xd, Wd, svd = x.to(dev), W8.to(dev), sv.to(dev)
+    y1 = torch.full((M, N), float("nan"), dtype=io, device=dev)
+    y2 = torch.full((M, N), float("nan"), dtype=io, device=dev)
+    ops.esimd_gemm_fp8_pert(xd, Wd, svd, y1)
+    ops.esimd_gemm_fp8_pert(xd, Wd, svd, y2)
+    y3 = torch.full((M, N), float("nan"), dtype=io, device=dev)
+    io_code = cabi.CEK_F16 if io == torch.float16 else cabi.CEK_BF16
+    fmt_code = cabi.CEK_E4M3 if fmt == torch.float8_e4m3fn else cabi.CEK_E5M2
+    assert lib.cek_gemm_fp8_pert(xd.data_ptr(), Wd.data_ptr(), svd.data_ptr(), y3.data_ptr(), M, N, K, io_code,
+                                 fmt_code, cabi.stream_ptr(torch.cuda.current_stream())) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    ref = ogemv.gemm_fp8_pert(x, W8, sv)
+    assert_close_fp(y1.cpu(), ref, f"w8a16 op M={M} K={K} N={N}")
+    assert_close_fp(y3.cpu(), ref, f"w8a16 unsplit M={M} K={K} N={N}")
+
+
 def _a8w8_inputs(M, K, N, seed):
     x = synthetic.activations(M, K, seed=seed)
     q, sa = onorm.per_token_quant(x)

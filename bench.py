@@ -344,11 +344,12 @@ def bench_gemm_all(ops, torch, steps, warmup, all_m=True):
     return head
 
 
-def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
+def bench_gemm_pert(ops, torch, steps, warmup, M=2048, rotate=False):
     """The reference's prefill op esimd_gemm_fp8_pert (fp16 activations, e4m3
     weights, fp32 per-tensor scale; the w8a16 fp16-MFMA path) at the three
-    config-4 projections, timed like the a8w8 leg; rate against the 2.5
-    PFLOP/s dense fp16 MFMA peak."""
+    config-4 projections, timed like the a8w8 leg (with rotate, launch i
+    reads weight copy i % C of C copies over > 2 GB: weights from HBM); rate
+    against the 2.5 PFLOP/s dense fp16 MFMA peak."""
     from esimd_learning_amd import synthetic
     dev = "cuda:0"
     stream = torch.cuda.Stream()
@@ -357,19 +358,25 @@ def bench_gemm_pert(ops, torch, steps, warmup, M=2048):
         x = synthetic.activations(M, K, seed=2).to(dev)
         W8, _ = synthetic.weight_fp8(N, K, seed=3)
         Wd = W8.to(dev)
+        copies = max(2, math.ceil(ROTATE_BYTES / (N * K))) if rotate else 1
+        Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
         sv = torch.tensor(0.01, dtype=torch.float32, device=dev)
         y = torch.empty(M, N, dtype=torch.float16, device=dev)
-        fn = lambda: ops.esimd_gemm_fp8_pert(x, Wd, sv, y)  # noqa: E731
+        fns = [(lambda W=W: ops.esimd_gemm_fp8_pert(x, W, sv, y)) for W in Ws]
         with torch.cuda.stream(stream):
             for _ in range(warmup):
-                fn()
+                fns[0]()
         torch.cuda.synchronize()
-        _, ev_ms, _ = time_graph([fn] * steps, torch, stream, warm_s=WARM_S / 2)
-        us = ev_ms * 1e3 / steps
+        n = max(steps, copies) if rotate else steps
+        _, ev_ms, _ = time_graph([fns[i % copies] for i in range(n)], torch, stream, warm_s=WARM_S / 2)
+        us = ev_ms * 1e3 / n
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
-        rows.append({"config": f"w8a16 M={M} K={K} N={N}", "avg_launch_us": round(us, 2), "tflops": round(tf, 1),
-                     "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
-        del x, Wd, y
+        row = {"config": f"w8a16 M={M} K={K} N={N}", "avg_launch_us": round(us, 2), "tflops": round(tf, 1),
+               "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+        if rotate:
+            row["weights"] = "rotating copies over > 2 GB (read from HBM)"
+        rows.append(row)
+        del x, Wd, Ws, y
     return rows
 
 
@@ -725,6 +732,8 @@ def main():
         out["gemm_pert"] = bench_gemm_pert(ops, torch, max(10, a.steps // 40), max(3, a.warmup // 10))
         log("gemm pert (w8a16): " + ", ".join(f"{r['config']}={r['avg_launch_us']}us/{r['tflops']}TF"
                                               for r in out["gemm_pert"]))
+        out["gemm_pert_m_table"] = [r for Mx in (512, 2048, 4096)
+                                    for r in bench_gemm_pert(ops, torch, max(10, a.steps // 40), 2, M=Mx, rotate=True)]
     if not a.no_layer:
         out["decoder_layer"] = bench_layer(torch, max(20, a.steps // 4))
         dl = out["decoder_layer"]

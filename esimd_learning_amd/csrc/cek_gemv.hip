@@ -76,14 +76,28 @@ struct TailArgs {
 struct NormArgs {
   const uint16_t* h;  // hidden [M, K]
   const uint16_t* r;  // residual [M, K] (read)
-  const uint16_t* w;  // RMSNorm weight [K] (Gemma w+1 convention)
-  uint16_t* r_out;    // h + r rounded [M, K], written by workgroup 0
+  const uint16_t* w;  // RMSNorm weight [K] (Gemma w+1 convention); EPI_ADDNORM: [N]
+  uint16_t* r_out;    // h + r rounded [M, K], written by workgroup 0; EPI_ADDNORM: the residual [M, N], in place
   uint16_t* h_out;    // normed rows [M, K] (fp16/bf16 form; may be null), workgroup 0
   uint8_t* q_out;     // e4m3 codes [M, K] (quant form), workgroup 0
   float* s_out;       // per-row scales [M] (quant form), workgroup 0
   float eps;
   TailArgs tail;      // epilogue arguments (TAIL forms only)
+  float* ss_out;      // EPI_ADDNORM: per-tile sums of squares [M][N / 16]
+  const float* ss_in; // EPI_ROWSCALE: the producer's [M][nss] sums of squares
+  int nss;
 };
+
+// Deferred RMSNorm between two GEMVs (EPI in gemv_lds_kernel).
+// EPI_ADDNORM (the producer, e.g. o_proj): after the tile's sums, o =
+// Out(sum * scale) as usual, then s = o + r (fp32), r = Out(s) in place,
+// y = Out(f32(r) * w[n]) -- the norm's weight product without its 1 / rms
+// -- and the tile's sum of s^2 per row to ss_out[m][tile].
+// EPI_ROWSCALE (the consumer, e.g. gate/up): x holds the producer's y; every
+// workgroup's wave 0 sums the nss partials of each row in a fixed order
+// (nss <= 256 and a multiple of 4, M <= 4), inv = rsqrt(sum / K + eps), and
+// scales its outputs by inv[m].
+enum EpiKind { EPI_NONE = 0, EPI_ADDNORM = 1, EPI_ROWSCALE = 2 };
 
 struct SegRef {
   const uint8_t* w;
@@ -401,6 +415,52 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
   }
 }
 
+// EPI_ADDNORM epilogue of one 16-row tile (M <= 16): the cross-wave sum,
+// o = Out(sum * scale), then the residual add, the norm weight product and
+// the tile's per-row sum of squares (see EpiKind).
+template <typename T>
+__device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave, int lane, int n0, int N, int M,
+                                          const SegRef& sr, int skind, uint32_t sc_bits, const NormArgs& na,
+                                          const uint16_t (&pres)[4], uint16_t pnw) {
+  f4* red = reinterpret_cast<f4*>(smem);  // [3][64]
+  __syncthreads();                         // every wave is done with the stages
+  if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  const int n16 = lane & 15, g = lane >> 4, n = n0 + n16;
+  const float sc = scale_value(sc_bits, skind);
+  const float wn = T::to_f32(pnw);
+  f4 c = acc;
+#pragma unroll
+  for (int w = 0; w < 3; ++w) c += red[w * 64 + lane];
+  float s2[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int m = g * 4 + v;
+    const float o = T::to_f32(T::from_f32(f32_round(c[v] * sc)));
+    const float sv = o + T::to_f32(pres[v]);
+    const uint16_t rp = T::from_f32(sv);
+    s2[v] = f32_round(sv * sv);  // rounded before the sums (no fma contraction)
+    if (n < N && m < M) {
+      na.r_out[(size_t)m * N + n] = rp;
+      sr.y[(size_t)m * N + n] = T::from_f32(f32_round(T::to_f32(rp) * wn));
+    }
+  }
+  // each D row (one 16-lane DPP row): the tile's 16 columns, pairwise
+  // ((c0 + c1) + (c2 + c3)) + ... through xor 1, xor 2, half mirror, mirror
+#pragma unroll
+  for (int v = 0; v < 4; ++v) s2[v] += CEK_DPP_F32(s2[v], 0xB1);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) s2[v] += CEK_DPP_F32(s2[v], 0x4E);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) s2[v] += CEK_DPP_F32(s2[v], 0x141);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) s2[v] += CEK_DPP_F32(s2[v], 0x140);
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    if (n16 == 0 && g * 4 + v < M) na.ss_out[(size_t)(g * 4 + v) * (N >> 4) + (n0 >> 4)] = s2[v];
+}
+
 // LDS writes of this wave done, then a workgroup barrier -- without the
 // vmcnt(0) a fenced __syncthreads adds, which would drain the loads of the
 // stages in flight.  The "memory" clobber keeps LDS accesses (and the
@@ -589,8 +649,12 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
 // runtime chunk offsets cost VALU address arithmetic, which made the
 // multi-tile and M > 4 forms 1-5% slower with it.
 template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
-          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0, bool ROT = false>
+          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0, bool ROT = false, int EPI = EPI_NONE>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M, NormArgs na) {
+  static_assert(EPI != EPI_ADDNORM || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !XF8 &&
+                                       std::is_same<T, TO>::value),
+                "deferred norm producer: one 16-row tile, fp16 / bf16");
+  static_assert(EPI != EPI_ROWSCALE || (MB == 1 && !NORM && !XF8), "deferred norm consumer: fp16 / bf16, M <= 16");
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 16), "activations go through LDS only for M <= 16");
@@ -719,6 +783,50 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     }
     asm volatile("" ::: "memory");  // before the weight prologue
   }
+  // EPI_ROWSCALE: wave 0 (the only wave that scales outputs) loads the
+  // producer's partial sums of rows 0..3, four per lane (nss <= 256, rows
+  // 16-byte aligned), before the weight prologue, so that its wait for them
+  // leaves the weight stages in flight
+  // The loads are unconditional (clamped addresses, dead values dropped at
+  // their use) under a wave-uniform branch: a lane-divergent load makes the
+  // compiler wait for it at the end of its branch.
+  [[maybe_unused]] const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  [[maybe_unused]] f4 rsp[4];
+  [[maybe_unused]] float rinv[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (EPI == EPI_ROWSCALE) {
+    if (wave_u == 0) {
+      const int e = min(4 * lane, na.nss - 4);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        rsp[m] = *reinterpret_cast<const f4*>(na.ss_in + (size_t)min(m, M - 1) * na.nss + e);
+    }
+    asm volatile("" ::: "memory");  // before the weight prologue
+  }
+  // EPI_ADDNORM: the residual values (rows 4 (lane >> 4) + v, column
+  // lane & 15 of the tile) and norm weight that wave 0's epilogue uses, raw,
+  // loaded before the weight prologue so that the epilogue does not wait
+  // for them
+  // (every wave loads them: a branch would merge the 16-bit values, which
+  // makes the compiler wait for them there)
+  [[maybe_unused]] uint16_t pres[4];
+  [[maybe_unused]] uint16_t pnw;
+  if constexpr (EPI == EPI_ADDNORM) {
+    const int n = min(nw + n16, N - 1);
+    pnw = na.w[n];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) pres[v] = na.r_out[(size_t)min(g * 4 + v, M - 1) * N + n];
+    asm volatile("" ::: "memory");  // before the weight prologue
+  }
+  // EPI_ROWSCALE: wave 0's epilogue row scales, sc_m[0][v] = inv of row 4 (lane >> 4) + v
+  auto pick_rs = [&]() {
+    if constexpr (EPI == EPI_ROWSCALE) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = min(g * 4 + v, 3);
+        sc_m[0][v] = m == 0 ? rinv[0] : (m == 1 ? rinv[1] : (m == 2 ? rinv[2] : rinv[3]));
+      }
+    }
+  };
   // NORM + XF8: wave 0's epilogue row scales, sc_m[0][v] for row 4 (lane >> 4) + v
   auto pick_row_scales = [&]() {
 #pragma unroll
@@ -737,6 +845,20 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   // the loads of the stages after it in flight.
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, wr[j], xr[j]);
+
+  if constexpr (EPI == EPI_ROWSCALE) {
+    // the rows' sums in a fixed order: each lane's four, then the wave's
+    // 64 lanes (wave_sum_dpp); wave 0 only, no barrier
+    if (wave_u == 0) {
+      const bool in = 4 * lane < na.nss;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float t = (rsp[m][0] + rsp[m][1]) + (rsp[m][2] + rsp[m][3]);
+        rinv[m] = rsqrtf(wave_sum_dpp(in && m < M ? t : 0.f) / (float)K + na.eps);
+      }
+      pick_rs();
+    }
+  }
 
   if constexpr (NORM) {
     // add_rmsnorm_kernel's arithmetic, row by row: s = h + r in fp32, r' =
@@ -897,10 +1019,11 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
         uint8_t* redp = smem + 2 * STAGE + XAREA;
         if constexpr (GLU) {
           if (i / STEPS == 0) {  // gate tile: keep the rounded values
-            lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8,
+            lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8 || EPI == EPI_ROWSCALE,
                                     [&](int, int b, int v, float o) { gate[b][v] = TO::to_f32(TO::from_f32(o)); });
           } else {  // up tile: gelu_and_mul and the store
-            lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8, [&](int, int b, int v, float o) {
+            lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8 || EPI == EPI_ROWSCALE,
+                                    [&](int, int b, int v, float o) {
               const int n = nw + n16, m = b * 16 + g * 4 + v;
               if (n < half && m < M)
                 sr.y[(size_t)m * half + n] =
@@ -909,7 +1032,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           }
         } else {
           lds_reduce_store_tile<NT, MB>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
-                                        XF8, std::is_same<TO, BF16>::value);
+                                        XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
         }
         if (i + 1 < NS) {
 #pragma unroll
@@ -919,13 +1042,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, tile_row(i / STEPS + 1), N, M, sr, skind,
                                   XF8 && !NORM ? sg.xs : nullptr);
           if constexpr (NORM && XF8) pick_row_scales();
+          pick_rs();
         }
       }
     }
   }
-  if constexpr (TPW == 1)
-    lds_reduce_store<NT, MB, TAIL != TAIL_NONE>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m, XF8,
-                                                std::is_same<TO, BF16>::value);
+  if constexpr (EPI == EPI_ADDNORM)
+    lds_reduce_addnorm<T>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
+  else if constexpr (TPW == 1)
+    lds_reduce_store<NT, MB, TAIL != TAIL_NONE>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
+                                                XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
   if constexpr (TAIL != TAIL_NONE) gemv_tail<T, TAIL, TP>(na.tail, sr.y, nw, N, M, smem);
 }
 
@@ -1067,13 +1193,21 @@ static bool launch_lds(const void* x, GemvSegs& sg, int skind, int M, int K, int
 // segment of 2 d rows, one workgroup per 16 output columns.  The per-M
 // configurations are the one-tile ones of launch_lds_steps for these K.
 template <typename T, typename TO, int FMT, bool XF8, int S>
-static void launch_glu_steps(const void* x, GemvSegs& sg, int skind, int M, int d, hipStream_t st) {
+static void launch_glu_steps(const void* x, GemvSegs& sg, int skind, int M, int d, const NormArgs* rs,
+                             hipStream_t st) {
   const int grid = (d + 15) / 16;
   sg.gstart[0] = 0;
   for (int i = 1; i <= MAX_SEGS; ++i) sg.gstart[i] = grid;
 #define CEK_GLU(D, MX, ROT)                                                                   \
   gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, 2, true, false, TAIL_NONE, 0, ROT><<<dim3(grid), 256, 0, st>>>( \
       x, sg, skind, M, NormArgs{})
+  if constexpr (!XF8 && FMT == CEK_E4M3) {
+    if (rs) {  // deferred RMSNorm consumer (M <= 4, checked by the caller)
+      gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, 3, S, 4, 2, true, false, TAIL_NONE, 0, true, EPI_ROWSCALE>
+          <<<dim3(grid), 256, 0, st>>>(x, sg, skind, M, *rs);
+      return;
+    }
+  }
   if constexpr (!XF8) {
     if (M <= 4) {
       CEK_GLU(3, 4, true);
@@ -1089,11 +1223,12 @@ static void launch_glu_steps(const void* x, GemvSegs& sg, int skind, int M, int 
 }
 
 template <typename T, typename TO, int FMT, bool XF8>
-static int launch_glu(const void* x, GemvSegs& sg, int skind, int M, int d, int K, hipStream_t st) {
+static int launch_glu(const void* x, GemvSegs& sg, int skind, int M, int d, int K, hipStream_t st,
+                      const NormArgs* rs = nullptr) {
   switch (K >> 10) {
-    case 3: launch_glu_steps<T, TO, FMT, XF8, 3>(x, sg, skind, M, d, st); break;
-    case 4: launch_glu_steps<T, TO, FMT, XF8, 4>(x, sg, skind, M, d, st); break;
-    case 5: launch_glu_steps<T, TO, FMT, XF8, 5>(x, sg, skind, M, d, st); break;
+    case 3: launch_glu_steps<T, TO, FMT, XF8, 3>(x, sg, skind, M, d, rs, st); break;
+    case 4: launch_glu_steps<T, TO, FMT, XF8, 4>(x, sg, skind, M, d, rs, st); break;
+    case 5: launch_glu_steps<T, TO, FMT, XF8, 5>(x, sg, skind, M, d, rs, st); break;
     default: return CEK_ERR_UNSUPPORTED;
   }
   return check_launch();
@@ -1340,7 +1475,8 @@ static int scale_kind(int scale_dtype) {
 // xs == null: x is io_dtype [M, K]; else x holds e4m3 codes [M, K] with
 // per-row fp32 scales xs (the a8w8 contract: e4m3 weights, fp32 scales).
 int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* scale, int skind, void* y,
-                    int64_t M, int64_t d, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st) {
+                    int64_t M, int64_t d, int64_t K, int io_dtype, int fp8_fmt, hipStream_t st,
+                    const NormArgs* rs = nullptr) {
   if (M < 0 || d < 0 || K <= 0 || d > INT32_MAX / 2 || K > INT32_MAX) return CEK_ERR_INVALID;
   if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
   if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
@@ -1353,6 +1489,7 @@ int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* s
   // aligned operands; other requests are left to GEMV + gelu_and_mul.
   if (M > 16 || K % 1024 != 0 || K < 3072 || K > 5120 || !aligned(x, 16) || !aligned(w, 16))
     return CEK_ERR_UNSUPPORTED;
+  if (rs && (xs || M > 4 || fp8_fmt != CEK_E4M3)) return CEK_ERR_UNSUPPORTED;
   GemvSegs sg{};
   sg.count = 1;
   sg.w[0] = static_cast<const uint8_t*>(w);
@@ -1361,6 +1498,10 @@ int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* s
   sg.n[0] = (int)(2 * d);
   sg.xs = xs;
   const int m = (int)M, dd = (int)d, k = (int)K;
+  if (rs) {
+    if (io_dtype == CEK_F16) return launch_glu<F16, F16, CEK_E4M3, false>(x, sg, skind, m, dd, k, st, rs);
+    return launch_glu<BF16, BF16, CEK_E4M3, false>(x, sg, skind, m, dd, k, st, rs);
+  }
   if (xs) {
     if (io_dtype == CEK_F16) return launch_glu<F16, F16, CEK_E4M3, true>(x, sg, SK_F32, m, dd, k, st);
     return launch_glu<F16, BF16, CEK_E4M3, true>(x, sg, SK_F32, m, dd, k, st);
@@ -1376,11 +1517,11 @@ int launch_gemv_glu(const void* x, const float* xs, const void* w, const void* s
 // depth 3, e4m3 weights, K in {3, 4, 5} KiB values; tp = L (ROPE, head dim
 // 128 or 256).  CEK_ERR_UNSUPPORTED for
 // other shapes (the caller runs the GEMV, then the op).
-template <typename T, int TAIL, int TP>
+template <typename T, int TAIL, int TP, int EPI = EPI_NONE>
 static void launch_tail_t(const void* x, GemvSegs& sg, int skind, int M, int K, const NormArgs& na, hipStream_t st) {
   const dim3 grid((unsigned)seg_grid(sg, 16));
-#define CEK_TAIL(S)                                                                                  \
-  gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, 3, S, 4, 1, false, false, TAIL, TP, true><<<grid, 256, 0, st>>>( \
+#define CEK_TAIL(S)                                                                                       \
+  gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, 3, S, 4, 1, false, false, TAIL, TP, true, EPI><<<grid, 256, 0, st>>>( \
       x, sg, skind, M, na)
   if (K == 3072) CEK_TAIL(3);
   else if (K == 4096) CEK_TAIL(4);
@@ -1410,25 +1551,157 @@ int launch_gemv_tail(const void* x, const void* w, const void* scale, int skind,
   const int m = (int)M, k = (int)K;
   const bool f16 = io_dtype == CEK_F16;
   (void)tail;
+  if (na.ss_in) {  // deferred RMSNorm consumer
+    if (tp == 8) {
+      if (f16) launch_tail_t<F16, TAIL_ROPE, 8, EPI_ROWSCALE>(x, sg, skind, m, k, na, st);
+      else launch_tail_t<BF16, TAIL_ROPE, 8, EPI_ROWSCALE>(x, sg, skind, m, k, na, st);
+    } else {
+      if (f16) launch_tail_t<F16, TAIL_ROPE, 16, EPI_ROWSCALE>(x, sg, skind, m, k, na, st);
+      else launch_tail_t<BF16, TAIL_ROPE, 16, EPI_ROWSCALE>(x, sg, skind, m, k, na, st);
+    }
+    return check_launch();
+  }
   if (tp == 8) { if (f16) launch_tail_t<F16, TAIL_ROPE, 8>(x, sg, skind, m, k, na, st); else launch_tail_t<BF16, TAIL_ROPE, 8>(x, sg, skind, m, k, na, st); }
   else { if (f16) launch_tail_t<F16, TAIL_ROPE, 16>(x, sg, skind, m, k, na, st); else launch_tail_t<BF16, TAIL_ROPE, 16>(x, sg, skind, m, k, na, st); }
   return check_launch();
 }
 
+// Deferred RMSNorm producer (EPI_ADDNORM) and plain consumer
+// (EPI_ROWSCALE): M <= 4 rows staged through LDS, one 16-row tile per
+// workgroup, rotated K order, e4m3 weights, K in {2, 3, 4, 5, 14, 24} KiB
+// values.
+template <typename T, int EPI, int S>
+static void launch_defer_t(const void* x, GemvSegs& sg, int skind, int M, const NormArgs& na, hipStream_t st) {
+  gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, (S >= 3 ? 3 : 2), S, 4, 1, false, false, TAIL_NONE, 0, true, EPI>
+      <<<dim3(seg_grid(sg, 16)), 256, 0, st>>>(x, sg, skind, M, na);
+}
+
+template <typename T, int EPI>
+static bool launch_defer_k(const void* x, GemvSegs& sg, int skind, int M, int K, const NormArgs& na, hipStream_t st) {
+  switch (K >> 10) {
+    case 2: launch_defer_t<T, EPI, 2>(x, sg, skind, M, na, st); return true;
+    case 3: launch_defer_t<T, EPI, 3>(x, sg, skind, M, na, st); return true;
+    case 4: launch_defer_t<T, EPI, 4>(x, sg, skind, M, na, st); return true;
+    case 5: launch_defer_t<T, EPI, 5>(x, sg, skind, M, na, st); return true;
+    case 14: launch_defer_t<T, EPI, 14>(x, sg, skind, M, na, st); return true;
+    case 24: launch_defer_t<T, EPI, 24>(x, sg, skind, M, na, st); return true;
+    default: return false;
+  }
+}
+
+// Common checks of the deferred-norm launches; CEK_OK to go on, else the status.
+static int defer_checks(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N,
+                        int64_t K, int io_dtype, int fp8_fmt) {
+  if (M < 0 || N < 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX) return CEK_ERR_INVALID;
+  if (io_dtype != CEK_F16 && io_dtype != CEK_BF16) return CEK_ERR_INVALID;
+  if (fp8_fmt != CEK_E4M3 && fp8_fmt != CEK_E5M2) return CEK_ERR_INVALID;
+  if (skind < 0) return CEK_ERR_INVALID;
+  if (M == 0 || N == 0) return CEK_OK;
+  if (!x || !w || !scale || !y) return CEK_ERR_INVALID;
+  if (N * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
+  if (M > 4 || K % 1024 != 0 || fp8_fmt != CEK_E4M3 || N % 16 != 0 || !aligned(x, 16) || !aligned(w, 16))
+    return CEK_ERR_UNSUPPORTED;
+  return CEK_OK;
+}
+
+int launch_gemv_addnorm(const void* x, const void* w, const void* scale, int skind, void* residual,
+                        const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N, int64_t K,
+                        int io_dtype, int fp8_fmt, hipStream_t st) {
+  const int rc = defer_checks(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt);
+  if (rc != CEK_OK || M == 0 || N == 0) return rc;
+  if (!residual || !norm_weight || !ss_out) return CEK_ERR_INVALID;
+  // other workgroups still read x and w while one writes y, the residual
+  // and the partial sums
+  const int64_t yb = M * N * 2;
+  for (const auto& [p, b] : {std::pair<const void*, int64_t>{y, yb}, {residual, yb}, {ss_out, M * (N / 16) * 4}})
+    if (overlaps(p, b, x, M * K * 2) || overlaps(p, b, w, N * K)) return CEK_ERR_UNSUPPORTED;
+  if (overlaps(y, yb, residual, yb) || overlaps(ss_out, M * (N / 16) * 4, y, yb) ||
+      overlaps(ss_out, M * (N / 16) * 4, residual, yb))
+    return CEK_ERR_UNSUPPORTED;
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = static_cast<const uint8_t*>(w);
+  sg.s[0] = scale;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)N;
+  NormArgs na{};
+  na.r_out = static_cast<uint16_t*>(residual);
+  na.w = static_cast<const uint16_t*>(norm_weight);
+  na.ss_out = ss_out;
+  const bool ok = io_dtype == CEK_F16 ? launch_defer_k<F16, EPI_ADDNORM>(x, sg, skind, (int)M, (int)K, na, st)
+                                      : launch_defer_k<BF16, EPI_ADDNORM>(x, sg, skind, (int)M, (int)K, na, st);
+  return ok ? check_launch() : CEK_ERR_UNSUPPORTED;
+}
+
+// The row-scale arguments of the deferred-norm consumers; CEK_OK or the status.
+static int rowscale_args(const float* row_ss, int64_t n_ss, float row_eps, int64_t M, NormArgs& na) {
+  if (M == 0) return CEK_OK;
+  if (!row_ss || n_ss < 1) return CEK_ERR_INVALID;
+  if (n_ss > 256 || n_ss % 4 != 0 || !aligned(row_ss, 16)) return CEK_ERR_UNSUPPORTED;
+  na.ss_in = row_ss;
+  na.nss = (int)n_ss;
+  na.eps = row_eps;
+  return CEK_OK;
+}
+
+int launch_gemv_rowscale(const void* x, const void* w, const void* scale, int skind, void* y, const float* row_ss,
+                         int64_t n_ss, float row_eps, int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt,
+                         hipStream_t st) {
+  const int rc = defer_checks(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt);
+  if (rc != CEK_OK || M == 0 || N == 0) return rc;
+  NormArgs na{};
+  const int rc2 = rowscale_args(row_ss, n_ss, row_eps, M, na);
+  if (rc2 != CEK_OK) return rc2;
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.w[0] = static_cast<const uint8_t*>(w);
+  sg.s[0] = scale;
+  sg.y[0] = static_cast<uint16_t*>(y);
+  sg.n[0] = (int)N;
+  const bool ok = io_dtype == CEK_F16 ? launch_defer_k<F16, EPI_ROWSCALE>(x, sg, skind, (int)M, (int)K, na, st)
+                                      : launch_defer_k<BF16, EPI_ROWSCALE>(x, sg, skind, (int)M, (int)K, na, st);
+  return ok ? check_launch() : CEK_ERR_UNSUPPORTED;
+}
+
 }  // namespace cek
 
-extern "C" int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, void* y,
-                                         const void* q_weight, const void* k_weight, const int64_t* positions,
-                                         int64_t n_q, int64_t n_k, int64_t head_dim, float eps, float theta,
-                                         int is_neox, int* counters, int64_t M, int64_t N, int64_t K, int io_dtype,
-                                         int fp8_fmt, int scale_dtype, void* stream) {
+extern "C" int cek_gemv_fp8_add_rms_norm_defer(const void* x, const void* w, const void* scale, void* residual,
+                                               const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N,
+                                               int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
+  return cek::launch_gemv_addnorm(x, w, scale, cek::scale_kind(scale_dtype), residual, norm_weight, y, ss_out, M, N, K,
+                                  io_dtype, fp8_fmt, (hipStream_t)stream);
+}
+
+extern "C" int cek_gemv_fp8_pern_rs(const void* x, const void* w, const void* scale, void* y, const float* row_ss,
+                                    int64_t n_ss, float row_eps, int64_t M, int64_t N, int64_t K, int io_dtype,
+                                    int fp8_fmt, int scale_dtype, void* stream) {
+  return cek::launch_gemv_rowscale(x, w, scale, cek::scale_kind(scale_dtype), y, row_ss, n_ss, row_eps, M, N, K,
+                                   io_dtype, fp8_fmt, (hipStream_t)stream);
+}
+
+extern "C" int cek_gemv_fp8_gelu_and_mul_rs(const void* x, const void* w, const void* scale, void* y,
+                                            const float* row_ss, int64_t n_ss, float row_eps, int64_t M, int64_t d,
+                                            int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
+  cek::NormArgs na{};
+  const int rc = cek::rowscale_args(row_ss, n_ss, row_eps, M, na);
+  if (rc != CEK_OK) return rc;
+  if (M > 4) return CEK_ERR_UNSUPPORTED;
+  return cek::launch_gemv_glu(x, nullptr, w, scale, cek::scale_kind(scale_dtype), y, M, d, K, io_dtype, fp8_fmt,
+                              (hipStream_t)stream, M == 0 ? nullptr : &na);
+}
+
+namespace cek {
+// The checks and tail arguments shared by the two QKV + q/k-norm + rope entry
+// points; CEK_OK when the launch may go ahead with na.
+static int qk_rope_args(const void* q_weight, const void* k_weight, const int64_t* positions, int64_t n_q,
+                        int64_t n_k, int64_t head_dim, float eps, float theta, int is_neox, int* counters, int64_t M,
+                        int64_t N, NormArgs& na) {
   if (M < 0 || N < 0 || n_q < 0 || n_k < 0 || head_dim <= 0 || !(theta > 0.f)) return CEK_ERR_INVALID;
   if ((n_q + n_k) * head_dim > N) return CEK_ERR_INVALID;
   if (M > 0 && N > 0 && (!positions || (n_q > 0 && !q_weight) || (n_k > 0 && !k_weight))) return CEK_ERR_INVALID;
   if (head_dim != 128 && head_dim != 256) return M == 0 || N == 0 ? CEK_OK : CEK_ERR_UNSUPPORTED;
-  if (N % 8 != 0 || (n_q > 0 && !cek::aligned(q_weight, 16)) || (n_k > 0 && !cek::aligned(k_weight, 16)))
+  if (N % 8 != 0 || (n_q > 0 && !aligned(q_weight, 16)) || (n_k > 0 && !aligned(k_weight, 16)))
     return M == 0 || N == 0 ? CEK_OK : CEK_ERR_UNSUPPORTED;
-  cek::NormArgs na{};
   na.tail.counters = counters;
   na.tail.qw = static_cast<const uint16_t*>(q_weight);
   na.tail.kw = static_cast<const uint16_t*>(k_weight);
@@ -1438,6 +1711,36 @@ extern "C" int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const voi
   na.tail.eps = eps;
   na.tail.theta = theta;
   na.tail.neox = is_neox != 0;
+  return CEK_OK;
+}
+}  // namespace cek
+
+extern "C" int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, void* y,
+                                         const void* q_weight, const void* k_weight, const int64_t* positions,
+                                         int64_t n_q, int64_t n_k, int64_t head_dim, float eps, float theta,
+                                         int is_neox, int* counters, int64_t M, int64_t N, int64_t K, int io_dtype,
+                                         int fp8_fmt, int scale_dtype, void* stream) {
+  cek::NormArgs na{};
+  const int rc = cek::qk_rope_args(q_weight, k_weight, positions, n_q, n_k, head_dim, eps, theta, is_neox, counters,
+                                   M, N, na);
+  if (rc != CEK_OK || (head_dim != 128 && head_dim != 256)) return rc;
+  return cek::launch_gemv_tail(x, w, scale, cek::scale_kind(scale_dtype), y, M, N, K, io_dtype, fp8_fmt,
+                               cek::TAIL_ROPE, (int)(head_dim / 16), na, (hipStream_t)stream);
+}
+
+extern "C" int cek_gemv_fp8_qk_norm_rope_rs(const void* x, const void* w, const void* scale, void* y,
+                                            const void* q_weight, const void* k_weight, const int64_t* positions,
+                                            int64_t n_q, int64_t n_k, int64_t head_dim, float eps, float theta,
+                                            int is_neox, int* counters, const float* row_ss, int64_t n_ss,
+                                            float row_eps, int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt,
+                                            int scale_dtype, void* stream) {
+  cek::NormArgs na{};
+  int rc = cek::qk_rope_args(q_weight, k_weight, positions, n_q, n_k, head_dim, eps, theta, is_neox, counters, M, N,
+                             na);
+  if (rc != CEK_OK || (head_dim != 128 && head_dim != 256)) return rc;
+  if (M == 0 || N == 0) return CEK_OK;
+  rc = cek::rowscale_args(row_ss, n_ss, row_eps, M, na);
+  if (rc != CEK_OK) return rc;
   return cek::launch_gemv_tail(x, w, scale, cek::scale_kind(scale_dtype), y, M, N, K, io_dtype, fp8_fmt,
                                cek::TAIL_ROPE, (int)(head_dim / 16), na, (hipStream_t)stream);
 }

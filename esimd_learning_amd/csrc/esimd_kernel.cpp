@@ -544,3 +544,131 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
                             (float)theta, is_neox ? 1 : 0, io, st),
            op);
 }
+
+// Deferred RMSNorm between two decode GEMVs (up to four rows, e4m3
+// weights).  The producer GEMV (e.g. o_proj) adds its rounded output into
+// the residual in place, writes output = residual * norm_weight (the norm
+// without its 1 / rms) and row_ss [M, N / 16], the per-16-column sums of
+// squares of the unrounded sums; the consumer ops below (the plain GEMV,
+// gate/up with gelu_and_mul, QKV with QK-norm + RoPE) take that output and
+// row_ss and scale their rows by rsqrt(sum / K + eps).  No fallback: shapes
+// the kernels do not take raise, and the caller runs the unfused ops.
+static void check_defer_common(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& weight_scale,
+                               const at::Tensor& output, const char* op, int64_t& M, int64_t& N, int64_t& K) {
+  check_gemv_io(input, output, op);
+  check_fp8_weight(weight, op);
+  check_device(weight, input, op, "weight");
+  check_device(weight_scale, input, op, "weight_scale");
+  check_device(output, input, op, "output");
+  check_contig(input, op, "input");
+  check_contig(weight, op, "weight");
+  check_contig(weight_scale, op, "weight_scale");
+  check_contig(output, op, "output");
+  TORCH_CHECK(weight.dim() == 2 && weight.size(0) > 0 && weight.size(1) > 0, op, ": weight must be [N, K]");
+  N = weight.size(0);
+  K = weight.size(1);
+  TORCH_CHECK(input.size(-1) == K, op, ": input must be [M, K]");
+  M = input.numel() / K;
+}
+
+static void check_row_ss(const at::Tensor& row_ss, const at::Tensor& input, int64_t M, const char* op) {
+  TORCH_CHECK(row_ss.scalar_type() == at::ScalarType::Float, op, ": row_ss must be fp32");
+  check_device(row_ss, input, op, "row_ss");
+  check_contig(row_ss, op, "row_ss");
+  TORCH_CHECK(row_ss.dim() == 2 && row_ss.size(0) == M && row_ss.size(1) > 0, op, ": row_ss must be [M, n]");
+}
+
+void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                                       at::Tensor residual, at::Tensor norm_weight, at::Tensor output,
+                                       at::Tensor row_ss) {
+  const char* op = "esimd_gemv_fp8_add_rms_norm_defer";
+  int64_t M, N, K;
+  check_defer_common(input, weight, weight_scale, output, op, M, N, K);
+  TORCH_CHECK(output.numel() == M * N, op, ": output must be [M, N]");
+  TORCH_CHECK(residual.scalar_type() == input.scalar_type() && norm_weight.scalar_type() == input.scalar_type(), op,
+              ": residual and norm_weight must have the input's dtype");
+  check_device(residual, input, op, "residual");
+  check_device(norm_weight, input, op, "norm_weight");
+  check_contig(residual, op, "residual");
+  check_contig(norm_weight, op, "norm_weight");
+  TORCH_CHECK(residual.numel() == M * N && norm_weight.numel() == N, op,
+              ": residual must be [M, N] and norm_weight [N]");
+  TORCH_CHECK(N % 16 == 0, op, ": N must be a multiple of 16");
+  TORCH_CHECK(row_ss.scalar_type() == at::ScalarType::Float, op, ": row_ss must be fp32");
+  check_device(row_ss, input, op, "row_ss");
+  check_contig(row_ss, op, "row_ss");
+  TORCH_CHECK(row_ss.numel() == M * (N / 16), op, ": row_ss must be [M, N / 16]");
+  const int scale_code = scale_code_of(weight_scale, N, op);
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_gemv_fp8_add_rms_norm_defer(input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(),
+                                           residual.data_ptr(), norm_weight.data_ptr(), output.data_ptr(),
+                                           static_cast<float*>(row_ss.data_ptr()), M, N, K,
+                                           io_code(input.scalar_type()), fp8_code(weight), scale_code,
+                                           current_stream(input)),
+           op);
+}
+
+void esimd_gemv_fp8_pern_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                            at::Tensor row_ss, double eps) {
+  const char* op = "esimd_gemv_fp8_pern_rs";
+  int64_t M, N, K;
+  check_defer_common(input, weight, weight_scale, output, op, M, N, K);
+  TORCH_CHECK(output.numel() == M * N, op, ": output must be [M, N]");
+  check_row_ss(row_ss, input, M, op);
+  const int scale_code = scale_code_of(weight_scale, N, op);
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_gemv_fp8_pern_rs(input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(), output.data_ptr(),
+                                static_cast<const float*>(row_ss.data_ptr()), row_ss.size(1), (float)eps, M, N, K,
+                                io_code(input.scalar_type()), fp8_code(weight), scale_code, current_stream(input)),
+           op);
+}
+
+void esimd_gemv_fp8_gelu_and_mul_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                                    at::Tensor row_ss, double eps) {
+  const char* op = "esimd_gemv_fp8_gelu_and_mul_rs";
+  int64_t M, N, K;
+  check_defer_common(input, weight, weight_scale, output, op, M, N, K);
+  TORCH_CHECK(N % 2 == 0 && output.size(-1) == N / 2 && output.numel() == M * (N / 2), op,
+              ": weight must be [2d, K] and output [M, d]");
+  TORCH_CHECK(weight_scale.numel() == N, op, ": weight_scale must hold 2d elements");
+  check_row_ss(row_ss, input, M, op);
+  const int scale_code = scale_code_of(weight_scale, N, op);
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_gemv_fp8_gelu_and_mul_rs(input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(),
+                                        output.data_ptr(), static_cast<const float*>(row_ss.data_ptr()),
+                                        row_ss.size(1), (float)eps, M, N / 2, K, io_code(input.scalar_type()),
+                                        fp8_code(weight), scale_code, current_stream(input)),
+           op);
+}
+
+void esimd_gemv_fp8_qk_norm_rope_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                                    at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
+                                    int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters,
+                                    at::Tensor row_ss, double row_eps) {
+  const char* op = "esimd_gemv_fp8_qk_norm_rope_rs";
+  int64_t M, N, K;
+  check_defer_common(input, weight, weight_scale, output, op, M, N, K);
+  TORCH_CHECK(output.numel() == M * N, op, ": output must be [M, N]");
+  for (const auto* t : {&q_weight, &k_weight, &positions}) check_device(*t, input, op, "operand");
+  check_contig(q_weight, op, "q_weight");
+  check_contig(k_weight, op, "k_weight");
+  check_contig(positions, op, "positions");
+  TORCH_CHECK(q_weight.scalar_type() == input.scalar_type() && k_weight.scalar_type() == input.scalar_type(), op,
+              ": q_weight and k_weight must have the input's dtype");
+  TORCH_CHECK(positions.scalar_type() == at::ScalarType::Long && positions.numel() == M, op,
+              ": positions must be int64 [M]");
+  const int64_t hd = q_weight.numel();
+  TORCH_CHECK(k_weight.numel() == hd && hd > 0, op, ": q_weight and k_weight must both have head_dim elements");
+  TORCH_CHECK(n_q >= 0 && n_k >= 0 && (n_q + n_k) * hd <= N, op, ": the q and k heads must fit in the output row");
+  check_counters(counters, input, 64 * (n_q + n_k), op);
+  check_row_ss(row_ss, input, M, op);
+  const int scale_code = scale_code_of(weight_scale, N, op);
+  c10::OptionalDeviceGuard guard(input.device());
+  check_rc(cek_gemv_fp8_qk_norm_rope_rs(
+               input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(), output.data_ptr(), q_weight.data_ptr(),
+               k_weight.data_ptr(), static_cast<const int64_t*>(positions.data_ptr()), n_q, n_k, hd, (float)eps,
+               (float)theta, is_neox ? 1 : 0, static_cast<int*>(counters.data_ptr()),
+               static_cast<const float*>(row_ss.data_ptr()), row_ss.size(1), (float)row_eps, M, N, K,
+               io_code(input.scalar_type()), fp8_code(weight), scale_code, current_stream(input)),
+           op);
+}

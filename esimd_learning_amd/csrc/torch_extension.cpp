@@ -62,6 +62,23 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
         "Tensor q_weight, Tensor k_weight, Tensor positions, int n_q, int n_k, float eps, float theta, "
         "bool is_neox, Tensor(b!) counters) -> ()");
   m.impl("esimd_gemv_fp8_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope);
+
+  m.def("esimd_gemv_fp8_add_rms_norm_defer(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) residual, "
+        "Tensor norm_weight, Tensor(b!) output, Tensor(c!) row_ss) -> ()");
+  m.impl("esimd_gemv_fp8_add_rms_norm_defer", c10::DispatchKey::CUDA, &esimd_gemv_fp8_add_rms_norm_defer);
+
+  m.def("esimd_gemv_fp8_pern_rs(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "
+        "Tensor row_ss, float eps) -> ()");
+  m.impl("esimd_gemv_fp8_pern_rs", c10::DispatchKey::CUDA, &esimd_gemv_fp8_pern_rs);
+
+  m.def("esimd_gemv_fp8_gelu_and_mul_rs(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "
+        "Tensor row_ss, float eps) -> ()");
+  m.impl("esimd_gemv_fp8_gelu_and_mul_rs", c10::DispatchKey::CUDA, &esimd_gemv_fp8_gelu_and_mul_rs);
+
+  m.def("esimd_gemv_fp8_qk_norm_rope_rs(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "
+        "Tensor q_weight, Tensor k_weight, Tensor positions, int n_q, int n_k, float eps, float theta, "
+        "bool is_neox, Tensor(b!) counters, Tensor row_ss, float row_eps) -> ()");
+  m.impl("esimd_gemv_fp8_qk_norm_rope_rs", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope_rs);
 }
 
 PyMODINIT_FUNC PyInit_custom_esimd_kernels() {

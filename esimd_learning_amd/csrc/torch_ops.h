@@ -59,6 +59,20 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
                                  at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
                                  int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters);
 
+// Deferred RMSNorm between two decode GEMVs: the producer (residual add,
+// norm weight, per-tile sums of squares) and the row-scaled consumers.
+void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
+                                       at::Tensor residual, at::Tensor norm_weight, at::Tensor output,
+                                       at::Tensor row_ss);
+void esimd_gemv_fp8_pern_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                            at::Tensor row_ss, double eps);
+void esimd_gemv_fp8_gelu_and_mul_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                                    at::Tensor row_ss, double eps);
+void esimd_gemv_fp8_qk_norm_rope_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
+                                    at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
+                                    int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters,
+                                    at::Tensor row_ss, double row_eps);
+
 at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
                                at::Tensor output);
 

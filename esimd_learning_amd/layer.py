@@ -33,6 +33,17 @@ and scales, and esimd_gemm_fp8_a8w8 (esimd_gemm_fp8_a8w8_gelu_and_mul for
 gate/up) consumes them (the hidden input is then
 only read, not overwritten with the normed value).  Needs e4m3 weights.
 
+With ``defer_norm`` (up to four rows, e4m3 weights, fp16/bf16 hand-offs,
+``fuse_tails`` and ``fuse_glu``) each add+RMSNorm is split across the two
+GEMVs around it instead of running as a launch of its own: the producer
+GEMV (o_proj; in ``forward``, also the down projection of every layer but
+the last, for the next layer's input norm) adds its output into the
+residual, writes residual * w and per-16-column sums of squares, and the
+consumer (gate/up, the next layer's QKV) scales its rows by the 1 / rms
+those sums give (esimd_gemv_fp8_add_rms_norm_defer and the ``_rs`` ops).
+Two launches fewer per layer; the values match the unfused layer to within
+the rounding of the moved 1 / rms, not bit for bit.
+
 The intermediate buffers and counters are allocated once in the
 constructor, so at decode sizes a step enqueues only kernels: it can be
 captured in a HIP graph (``capture``) and replayed, which removes host launch
@@ -47,7 +58,7 @@ import torch
 
 class GemmaDecodeLayer:
     def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False, fuse_glu=True,
-                 fuse_norm=False, fuse_tails=True):
+                 fuse_norm=False, fuse_tails=True, defer_norm=False):
         from . import ops as _load_ops
         self.ops = _load_ops()
         p = params
@@ -75,6 +86,15 @@ class GemmaDecodeLayer:
         self.r_mid = mk(self.hidden)            # r1 between the two fused norms
         self.fuse_tails = fuse_tails and not act_fp8 and not self.fuse_norm
         self.cnt_rope = self.ops.gemv_tail_counters(self.nq, self.nk, device)
+        e4m3 = all(w.dtype == torch.float8_e4m3fn for w in (self.Wqkv, self.Wo, self.Wgu, self.Wd))
+        # the shapes the deferred-norm kernels take (else the unfused step)
+        kib = lambda k: k % 1024 == 0 and k // 1024 in (2, 3, 4, 5, 14, 24)  # noqa: E731
+        shapes = (self.hidden in (3072, 4096, 5120) and kib(self.nq * self.hd) and kib(self.mlp)
+                  and self.hd in (128, 256) and nqkv % 16 == 0 and self.mlp % 16 == 0)
+        self.defer_norm = defer_norm and M <= 4 and e4m3 and self.fuse_tails and fuse_glu and shapes
+        if self.defer_norm:
+            ss = lambda: torch.empty(M, self.hidden // 16, dtype=torch.float32, device=device)  # noqa: E731
+            self.ss_o, self.ss_d = ss(), ss()    # after o_proj; after down (the next layer's input norm)
         if act_fp8:
             if self.Wqkv.dtype != torch.float8_e4m3fn or self.Wgu.dtype != torch.float8_e4m3fn:
                 raise ValueError("act_fp8 needs e4m3 weights")
@@ -87,11 +107,21 @@ class GemmaDecodeLayer:
     def weight_bytes(self):
         return sum(w.numel() for w in (self.Wqkv, self.Wo, self.Wgu, self.Wd))
 
-    def step(self, hidden, residual, positions):
-        """hidden, residual: [M, hidden] (residual updated in place); returns out."""
+    def step(self, hidden, residual, positions, ss_in=None, next_norm=None):
+        """hidden, residual: [M, hidden] (residual updated in place); returns out.
+
+        defer_norm only: with ``ss_in`` (the previous layer's ss_d) hidden
+        already holds residual * w_in of the previous layer's deferred input
+        norm of this layer and residual its sum; with ``next_norm`` (the next
+        layer's w_in) the down projection produces that for the next layer
+        and ss_d."""
         o, hd, nq, nk = self.ops, self.hd, self.nq, self.nk
         if self.fuse_norm:
             return self._step_fused(hidden, residual, positions)
+        if self.defer_norm:
+            return self._step_defer(hidden, residual, positions, ss_in, next_norm)
+        if ss_in is not None or next_norm is not None:
+            raise ValueError("ss_in / next_norm need defer_norm")
         if self.act_fp8:
             o.esimd_fused_add_rms_norm_quant_fp8(hidden, residual, self.w_in, self.eps, self.q8, self.s8)
             o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wqkv8, self.sqkv32, self.qkv)
@@ -150,6 +180,24 @@ class GemmaDecodeLayer:
         o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
         return self.out
 
+    def _step_defer(self, hidden, residual, positions, ss_in, next_norm):
+        o, hd, nq, nk, eps = self.ops, self.hd, self.nq, self.nk, self.eps
+        if ss_in is None:
+            o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, eps)
+            o.esimd_gemv_fp8_qk_norm_rope(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
+                                          nq, nk, eps, self.theta, True, self.cnt_rope)
+        else:
+            o.esimd_gemv_fp8_qk_norm_rope_rs(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
+                                             nq, nk, eps, self.theta, True, self.cnt_rope, ss_in, eps)
+        self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
+        o.esimd_gemv_fp8_add_rms_norm_defer(self.attn, self.Wo, self.so, residual, self.w_post, self.o, self.ss_o)
+        o.esimd_gemv_fp8_gelu_and_mul_rs(self.o, self.Wgu, self.sgu, self.act, self.ss_o, eps)
+        if next_norm is None:
+            o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
+        else:
+            o.esimd_gemv_fp8_add_rms_norm_defer(self.act, self.Wd, self.sd, residual, next_norm, self.out, self.ss_d)
+        return self.out
+
     def capture(self, hidden, residual, positions, stream=None):
         """Capture one step on fixed input buffers in a HIP graph; replay with replay()."""
         s = stream or torch.cuda.Stream()
@@ -169,10 +217,20 @@ def forward(layers, hidden, residual, positions):
     """A decode forward over `layers` in sequence: each layer's output buffer
     is the next layer's hidden state (which that layer's first norm
     overwrites), and the residual stream is updated in place by every layer.
-    Returns the last layer's output buffer."""
-    h = hidden
-    for layer in layers:
-        h = layer.step(h, residual, positions)
+    Between two ``defer_norm`` layers the next layer's input norm is
+    deferred across the down projection and its QKV GEMV.  Returns the last
+    layer's output buffer (for a deferred pair as for any other: the down
+    projection's output is only the normed input of the next layer, the
+    last layer's is the plain one)."""
+    h, ss = hidden, None
+    for i, layer in enumerate(layers):
+        nxt = layers[i + 1] if i + 1 < len(layers) else None
+        chain = nxt is not None and layer.defer_norm and nxt.defer_norm
+        if layer.defer_norm:
+            h = layer.step(h, residual, positions, ss_in=ss, next_norm=nxt.w_in if chain else None)
+        else:
+            h = layer.step(h, residual, positions)
+        ss = layer.ss_d if chain else None
     return h
 
 

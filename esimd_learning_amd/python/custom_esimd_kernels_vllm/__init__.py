@@ -28,6 +28,10 @@ from custom_esimd_kernels_vllm.ops import (  # noqa: F401
     esimd_qk_norm_rope,
     esimd_gemv_fp8_qk_norm_rope,
     gemv_tail_counters,
+    esimd_gemv_fp8_add_rms_norm_defer,
+    esimd_gemv_fp8_pern_rs,
+    esimd_gemv_fp8_gelu_and_mul_rs,
+    esimd_gemv_fp8_qk_norm_rope_rs,
     esimd_gemm_fp8_a8w8,
     esimd_gemm_fp8_a8w8_gelu_and_mul,
 )

@@ -166,6 +166,49 @@ def esimd_gemv_fp8_qk_norm_rope(
                                      eps, theta, is_neox, counters)
 
 
+def esimd_gemv_fp8_add_rms_norm_defer(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, residual: torch.Tensor,
+    norm_weight: torch.Tensor, output: torch.Tensor, row_ss: torch.Tensor,
+) -> None:
+    """The producer half of an add + RMSNorm deferred into the next GEMV
+    (up to four rows, e4m3 weights): o = the GEMV's rounded output; residual
+    += o in place; output = residual * norm_weight (rounded; the norm
+    without its 1 / rms); row_ss [M, N / 16] fp32 = the sums of squares of
+    the unrounded o + residual over each 16 columns.  Feed output and row_ss
+    to a ``*_rs`` op, which applies rsqrt(sum(row_ss[m]) / N + eps)."""
+    _ops.esimd_gemv_fp8_add_rms_norm_defer(input, weight, weight_scale, residual, norm_weight, output, row_ss)
+
+
+def esimd_gemv_fp8_pern_rs(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
+    row_ss: torch.Tensor, eps: float,
+) -> None:
+    """esimd_gemv_fp8_pern with each output row m scaled by
+    rsqrt(sum(row_ss[m]) / K + eps) (the deferred norm's consumer)."""
+    _ops.esimd_gemv_fp8_pern_rs(input, weight, weight_scale, output, row_ss, eps)
+
+
+def esimd_gemv_fp8_gelu_and_mul_rs(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
+    row_ss: torch.Tensor, eps: float,
+) -> None:
+    """esimd_gemv_fp8_gelu_and_mul with the gate and up rows scaled by the
+    deferred norm's rsqrt(sum(row_ss[m]) / K + eps) before gelu_and_mul."""
+    _ops.esimd_gemv_fp8_gelu_and_mul_rs(input, weight, weight_scale, output, row_ss, eps)
+
+
+def esimd_gemv_fp8_qk_norm_rope_rs(
+    input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
+    q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor, n_q: int, n_k: int,
+    eps: float, theta: float, is_neox: bool, counters: torch.Tensor, row_ss: torch.Tensor, row_eps: float,
+) -> None:
+    """esimd_gemv_fp8_qk_norm_rope with the GEMV's rows scaled by the
+    deferred norm's rsqrt(sum(row_ss[m]) / K + row_eps) before QK-norm and
+    RoPE."""
+    _ops.esimd_gemv_fp8_qk_norm_rope_rs(input, weight, weight_scale, output, q_weight, k_weight, positions, n_q,
+                                        n_k, eps, theta, is_neox, counters, row_ss, row_eps)
+
+
 def esimd_gemm_fp8_a8w8(
     a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
     output: torch.Tensor,

@@ -257,6 +257,44 @@ int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, v
                               int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
 
 /*
+ * NEW: an add + RMSNorm deferred across the GEMV that produces its input
+ * and the GEMV that consumes its output (no counterpart in the reference:
+ * there it is esimd_gemv_fp8_pern, csrc/xpu/esimd_kernel.sycl:22-53, then
+ * esimd_fused_add_rms_norm_batched, :92-120, then the next GEMV).
+ *
+ * Producer, cek_gemv_fp8_add_rms_norm_defer: o = the GEMV's rounded output
+ * [M, N]; s = o + residual (fp32); residual = round(s) in place;
+ * y = round(residual * norm_weight[n]) -- the norm without its 1 / rms --
+ * and ss_out [M][N / 16] = sum over each 16 columns of s^2.  y, residual and
+ * ss_out must not overlap each other, x or w.
+ *
+ * Consumers (_rs): the named op over x = the producer's y, with each output
+ * row m scaled, before rounding (and before gelu_and_mul, QK-norm and RoPE),
+ * by inv[m] = rsqrt(sum_j row_ss[m][j] / K + row_eps); n_ss = the producer's
+ * N / 16 (<= 256, a multiple of 4, row_ss 16-byte aligned), summed in a fixed order.  The result equals the unfused
+ * norm -> GEMV to within the rounding of the moved 1 / rms (not bit for bit).
+ *
+ * All: M <= 4, K a multiple of 1024 (producer and plain consumer: K / 1024
+ * in {2, 3, 4, 5, 14, 24}; gate/up and QKV: 3072, 4096, 5120), N % 16 == 0,
+ * e4m3 weights, 16-byte aligned x and w; CEK_ERR_UNSUPPORTED otherwise (no
+ * fallback: run the unfused ops).
+ */
+int cek_gemv_fp8_add_rms_norm_defer(const void* x, const void* w, const void* scale, void* residual,
+                                    const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N, int64_t K,
+                                    int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+int cek_gemv_fp8_pern_rs(const void* x, const void* w, const void* scale, void* y, const float* row_ss, int64_t n_ss,
+                         float row_eps, int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype,
+                         void* stream);
+int cek_gemv_fp8_gelu_and_mul_rs(const void* x, const void* w, const void* scale, void* y, const float* row_ss,
+                                 int64_t n_ss, float row_eps, int64_t M, int64_t d, int64_t K, int io_dtype,
+                                 int fp8_fmt, int scale_dtype, void* stream);
+int cek_gemv_fp8_qk_norm_rope_rs(const void* x, const void* w, const void* scale, void* y, const void* q_weight,
+                                 const void* k_weight, const int64_t* positions, int64_t n_q, int64_t n_k,
+                                 int64_t head_dim, float eps, float theta, int is_neox, int* counters,
+                                 const float* row_ss, int64_t n_ss, float row_eps, int64_t M, int64_t N, int64_t K,
+                                 int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+
+/*
  * NEW: per-head RMSNorm (weight qw / kw of length head_dim, Gemma w+1) then
  * rotary embedding, in place on q [T, n_q * head_dim] and
  * k [T, n_k * head_dim] (row strides q_stride / k_stride elements, so both

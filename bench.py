@@ -427,13 +427,15 @@ def bench_small_ops(ops, torch, reps=200):
     return rows
 
 
-# Decoder-step variants timed side by side: the default step (gelu_and_mul in
-# the gate/up GEMV's epilogue, QK-norm+RoPE in the QKV GEMV's last workgroup
-# of each head), the same with QK-norm+RoPE as its own launch,
-# the e4m3 hand-off, every op its own launch, the add+RMSNorms in the GEMV
-# prologues, and the add+RMSNorms deferred across the GEMVs around them.
+# Decoder-step variants timed side by side: the default step (add+RMSNorms
+# deferred across the GEMVs around them, gelu_and_mul in the gate/up GEMV's
+# epilogue, QK-norm+RoPE and the attention stand-in's copy of q in the QKV
+# GEMV's last workgroup of each head), the same with the norms as launches of
+# their own (equal to the separate ops bit for bit), with QK-norm+RoPE as its
+# own launch too, the e4m3 hand-off, every op its own launch, and the
+# add+RMSNorms in the GEMV prologues.
 LAYER_VARIANTS = {"us_per_step": dict(),
-                  "defer_norm_us_per_step": dict(defer_norm=True),
+                  "no_defer_us_per_step": dict(defer_norm=False),
                   "no_tails_us_per_step": dict(fuse_tails=False),
                   "act_fp8_us_per_step": dict(act_fp8=True),
                   "unfused_us_per_step": dict(fuse_glu=False, fuse_tails=False),

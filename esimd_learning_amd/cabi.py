@@ -42,13 +42,13 @@ SIGNATURES = {
     "cek_add_rms_norm_gemv_fp8": (_i, [_p, _p, _p, _f, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _i,
                                        _p]),
     "cek_qk_norm_rope": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f, _f, _i, _i, _p]),
-    "cek_gemv_fp8_qk_norm_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _i64, _i64,
+    "cek_gemv_fp8_qk_norm_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _p, _i64, _i64,
                                        _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_add_rms_norm_defer": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_pern_rs": (_i, [_p, _p, _p, _p, _p, _i64, _f, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_gelu_and_mul_rs": (_i, [_p, _p, _p, _p, _p, _i64, _f, _i64, _i64, _i64, _i, _i, _i, _p]),
-    "cek_gemv_fp8_qk_norm_rope_rs": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _p, _i64, _f,
-                                          _i64, _i64, _i64, _i, _i, _i, _p]),
+    "cek_gemv_fp8_qk_norm_rope_rs": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _p, _p,
+                                          _i64, _f, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_hbm_read_probe": (_i, [_p, _i64, _p, _p]),
 }
 

@@ -71,6 +71,7 @@ struct TailArgs {
   int nq, nk;             // ROPE: heads q then k at output columns [0, (nq + nk) hd)
   float eps, theta;
   int neox;
+  uint16_t* qcopy;        // ROPE: optional [M, nq hd] copy of the rotated q heads
 };
 
 struct NormArgs {
@@ -594,6 +595,11 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
       if (m < M) {
         *reinterpret_cast<u4*>(v + 8 * c) = oa;
         *reinterpret_cast<u4*>(v + HALF + 8 * c) = ob;
+        if (ta.qcopy && head < ta.nq) {
+          uint16_t* qv = ta.qcopy + (size_t)m * ta.nq * HD + (size_t)head * HD;
+          *reinterpret_cast<u4*>(qv + 8 * c) = oa;
+          *reinterpret_cast<u4*>(qv + HALF + 8 * c) = ob;
+        }
       }
     }
   }
@@ -1540,8 +1546,15 @@ int launch_gemv_tail(const void* x, const void* w, const void* scale, int skind,
   if (N * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
   if (M > 4 || (K != 3072 && K != 4096 && K != 5120) || fp8_fmt != CEK_E4M3 || N % 16 != 0) return CEK_ERR_UNSUPPORTED;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16)) return CEK_ERR_UNSUPPORTED;
-  // the output is re-read by the tail: it must not share memory with the inputs
+  // the output is re-read by the tail: it must not share memory with the
+  // inputs, nor with the q copy that other heads' tails write meanwhile
   if (overlaps(y, M * N * 2, x, M * K * 2) || overlaps(y, M * N * 2, w, N * K)) return CEK_ERR_UNSUPPORTED;
+  if (na.tail.qcopy) {
+    const int64_t qb = M * na.tail.nq * 16 * tp * 2;
+    if (overlaps(na.tail.qcopy, qb, y, M * N * 2) || overlaps(na.tail.qcopy, qb, x, M * K * 2) ||
+        overlaps(na.tail.qcopy, qb, w, N * K))
+      return CEK_ERR_UNSUPPORTED;
+  }
   GemvSegs sg{};
   sg.count = 1;
   sg.w[0] = static_cast<const uint8_t*>(w);
@@ -1694,8 +1707,8 @@ namespace cek {
 // The checks and tail arguments shared by the two QKV + q/k-norm + rope entry
 // points; CEK_OK when the launch may go ahead with na.
 static int qk_rope_args(const void* q_weight, const void* k_weight, const int64_t* positions, int64_t n_q,
-                        int64_t n_k, int64_t head_dim, float eps, float theta, int is_neox, int* counters, int64_t M,
-                        int64_t N, NormArgs& na) {
+                        int64_t n_k, int64_t head_dim, float eps, float theta, int is_neox, int* counters,
+                        void* q_out, int64_t M, int64_t N, NormArgs& na) {
   if (M < 0 || N < 0 || n_q < 0 || n_k < 0 || head_dim <= 0 || !(theta > 0.f)) return CEK_ERR_INVALID;
   if ((n_q + n_k) * head_dim > N) return CEK_ERR_INVALID;
   if (M > 0 && N > 0 && (!positions || (n_q > 0 && !q_weight) || (n_k > 0 && !k_weight))) return CEK_ERR_INVALID;
@@ -1711,6 +1724,10 @@ static int qk_rope_args(const void* q_weight, const void* k_weight, const int64_
   na.tail.eps = eps;
   na.tail.theta = theta;
   na.tail.neox = is_neox != 0;
+  if (q_out && n_q > 0 && M > 0) {
+    if (!aligned(q_out, 16)) return CEK_ERR_UNSUPPORTED;
+    na.tail.qcopy = static_cast<uint16_t*>(q_out);
+  }
   return CEK_OK;
 }
 }  // namespace cek
@@ -1718,11 +1735,11 @@ static int qk_rope_args(const void* q_weight, const void* k_weight, const int64_
 extern "C" int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, void* y,
                                          const void* q_weight, const void* k_weight, const int64_t* positions,
                                          int64_t n_q, int64_t n_k, int64_t head_dim, float eps, float theta,
-                                         int is_neox, int* counters, int64_t M, int64_t N, int64_t K, int io_dtype,
-                                         int fp8_fmt, int scale_dtype, void* stream) {
+                                         int is_neox, int* counters, void* q_out, int64_t M, int64_t N, int64_t K,
+                                         int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
   cek::NormArgs na{};
   const int rc = cek::qk_rope_args(q_weight, k_weight, positions, n_q, n_k, head_dim, eps, theta, is_neox, counters,
-                                   M, N, na);
+                                   q_out, M, N, na);
   if (rc != CEK_OK || (head_dim != 128 && head_dim != 256)) return rc;
   return cek::launch_gemv_tail(x, w, scale, cek::scale_kind(scale_dtype), y, M, N, K, io_dtype, fp8_fmt,
                                cek::TAIL_ROPE, (int)(head_dim / 16), na, (hipStream_t)stream);
@@ -1731,12 +1748,12 @@ extern "C" int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const voi
 extern "C" int cek_gemv_fp8_qk_norm_rope_rs(const void* x, const void* w, const void* scale, void* y,
                                             const void* q_weight, const void* k_weight, const int64_t* positions,
                                             int64_t n_q, int64_t n_k, int64_t head_dim, float eps, float theta,
-                                            int is_neox, int* counters, const float* row_ss, int64_t n_ss,
-                                            float row_eps, int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt,
-                                            int scale_dtype, void* stream) {
+                                            int is_neox, int* counters, void* q_out, const float* row_ss,
+                                            int64_t n_ss, float row_eps, int64_t M, int64_t N, int64_t K,
+                                            int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
   cek::NormArgs na{};
-  int rc = cek::qk_rope_args(q_weight, k_weight, positions, n_q, n_k, head_dim, eps, theta, is_neox, counters, M, N,
-                             na);
+  int rc = cek::qk_rope_args(q_weight, k_weight, positions, n_q, n_k, head_dim, eps, theta, is_neox, counters, q_out,
+                             M, N, na);
   if (rc != CEK_OK || (head_dim != 128 && head_dim != 256)) return rc;
   if (M == 0 || N == 0) return CEK_OK;
   rc = cek::rowscale_args(row_ss, n_ss, row_eps, M, na);

@@ -495,9 +495,22 @@ static int scale_code_of(const at::Tensor& scale, int64_t N, const char* op) {
   return st == at::ScalarType::Float ? CEK_F32 : (st == at::ScalarType::Half ? CEK_F16 : CEK_BF16);
 }
 
+// q_out (optional, [M, n_q hd] of the input's dtype): also receives the
+// rotated q heads, as a copy of output's q columns would.
+static void* check_q_out(const c10::optional<at::Tensor>& q_out, const at::Tensor& input, int64_t M, int64_t n_q,
+                         int64_t hd, const char* op) {
+  if (!q_out.has_value() || !q_out->defined()) return nullptr;
+  TORCH_CHECK(q_out->scalar_type() == input.scalar_type(), op, ": q_out must have the input's dtype");
+  check_device(*q_out, input, op, "q_out");
+  check_contig(*q_out, op, "q_out");
+  TORCH_CHECK(q_out->numel() == M * n_q * hd, op, ": q_out must be [M, n_q * head_dim]");
+  return q_out->data_ptr();
+}
+
 void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
                                  at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
-                                 int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters) {
+                                 int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters,
+                                 c10::optional<at::Tensor> q_out) {
   const char* op = "esimd_gemv_fp8_qk_norm_rope";
   check_gemv_io(input, output, op);
   check_fp8_weight(weight, op);
@@ -524,6 +537,7 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
               ": q_weight and k_weight must both have head_dim (even, <= 512) elements");
   TORCH_CHECK(n_q >= 0 && n_k >= 0 && (n_q + n_k) * hd <= N, op, ": the q and k heads must fit in the output row");
   check_counters(counters, input, 64 * (n_q + n_k), op);
+  void* qo = check_q_out(q_out, input, M, n_q, hd, op);
   const int scale_code = scale_code_of(weight_scale, N, op);
   c10::OptionalDeviceGuard guard(input.device());
   void* st = current_stream(input);
@@ -531,7 +545,7 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
   const int rc = cek_gemv_fp8_qk_norm_rope(
       input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(), output.data_ptr(), q_weight.data_ptr(),
       k_weight.data_ptr(), static_cast<const int64_t*>(positions.data_ptr()), n_q, n_k, hd, (float)eps, (float)theta,
-      is_neox ? 1 : 0, static_cast<int*>(counters.data_ptr()), M, N, K, io, fp8_code(weight), scale_code, st);
+      is_neox ? 1 : 0, static_cast<int*>(counters.data_ptr()), qo, M, N, K, io, fp8_code(weight), scale_code, st);
   if (rc != CEK_ERR_UNSUPPORTED) {
     check_rc(rc, op);
     return;
@@ -543,6 +557,7 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
                             static_cast<const int64_t*>(positions.data_ptr()), M, n_q, n_k, hd, N, N, (float)eps,
                             (float)theta, is_neox ? 1 : 0, io, st),
            op);
+  if (qo) q_out->view({M, n_q * hd}).copy_(output.view({M, N}).narrow(1, 0, n_q * hd));
 }
 
 // Deferred RMSNorm between two decode GEMVs (up to four rows, e4m3
@@ -644,7 +659,7 @@ void esimd_gemv_fp8_gelu_and_mul_rs(at::Tensor input, at::Tensor weight, at::Ten
 void esimd_gemv_fp8_qk_norm_rope_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
                                     at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
                                     int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters,
-                                    at::Tensor row_ss, double row_eps) {
+                                    at::Tensor row_ss, double row_eps, c10::optional<at::Tensor> q_out) {
   const char* op = "esimd_gemv_fp8_qk_norm_rope_rs";
   int64_t M, N, K;
   check_defer_common(input, weight, weight_scale, output, op, M, N, K);
@@ -662,12 +677,13 @@ void esimd_gemv_fp8_qk_norm_rope_rs(at::Tensor input, at::Tensor weight, at::Ten
   TORCH_CHECK(n_q >= 0 && n_k >= 0 && (n_q + n_k) * hd <= N, op, ": the q and k heads must fit in the output row");
   check_counters(counters, input, 64 * (n_q + n_k), op);
   check_row_ss(row_ss, input, M, op);
+  void* qo = check_q_out(q_out, input, M, n_q, hd, op);
   const int scale_code = scale_code_of(weight_scale, N, op);
   c10::OptionalDeviceGuard guard(input.device());
   check_rc(cek_gemv_fp8_qk_norm_rope_rs(
                input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(), output.data_ptr(), q_weight.data_ptr(),
                k_weight.data_ptr(), static_cast<const int64_t*>(positions.data_ptr()), n_q, n_k, hd, (float)eps,
-               (float)theta, is_neox ? 1 : 0, static_cast<int*>(counters.data_ptr()),
+               (float)theta, is_neox ? 1 : 0, static_cast<int*>(counters.data_ptr()), qo,
                static_cast<const float*>(row_ss.data_ptr()), row_ss.size(1), (float)row_eps, M, N, K,
                io_code(input.scalar_type()), fp8_code(weight), scale_code, current_stream(input)),
            op);

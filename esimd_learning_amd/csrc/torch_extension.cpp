@@ -60,7 +60,7 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
 
   m.def("esimd_gemv_fp8_qk_norm_rope(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "
         "Tensor q_weight, Tensor k_weight, Tensor positions, int n_q, int n_k, float eps, float theta, "
-        "bool is_neox, Tensor(b!) counters) -> ()");
+        "bool is_neox, Tensor(b!) counters, Tensor(c!)? q_out=None) -> ()");
   m.impl("esimd_gemv_fp8_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope);
 
   m.def("esimd_gemv_fp8_add_rms_norm_defer(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) residual, "
@@ -77,7 +77,7 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
 
   m.def("esimd_gemv_fp8_qk_norm_rope_rs(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "
         "Tensor q_weight, Tensor k_weight, Tensor positions, int n_q, int n_k, float eps, float theta, "
-        "bool is_neox, Tensor(b!) counters, Tensor row_ss, float row_eps) -> ()");
+        "bool is_neox, Tensor(b!) counters, Tensor row_ss, float row_eps, Tensor(c!)? q_out=None) -> ()");
   m.impl("esimd_gemv_fp8_qk_norm_rope_rs", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope_rs);
 }
 

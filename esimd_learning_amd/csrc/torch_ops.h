@@ -57,7 +57,8 @@ void esimd_qk_norm_rope(at::Tensor q, at::Tensor k, at::Tensor q_weight, at::Ten
 // the last workgroup of each head.
 void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
                                  at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
-                                 int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters);
+                                 int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters,
+                                 c10::optional<at::Tensor> q_out);
 
 // Deferred RMSNorm between two decode GEMVs: the producer (residual add,
 // norm weight, per-tile sums of squares) and the row-scaled consumers.
@@ -71,7 +72,7 @@ void esimd_gemv_fp8_gelu_and_mul_rs(at::Tensor input, at::Tensor weight, at::Ten
 void esimd_gemv_fp8_qk_norm_rope_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
                                     at::Tensor q_weight, at::Tensor k_weight, at::Tensor positions, int64_t n_q,
                                     int64_t n_k, double eps, double theta, bool is_neox, at::Tensor counters,
-                                    at::Tensor row_ss, double row_eps);
+                                    at::Tensor row_ss, double row_eps, c10::optional<at::Tensor> q_out);
 
 at::Tensor esimd_gemm_fp8_a8w8(at::Tensor a, at::Tensor a_scale, at::Tensor b, at::Tensor b_scale,
                                at::Tensor output);

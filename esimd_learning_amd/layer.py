@@ -4,7 +4,7 @@
     qkv    = h1 @ Wqkv^T * sqkv                           esimd_gemv_fp8_pern
                                    (the two as one launch: esimd_fused_add_rms_norm_gemv_fp8)
     q, k   = per-head RMSNorm + RoPE (in place in qkv)     esimd_qk_norm_rope
-    a      = attention(q, k, v)        -- out of scope: q stands in for its output
+    a      = attention(q, k, v)        -- out of scope: a copy of q stands in for its output
     o      = a @ Wo^T * so                                esimd_gemv_fp8_pern
     h2, r2 = add_rmsnorm(o, r1, w_post)                   esimd_fused_add_rms_norm_batched
     g      = gelu_tanh(h2 @ Wg^T * sg) * (h2 @ Wu^T * su) esimd_gemv_fp8_gelu_and_mul
@@ -23,8 +23,9 @@ workgroups of QKV and gate/up costs more than the norm launch it saves.
 
 With ``fuse_tails`` (the default; fp16/bf16 hand-offs, no ``fuse_norm``)
 QK-norm+RoPE runs in the QKV GEMV (esimd_gemv_fp8_qk_norm_rope: per head,
-the workgroup that finishes the head's rows last) -- one launch fewer per
-step, the same values bit for bit.  Its arrival counters are allocated
+the workgroup that finishes the head's rows last), which also writes the
+rotated q heads into the attention stand-in's output -- two launches fewer
+per step, the same values bit for bit.  Its arrival counters are allocated
 (zeroed) once here and left zero by every call.
 
 With ``act_fp8=True`` the two norm -> GEMV hand-offs carry e4m3 activations
@@ -33,8 +34,9 @@ and scales, and esimd_gemm_fp8_a8w8 (esimd_gemm_fp8_a8w8_gelu_and_mul for
 gate/up) consumes them (the hidden input is then
 only read, not overwritten with the normed value).  Needs e4m3 weights.
 
-With ``defer_norm`` (up to four rows, e4m3 weights, fp16/bf16 hand-offs,
-``fuse_tails`` and ``fuse_glu``) each add+RMSNorm is split across the two
+With ``defer_norm`` (the default where it applies: up to four rows, e4m3
+weights, fp16/bf16 hand-offs, ``fuse_tails`` and ``fuse_glu``, the shapes
+the kernels take) each add+RMSNorm is split across the two
 GEMVs around it instead of running as a launch of its own: the producer
 GEMV (o_proj; in ``forward``, also the down projection of every layer but
 the last, for the next layer's input norm) adds its output into the
@@ -42,7 +44,8 @@ residual, writes residual * w and per-16-column sums of squares, and the
 consumer (gate/up, the next layer's QKV) scales its rows by the 1 / rms
 those sums give (esimd_gemv_fp8_add_rms_norm_defer and the ``_rs`` ops).
 Two launches fewer per layer; the values match the unfused layer to within
-the rounding of the moved 1 / rms, not bit for bit.
+the rounding of the moved 1 / rms, not bit for bit (``defer_norm=False``
+gives the step that equals the separate ops bit for bit).
 
 The intermediate buffers and counters are allocated once in the
 constructor, so at decode sizes a step enqueues only kernels: it can be
@@ -58,7 +61,7 @@ import torch
 
 class GemmaDecodeLayer:
     def __init__(self, params, M, device="cuda:0", dtype=torch.float16, act_fp8=False, fuse_glu=True,
-                 fuse_norm=False, fuse_tails=True, defer_norm=False):
+                 fuse_norm=False, fuse_tails=True, defer_norm=True):
         from . import ops as _load_ops
         self.ops = _load_ops()
         p = params
@@ -127,15 +130,15 @@ class GemmaDecodeLayer:
             o.esimd_gemm_fp8_a8w8(self.q8.view(torch.uint8), self.s8, self.Wqkv8, self.sqkv32, self.qkv)
         else:
             o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, self.eps)
-            if self.fuse_tails:
+            if self.fuse_tails:   # the tail also writes the attention stand-in's output
                 o.esimd_gemv_fp8_qk_norm_rope(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
-                                              nq, nk, self.eps, self.theta, True, self.cnt_rope)
+                                              nq, nk, self.eps, self.theta, True, self.cnt_rope, self.attn)
             else:
                 o.esimd_gemv_fp8_pern(hidden, self.Wqkv, self.sqkv, self.qkv, self.Wqkv.shape[0], self.hidden)
         if not self.fuse_tails:
             o.esimd_qk_norm_rope(self.qkv[:, : nq * hd], self.qkv[:, nq * hd:(nq + nk) * hd], self.qw, self.kw,
                                  positions, self.eps, self.theta, True)
-        self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
+            self.attn.copy_(self.qkv[:, : nq * hd])                # attention stand-in
         o.esimd_gemv_fp8_pern(self.attn, self.Wo, self.so, self.o, self.hidden, nq * hd)
         if self.act_fp8:
             o.esimd_fused_add_rms_norm_quant_fp8(self.o, residual, self.w_post, self.eps, self.q8, self.s8)
@@ -185,11 +188,10 @@ class GemmaDecodeLayer:
         if ss_in is None:
             o.esimd_fused_add_rms_norm_batched(hidden, residual, self.w_in, eps)
             o.esimd_gemv_fp8_qk_norm_rope(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
-                                          nq, nk, eps, self.theta, True, self.cnt_rope)
+                                          nq, nk, eps, self.theta, True, self.cnt_rope, self.attn)
         else:
             o.esimd_gemv_fp8_qk_norm_rope_rs(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
-                                             nq, nk, eps, self.theta, True, self.cnt_rope, ss_in, eps)
-        self.attn.copy_(self.qkv[:, : nq * hd])                    # attention stand-in
+                                             nq, nk, eps, self.theta, True, self.cnt_rope, ss_in, eps, self.attn)
         o.esimd_gemv_fp8_add_rms_norm_defer(self.attn, self.Wo, self.so, residual, self.w_post, self.o, self.ss_o)
         o.esimd_gemv_fp8_gelu_and_mul_rs(self.o, self.Wgu, self.sgu, self.act, self.ss_o, eps)
         if next_norm is None:

@@ -155,15 +155,17 @@ def esimd_gemv_fp8_qk_norm_rope(
     input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
     q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor, n_q: int, n_k: int,
     eps: float, theta: float = 10000.0, is_neox: bool = True, counters: torch.Tensor = None,
+    q_out: torch.Tensor = None,
 ) -> None:
     """The QKV GEMV (esimd_gemv_fp8_pern into output [M, N]) followed by
     esimd_qk_norm_rope on its q columns [0, n_q hd) and k columns
     [n_q hd, (n_q + n_k) hd), in one launch for decode batches.  counters:
     int32 device tensor of >= 64 * (n_q + n_k) elements
     (``gemv_tail_counters``), zero before the first call and left zero by
-    each."""
+    each.  q_out (optional, [M, n_q hd]) also receives the rotated q heads,
+    as a copy of output's q columns would."""
     _ops.esimd_gemv_fp8_qk_norm_rope(input, weight, weight_scale, output, q_weight, k_weight, positions, n_q, n_k,
-                                     eps, theta, is_neox, counters)
+                                     eps, theta, is_neox, counters, q_out)
 
 
 def esimd_gemv_fp8_add_rms_norm_defer(
@@ -201,12 +203,13 @@ def esimd_gemv_fp8_qk_norm_rope_rs(
     input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
     q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor, n_q: int, n_k: int,
     eps: float, theta: float, is_neox: bool, counters: torch.Tensor, row_ss: torch.Tensor, row_eps: float,
+    q_out: torch.Tensor = None,
 ) -> None:
     """esimd_gemv_fp8_qk_norm_rope with the GEMV's rows scaled by the
     deferred norm's rsqrt(sum(row_ss[m]) / K + row_eps) before QK-norm and
     RoPE."""
     _ops.esimd_gemv_fp8_qk_norm_rope_rs(input, weight, weight_scale, output, q_weight, k_weight, positions, n_q,
-                                        n_k, eps, theta, is_neox, counters, row_ss, row_eps)
+                                        n_k, eps, theta, is_neox, counters, row_ss, row_eps, q_out)
 
 
 def esimd_gemm_fp8_a8w8(

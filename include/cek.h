@@ -246,15 +246,18 @@ int cek_gemv_fp8_gelu_and_mul(const void* x, const float* x_scale, const void* w
  * finishes the head's rows last does its norm and rotation; `counters`
  * (64 * (n_q + n_k) ints: one counter per head, 256 bytes apart) must be
  * zero before the first call and are left zero -- calls that may overlap in
- * time need their own.  Covers M <= 4,
+ * time need their own.  q_out (may be null): [M, n_q hd], also receives the
+ * rotated q heads (what a copy of y's q columns gives), written by the same
+ * workgroups; it must not overlap y, x or w.  Covers M <= 4,
  * K in {3072, 4096, 5120}, N % 16 == 0, head_dim 128 or 256, e4m3 weights,
  * 16-byte aligned operands; CEK_ERR_UNSUPPORTED otherwise (run the GEMV,
  * then cek_qk_norm_rope).
  */
 int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, void* y, const void* q_weight,
                               const void* k_weight, const int64_t* positions, int64_t n_q, int64_t n_k,
-                              int64_t head_dim, float eps, float theta, int is_neox, int* counters, int64_t M,
-                              int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+                              int64_t head_dim, float eps, float theta, int is_neox, int* counters, void* q_out,
+                              int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype,
+                              void* stream);
 
 /*
  * NEW: an add + RMSNorm deferred across the GEMV that produces its input
@@ -290,7 +293,7 @@ int cek_gemv_fp8_gelu_and_mul_rs(const void* x, const void* w, const void* scale
                                  int fp8_fmt, int scale_dtype, void* stream);
 int cek_gemv_fp8_qk_norm_rope_rs(const void* x, const void* w, const void* scale, void* y, const void* q_weight,
                                  const void* k_weight, const int64_t* positions, int64_t n_q, int64_t n_k,
-                                 int64_t head_dim, float eps, float theta, int is_neox, int* counters,
+                                 int64_t head_dim, float eps, float theta, int is_neox, int* counters, void* q_out,
                                  const float* row_ss, int64_t n_ss, float row_eps, int64_t M, int64_t N, int64_t K,
                                  int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
 

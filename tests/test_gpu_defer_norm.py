@@ -153,12 +153,14 @@ def test_qk_rope_rs_equals_unfused(ops, dev, M, hd, nq, nk):
     cnt = ops.gemv_tail_counters(nq, nk, dev)
     Wd, sd = W.to(dev), s.to(dev)
     out = torch.full((M, N), float("nan"), dtype=dtype, device=dev)
-    ops.esimd_gemv_fp8_qk_norm_rope_rs(v, Wd, sd, out, qw, kw, pos, nq, nk, EPS, 10000.0, True, cnt, ss, EPS)
+    q_out = torch.full((M, nq * hd), float("nan"), dtype=dtype, device=dev)
+    ops.esimd_gemv_fp8_qk_norm_rope_rs(v, Wd, sd, out, qw, kw, pos, nq, nk, EPS, 10000.0, True, cnt, ss, EPS, q_out)
     ref = torch.empty(M, N, dtype=dtype, device=dev)
     ops.esimd_gemv_fp8_pern_rs(v, Wd, sd, ref, ss, EPS)
     ops.esimd_qk_norm_rope(ref[:, : nq * hd], ref[:, nq * hd:(nq + nk) * hd], qw, kw, pos, EPS, 10000.0, True)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+    assert torch.equal(q_out, ref[:, : nq * hd])
     assert int(cnt.abs().sum()) == 0, "arrival counters must be left zero"
 
 

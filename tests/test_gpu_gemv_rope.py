@@ -62,10 +62,15 @@ def test_gemv_qk_norm_rope(ops, dev, M, K, nq, nk, hd, dt, neox):
     qo, ko = oact.qk_norm_rope(y0[:, : nq * hd].float().numpy(), y0[:, nq * hd:(nq + nk) * hd].float().numpy(),
                                qw.float().numpy(), kw.float().numpy(), pos.numpy(), EPS, 10000.0, neox, hd)
     for call in range(2):
+        # the second call also writes the rotated q heads to q_out (the
+        # fused launch's tail, or a copy after the unfused ops)
         y = torch.full((M, N), float("nan"), dtype=dt, device=dev)
-        ops.esimd_gemv_fp8_qk_norm_rope(xd, Wd, sd, y, qwd, kwd, pd, nq, nk, EPS, 10000.0, neox, cnt)
+        q_out = torch.full((M, nq * hd), float("nan"), dtype=dt, device=dev) if call else None
+        ops.esimd_gemv_fp8_qk_norm_rope(xd, Wd, sd, y, qwd, kwd, pd, nq, nk, EPS, 10000.0, neox, cnt, q_out)
         torch.cuda.synchronize()
         assert int(cnt.abs().sum().item()) == 0, f"counters not zero after call {call}"
+        if call:
+            assert torch.equal(q_out, y[:, : nq * hd]), "q_out differs from the output's q columns"
         if 3 <= M <= 4:
             assert torch.equal(y, y_ref), f"call {call}: output differs from the unfused ops"
         out = y.cpu()
@@ -84,9 +89,10 @@ def test_gemv_qk_norm_rope_graph_replays(ops, dev):
     xd, Wd, sd, qwd, kwd, pd = x.to(dev), W8.to(dev), s.to(dev), qw.to(dev), kw.to(dev), pos.to(dev)
     cnt = ops.gemv_tail_counters(nq, nk, dev)
     qkv = torch.empty(M, N, dtype=dt, device=dev)
+    q_out = torch.empty(M, nq * hd, dtype=dt, device=dev)
 
     def step():
-        ops.esimd_gemv_fp8_qk_norm_rope(xd, Wd, sd, qkv, qwd, kwd, pd, nq, nk, EPS, 10000.0, True, cnt)
+        ops.esimd_gemv_fp8_qk_norm_rope(xd, Wd, sd, qkv, qwd, kwd, pd, nq, nk, EPS, 10000.0, True, cnt, q_out)
 
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
@@ -105,8 +111,10 @@ def test_gemv_qk_norm_rope_graph_replays(ops, dev):
         torch.cuda.synchronize()
         eager = qkv.clone()
         qkv.fill_(float("nan"))
+        q_out.fill_(float("nan"))
         gph.replay()
         torch.cuda.synchronize()
         assert torch.equal(qkv, eager), f"replay {rep}"
+        assert torch.equal(q_out, eager[:, : nq * hd]), f"replay {rep}: q_out"
         assert int(cnt.abs().sum().item()) == 0
         torch.randn(1000, device=dev).sum().item()

@@ -72,15 +72,38 @@ def test_decoder_step_graph_replays(ops, dev, act_fp8, fuse_norm, dims):
         torch.randn(1000, device=dev).sum().item()   # unrelated eager work between replays
 
 
+@pytest.mark.parametrize("dims,M", [(CONFIG5, 4), (CONFIG5, 1), (SMALL, 3)])
+def test_decoder_step_default_vs_oracle(ops, dev, dims, M):
+    """The default step -- add+RMSNorms deferred across the GEMVs where the
+    shapes allow (config 5 up to four rows), QK-norm+RoPE and the attention
+    stand-in in the QKV GEMV's tail, gelu_and_mul in the gate/up epilogue --
+    against the oracle."""
+    _say(f"decoder step (default) M={M} {dims}")
+    p = synthetic.gemma_layer(seed=16, **dims)
+    layer = GemmaDecodeLayer(p, M, dev)
+    assert layer.defer_norm == (dims is CONFIG5)
+    h = synthetic.activations(M, dims["hidden"], seed=23)
+    r = synthetic.activations(M, dims["hidden"], seed=24)
+    pos = synthetic.positions(M, seed=25)
+    hd, rd = h.to(dev), r.to(dev)
+    out = layer.step(hd, rd, pos.to(dev)).clone()
+    torch.cuda.synchronize()
+    ref_out, ref_r, _ = olayer.decoder_step(p, h, r, pos)
+    assert_close_fp(rd.cpu(), ref_r.float(), "residual after the layer")
+    assert_close_fp(out.cpu(), ref_out, "layer output")
+    nq = dims["n_q"] * dims["head_dim"]
+    assert torch.equal(layer.attn, layer.qkv[:, :nq]), "attention stand-in = the rotated q heads"
+
+
 def test_decoder_step_tails_equal_separate_ops(ops, dev):
-    """QK-norm+RoPE in the QKV GEMV's last workgroup of each head (the default
-    step) gives the step the separate launch gives, bit for bit; and the step
-    matches the oracle."""
+    """QK-norm+RoPE (and the attention stand-in's copy of q) in the QKV GEMV's
+    last workgroup of each head gives the step the separate launches give,
+    bit for bit; and the step matches the oracle."""
     M, dims = 4, CONFIG5
     p = synthetic.gemma_layer(seed=13, **dims)
     res = []
     for tails in (True, False):
-        layer = GemmaDecodeLayer(p, M, dev, fuse_tails=tails)
+        layer = GemmaDecodeLayer(p, M, dev, fuse_tails=tails, defer_norm=False)
         assert layer.fuse_tails == tails
         h = synthetic.activations(M, dims["hidden"], seed=50)
         r = synthetic.activations(M, dims["hidden"], seed=51)

@@ -1131,8 +1131,10 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   if constexpr (!XF8) {
     // fp16/bf16, M <= 8: activations staged through LDS (contiguous loads
     // of just the M rows); for long K only up to 12288 rows (5-20% faster
-    // there, slower for wider matrices).
-    if (M <= 8 && (SHORT || N <= 12288)) {
+    // there, slower for wider matrices), except at one row (M = 1,
+    // K = 14336: N = 14336 34.0 against 38.2 us, N = 28672 61.7 against
+    // 66.7 us).
+    if (M <= 8 && (SHORT || N <= 12288 || M == 1)) {
       if (M <= 4) CEK_LDS_TPW(1, (S >= 3 ? 3 : 2), 4, true);
       else CEK_LDS_TPW(1, 2, 8, false);
       return true;
@@ -1340,10 +1342,13 @@ static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bo
   int N = 0;  // launch shape is chosen from the total row count
   for (int i = 0; i < sg.count; ++i) N += sg.n[i];
   // The LDS-staged MFMA kernel from three rows on (measured faster than the
-  // v_dot2 kernel there, and than the direct MFMA kernel throughout); from two
-  // rows on for K >= 14336, whose v_dot2 workgroups re-read long activation
-  // rows.
-  const int m_lds = K >= 14336 ? 2 : 3;
+  // v_dot2 kernel there, and than the direct MFMA kernel throughout); from one
+  // row on for K >= 14336, whose v_dot2 workgroups re-read long activation
+  // rows (M = 1, K = 14336, N = 4096: 11.54 -> 11.06 us).  The choice depends
+  // on M and K only, so a multi-matrix launch runs the kernel family that
+  // each matrix alone would (the LDS forms it may pick between agree bit for
+  // bit).
+  const int m_lds = K >= 14336 ? 1 : 3;
   if (vec16 && M >= m_lds && launch_lds<T, TO, FMT, XF8>(x, sg, skind, M, K, N, st)) return check_launch();
   if (M > 16) return CEK_ERR_UNSUPPORTED;
   if (vec16 && M <= 4) {

@@ -27,7 +27,7 @@ def _say(msg):
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("Ns,K", [((4096, 1024, 1024), 3072), ((14336, 14336), 4096), ((512, 512), 2048),
-                                  ((100, 7, 2049), 1024), ((4096,), 14336)])
+                                  ((100, 7, 2049), 1024), ((4096,), 14336), ((8192, 8192), 14336)])
 def test_pern_fused_equals_separate(ops, dev, M, Ns, K):
     _say(f"fused pern M={M} Ns={Ns} K={K}")
     Ws, Ss = zip(*[synthetic.weight_fp8(n, K, seed=n + i) for i, n in enumerate(Ns)])

@@ -852,19 +852,39 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, wr[j], xr[j]);
 
-  if constexpr (EPI == EPI_ROWSCALE) {
-    // the rows' sums in a fixed order: each lane's four, then the wave's
-    // 64 lanes (wave_sum_dpp); wave 0 only, no barrier
-    if (wave_u == 0) {
-      const bool in = 4 * lane < na.nss;
+  // EPI_ROWSCALE: the rows' sums in a fixed order -- each lane's four,
+  // then the wave's 64 lanes (the DPP steps of wave_sum_dpp, the four rows
+  // interleaved) -- and their 1 / rms, in wave 0 (no barrier).  Run where
+  // the row scales are first needed, the first tile's epilogue: the wait
+  // for the partial sums' loads there is long over (at the start of the
+  // K loop it delayed wave 0's first stage by ~1 us at M = 4).
+  auto rowscale_sums = [&]() {
+    if constexpr (EPI == EPI_ROWSCALE) {
+      if (wave_u == 0) {
+        const bool in = 4 * lane < na.nss;
+        float t[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const float t = (rsp[m][0] + rsp[m][1]) + (rsp[m][2] + rsp[m][3]);
-        rinv[m] = rsqrtf(wave_sum_dpp(in && m < M ? t : 0.f) / (float)K + na.eps);
+        for (int m = 0; m < 4; ++m) t[m] = in && m < M ? (rsp[m][0] + rsp[m][1]) + (rsp[m][2] + rsp[m][3]) : 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) t[m] += CEK_DPP_F32(t[m], 0xB1);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) t[m] += CEK_DPP_F32(t[m], 0x4E);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) t[m] += CEK_DPP_F32(t[m], 0x141);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) t[m] += CEK_DPP_F32(t[m], 0x140);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 0)) +
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 16)) +
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 32)) +
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 48));
+          rinv[m] = rsqrtf(sum / (float)K + na.eps);
+        }
+        pick_rs();
       }
-      pick_rs();
     }
-  }
+  };
 
   if constexpr (NORM) {
     // add_rmsnorm_kernel's arithmetic, row by row: s = h + r in fp32, r' =
@@ -1023,6 +1043,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     if constexpr (TPW > 1) {
       if (i % STEPS == STEPS - 1) {  // tile i / STEPS is complete
         uint8_t* redp = smem + 2 * STAGE + XAREA;
+        if (i == STEPS - 1) rowscale_sums();
         if constexpr (GLU) {
           if (i / STEPS == 0) {  // gate tile: keep the rounded values
             lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8 || EPI == EPI_ROWSCALE,
@@ -1053,6 +1074,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       }
     }
   }
+  if constexpr (TPW == 1) rowscale_sums();
   if constexpr (EPI == EPI_ADDNORM)
     lds_reduce_addnorm<T>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
   else if constexpr (TPW == 1)

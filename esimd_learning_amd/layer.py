@@ -92,7 +92,9 @@ class GemmaDecodeLayer:
         e4m3 = all(w.dtype == torch.float8_e4m3fn for w in (self.Wqkv, self.Wo, self.Wgu, self.Wd))
         # the shapes the deferred-norm kernels take (else the unfused step)
         kib = lambda k: k % 1024 == 0 and k // 1024 in (2, 3, 4, 5, 14, 24)  # noqa: E731
-        shapes = (self.hidden in (3072, 4096, 5120) and kib(self.nq * self.hd) and kib(self.mlp)
+        # (hidden: the QKV and gate/up K the consumers take, and at most 256
+        # partial sums per row from the producers, N = hidden)
+        shapes = (self.hidden in (3072, 4096) and kib(self.nq * self.hd) and kib(self.mlp)
                   and self.hd in (128, 256) and nqkv % 16 == 0 and self.mlp % 16 == 0)
         self.defer_norm = defer_norm and M <= 4 and e4m3 and self.fuse_tails and fuse_glu and shapes
         if self.defer_norm:

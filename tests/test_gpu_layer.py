@@ -95,6 +95,25 @@ def test_decoder_step_default_vs_oracle(ops, dev, dims, M):
     assert torch.equal(layer.attn, layer.qkv[:, :nq]), "attention stand-in = the rotated q heads"
 
 
+def test_decoder_step_wide_hidden_runs_undeferred(ops, dev):
+    """hidden = 5120 (320 partial sums per row, above what the deferred-norm
+    consumers take): the layer keeps the norms as launches and steps
+    correctly."""
+    M, dims = 2, dict(hidden=5120, n_q=8, n_kv=4, head_dim=128, mlp=2048)
+    p = synthetic.gemma_layer(seed=17, **dims)
+    layer = GemmaDecodeLayer(p, M, dev)
+    assert not layer.defer_norm
+    h = synthetic.activations(M, dims["hidden"], seed=26)
+    r = synthetic.activations(M, dims["hidden"], seed=27)
+    pos = synthetic.positions(M, seed=28)
+    hd, rd = h.to(dev), r.to(dev)
+    out = layer.step(hd, rd, pos.to(dev)).clone()
+    torch.cuda.synchronize()
+    ref_out, ref_r, _ = olayer.decoder_step(p, h, r, pos)
+    assert_close_fp(rd.cpu(), ref_r.float(), "residual after the layer")
+    assert_close_fp(out.cpu(), ref_out, "layer output")
+
+
 def test_decoder_step_tails_equal_separate_ops(ops, dev):
     """QK-norm+RoPE (and the attention stand-in's copy of q) in the QKV GEMV's
     last workgroup of each head gives the step the separate launches give,

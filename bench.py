@@ -10,12 +10,12 @@ weights in the 256 MB Infinity Cache.  All inputs are resident in HBM before
 the timed region.
 
 Timing: W untimed warm-up steps, then exactly K steps captured in one HIP
-graph (so host launch cost is not measured); the graph is replayed untimed
-for WARM_S seconds (a cold MI355X runs the first replays 7-20% slower while
-its clocks settle), then replayed once, timed, between device
-synchronisations; ms_per_step = wall time / K.  The dominant kernel's
-average launch duration is measured with HIP events on the launch stream
-around the same graph replay; it feeds roofline.achieved.
+graph (one graph launch instead of K kernel launches from the host); the
+graph is replayed untimed for WARM_S seconds (a cold MI355X runs the first
+replays 7-20% slower while its clocks settle), then replayed once, timed,
+between device synchronisations; ms_per_step = wall time / K.  The dominant
+kernel's average launch duration is measured with HIP events on the launch
+stream around one more replay of the same graph; it feeds roofline.achieved.
 
 Further legs (same JSON line): "gemm" (a8w8 at M = 2048,
 three projections), "gemm_pert" (the reference's esimd_gemm_fp8_pert, w8a16,
@@ -71,7 +71,10 @@ def time_graph(fn_list, torch, stream, warm_s=0.0):
     """Capture fn_list (one launch each) in a graph, replay it for warm_s
     seconds (the GPU's clocks take about a second of load to settle: a cold
     GPU runs the first replays 7% (GEMV) to 20% (GEMM) slower), then time one
-    replay between device synchronisations; returns (wall_s, event_ms, graph)."""
+    replay between device synchronisations (wall clock: nothing else in the
+    bracket -- two event records there added ~14 us to a 20-launch replay)
+    and one more between events on its stream (GPU time); returns
+    (wall_s, event_ms, graph)."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for fn in fn_list:
@@ -83,16 +86,19 @@ def time_graph(fn_list, torch, stream, warm_s=0.0):
     while time.perf_counter() < t_end:
         g.replay()
         torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         e0.record(stream)
         g.replay()
         e1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     return wall, e0.elapsed_time(e1), g
 
 

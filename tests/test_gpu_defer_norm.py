@@ -138,10 +138,11 @@ def test_glu_rs_equals_unfused(ops, dev, M, K, dtype):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("hd,nq,nk", [(256, 16, 16), (128, 8, 2)])
 @pytest.mark.parametrize("M", [1, 4])
-def test_qk_rope_rs_equals_unfused(ops, dev, M, hd, nq, nk):
-    K, dtype = 3072, torch.float16
+def test_qk_rope_rs_equals_unfused(ops, dev, M, hd, nq, nk, dtype):
+    K = 3072
     N = (nq + 2 * nk) * hd
     _say(f"defer qkv M={M} hd={hd}")
     W, s = synthetic.weight_fp8(N, K, seed=N + 13)
@@ -162,6 +163,38 @@ def test_qk_rope_rs_equals_unfused(ops, dev, M, hd, nq, nk):
     assert torch.equal(out, ref)
     assert torch.equal(q_out, ref[:, : nq * hd])
     assert int(cnt.abs().sum()) == 0, "arrival counters must be left zero"
+
+
+def test_empty_batch_is_a_no_op(ops, dev):
+    """M = 0: every deferred-norm op returns without touching its outputs."""
+    K, N, d = 4096, 3072, 1024
+    W, s = synthetic.weight_fp8(N, K, seed=3)
+    Wg, sg = synthetic.weight_fp8(2 * d, 3072, seed=4)
+    Wd, sd, Wgd, sgd = W.to(dev), s.to(dev), Wg.to(dev), sg.to(dev)
+    x = torch.empty(0, K, dtype=torch.float16, device=dev)
+    res = torch.empty(0, N, dtype=torch.float16, device=dev)
+    y = torch.empty(0, N, dtype=torch.float16, device=dev)
+    ss = torch.empty(0, N // 16, dtype=torch.float32, device=dev)
+    nw = synthetic.norm_weight(N, seed=5).to(dev)
+    ops.esimd_gemv_fp8_add_rms_norm_defer(x, Wd, sd, res, nw, y, ss)
+    ops.esimd_gemv_fp8_pern_rs(x, Wd, sd, y, ss, EPS)
+    xg = torch.empty(0, 3072, dtype=torch.float16, device=dev)
+    out = torch.empty(0, d, dtype=torch.float16, device=dev)
+    ops.esimd_gemv_fp8_gelu_and_mul_rs(xg, Wgd, sgd, out, torch.empty(0, 192, device=dev), EPS)
+    torch.cuda.synchronize()
+
+
+def test_producer_refuses_aliased_outputs(ops, dev):
+    """The producer's output must not share memory with the residual it
+    updates (other workgroups still read it): the op raises."""
+    M, K, N = 2, 4096, 3072
+    W, s = synthetic.weight_fp8(N, K, seed=6)
+    x = synthetic.activations(M, K, seed=7).to(dev)
+    res = synthetic.activations(M, N, seed=8).to(dev)
+    nw = synthetic.norm_weight(N, seed=9).to(dev)
+    ss = torch.empty(M, N // 16, dtype=torch.float32, device=dev)
+    with pytest.raises(RuntimeError):
+        ops.esimd_gemv_fp8_add_rms_norm_defer(x, W.to(dev), s.to(dev), res, nw, res, ss)
 
 
 def test_unsupported_shapes_raise(ops, dev):

@@ -565,7 +565,8 @@ __device__ inline bool tail_arrive(int* counters, int slot, int expect, int* fla
 }
 
 template <typename T, int TAIL, int TP>
-__device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M, uint8_t* smem) {
+__device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M, uint8_t* smem, const float (&rcs)[2],
+                          const float (&rsn)[2]) {
   static_assert(TAIL == TAIL_ROPE, "tail kinds");
   __shared__ int flag;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -581,14 +582,22 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
     const uint16_t* w = head < ta.nq ? ta.qw : ta.kw;
     const int c = lane % L;
     const u4 wa = load_u4(w + 8 * c), wb = load_u4(w + HALF + 8 * c);
-    const double lt = log2((double)ta.theta);
     for (int m0 = 0; m0 < M; m0 += 4 * HPW) {
       const int m = m0 + wave * HPW + lane / L, mc = min(m, M - 1);
       uint16_t* v = y + (size_t)mc * N + (size_t)head * HD;
-      // the row's loads first, the fp64 angles behind them
+      // the row's loads first; the cos / sin table (entries tid and tid +
+      // 256, M * HALF <= 512 for M <= 4) was computed in the prologue
       const u4 va = load_u4_dev(v + 8 * c), vb = load_u4_dev(v + HALF + 8 * c);
-      if (m0 == 0)
-        for (int i = tid; i < M * HALF; i += 256) rope_angle((double)ta.pos[i / HALF], i % HALF, HD, lt, cs[i], sn[i]);
+      if (m0 == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int i = tid + 256 * j;
+          if (i < M * HALF) {
+            cs[i] = rcs[j];
+            sn[i] = rsn[j];
+          }
+        }
+      }
       __syncthreads();
       u4 oa, ob;
       norm_rope_chunks<T, L>(va, vb, wa, wb, cs + mc * HALF, sn + mc * HALF, ta.eps, ta.neox != 0, c, oa, ob);
@@ -789,6 +798,17 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     }
     asm volatile("" ::: "memory");  // before the weight prologue
   }
+  // TAIL_ROPE: the positions of the cos / sin table entries this thread
+  // fills if its workgroup runs the tail (entries t and t + 256 of the
+  // M x hd/2 table), loaded before the weight prologue so that the wait for
+  // them does not drain the weight stages
+  [[maybe_unused]] int64_t rpos[2] = {0, 0};
+  if constexpr (TAIL == TAIL_ROPE) {
+    constexpr int HALF = 8 * TP;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) rpos[j] = na.tail.pos[min((int)threadIdx.x + 256 * j, M * HALF - 1) / HALF];
+    asm volatile("" ::: "memory");  // before the weight prologue
+  }
   // EPI_ROWSCALE: wave 0 (the only wave that scales outputs) loads the
   // producer's partial sums of rows 0..3, four per lane (nss <= 256, rows
   // 16-byte aligned), before the weight prologue, so that its wait for them
@@ -851,6 +871,23 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   // the loads of the stages after it in flight.
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, wr[j], xr[j]);
+
+  // TAIL_ROPE: this thread's cos / sin table entries (fp64 angles, the
+  // standalone op's rope_angle), computed while the first weight stages are
+  // in flight -- in the tail they sat on the launch's critical path.  Every
+  // q / k workgroup computes them; only the last of each head uses them.
+  [[maybe_unused]] float rcs[2] = {0.f, 0.f}, rsn[2] = {0.f, 0.f};
+  if constexpr (TAIL == TAIL_ROPE) {
+    constexpr int HALF = 8 * TP, HD = 16 * TP;
+    if (nw / HD < na.tail.nq + na.tail.nk) {  // q / k heads (uniform per workgroup)
+      const double lt = log2((double)na.tail.theta);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int i = (int)threadIdx.x + 256 * j;
+        if (i < M * HALF) rope_angle((double)rpos[j], i % HALF, HD, lt, rcs[j], rsn[j]);
+      }
+    }
+  }
 
   // EPI_ROWSCALE: the rows' sums in a fixed order -- each lane's four,
   // then the wave's 64 lanes (the DPP steps of wave_sum_dpp, the four rows
@@ -1080,7 +1117,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   else if constexpr (TPW == 1)
     lds_reduce_store<NT, MB, TAIL != TAIL_NONE>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
                                                 XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
-  if constexpr (TAIL != TAIL_NONE) gemv_tail<T, TAIL, TP>(na.tail, sr.y, nw, N, M, smem);
+  if constexpr (TAIL != TAIL_NONE) gemv_tail<T, TAIL, TP>(na.tail, sr.y, nw, N, M, smem, rcs, rsn);
 }
 
 // ---------------------------------------------------------------------------

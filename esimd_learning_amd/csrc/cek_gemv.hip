@@ -670,6 +670,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
                                        std::is_same<T, TO>::value),
                 "deferred norm producer: one 16-row tile, fp16 / bf16");
   static_assert(EPI != EPI_ROWSCALE || (MB == 1 && !NORM && !XF8), "deferred norm consumer: fp16 / bf16, M <= 16");
+  static_assert(EPI != EPI_ROWSCALE || STEPS * TPW >= 2, "deferred norm consumer: row scales at stage 1");
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 16), "activations go through LDS only for M <= 16");
@@ -891,10 +892,12 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 
   // EPI_ROWSCALE: the rows' sums in a fixed order -- each lane's four,
   // then the wave's 64 lanes (the DPP steps of wave_sum_dpp, the four rows
-  // interleaved) -- and their 1 / rms, in wave 0 (no barrier).  Run where
-  // the row scales are first needed, the first tile's epilogue: the wait
-  // for the partial sums' loads there is long over (at the start of the
-  // K loop it delayed wave 0's first stage by ~1 us at M = 4).
+  // interleaved) -- and their 1 / rms (v_rsq_f32 of sum / K + eps, the
+  // argument >= eps), in wave 0 (no barrier).  Run at the top of the second
+  // K stage: the partial sums' loads (issued before stage 0's) are in, and
+  // wave 0 would otherwise wait there for stage 1's; before stage 0 it
+  // delayed the first stage, in the epilogue it lengthened every
+  // workgroup's critical path.
   auto rowscale_sums = [&]() {
     if constexpr (EPI == EPI_ROWSCALE) {
       if (wave_u == 0) {
@@ -916,7 +919,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 16)) +
                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 32)) +
                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[m]), 48));
-          rinv[m] = rsqrtf(sum / (float)K + na.eps);
+          rinv[m] = __builtin_amdgcn_rsqf(sum * (1.f / (float)K) + na.eps);
         }
         pick_rs();
       }
@@ -1025,6 +1028,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   }
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
+    if (i == 1) rowscale_sums();
     // Stage i into LDS buffer i & 1 (last read at step i - 2, which every
     // wave finished before the barrier of step i - 1).  Lane l's unit lands
     // at slot l, i.e. unit v of row r at slot v ^ (r & 15).
@@ -1080,7 +1084,6 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     if constexpr (TPW > 1) {
       if (i % STEPS == STEPS - 1) {  // tile i / STEPS is complete
         uint8_t* redp = smem + 2 * STAGE + XAREA;
-        if (i == STEPS - 1) rowscale_sums();
         if constexpr (GLU) {
           if (i / STEPS == 0) {  // gate tile: keep the rounded values
             lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, XF8 || EPI == EPI_ROWSCALE,
@@ -1111,7 +1114,6 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       }
     }
   }
-  if constexpr (TPW == 1) rowscale_sums();
   if constexpr (EPI == EPI_ADDNORM)
     lds_reduce_addnorm<T>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
   else if constexpr (TPW == 1)

@@ -670,7 +670,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
                                        std::is_same<T, TO>::value),
                 "deferred norm producer: one 16-row tile, fp16 / bf16");
   static_assert(EPI != EPI_ROWSCALE || (MB == 1 && !NORM && !XF8), "deferred norm consumer: fp16 / bf16, M <= 16");
-  static_assert(EPI != EPI_ROWSCALE || STEPS * TPW >= 2, "deferred norm consumer: row scales at stage 1");
+  static_assert(EPI != EPI_ROWSCALE || STEPS >= 2, "deferred norm consumer: row scales at stage 1, before tile 0 ends");
   constexpr int NS = STEPS * TPW;  // stages of the workgroup
   static_assert(D >= 1 && D <= NS, "prefetch depth");
   static_assert(MX == 0 || (MB == 1 && MX <= 16), "activations go through LDS only for M <= 16");

@@ -1203,8 +1203,9 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   }
   if constexpr (!XF8 && S == 14) {
     // K = 14336, 8 < M <= 16, N <= 4096 (the down projection): the 16
-    // activation rows staged through LDS (measured on MI355X at N = 4096:
-    // 19.7 -> 18.5 us; at K = 4096 staging 9-16 rows was 3-33% slower)
+    // activation rows staged through LDS (measured on MI355X at M = 16,
+    // N = 4096: 18.7 -> 16.2 us; at K = 4096 staging 9-16 rows was 3-33%
+    // slower)
     if (M > 8 && M <= 16 && N <= 4096) {
       CEK_LDS_T(1, 2, 16, 1, false);
       return true;

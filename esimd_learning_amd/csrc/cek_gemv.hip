@@ -422,7 +422,7 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
 template <typename T>
 __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave, int lane, int n0, int N, int M,
                                           const SegRef& sr, int skind, uint32_t sc_bits, const NormArgs& na,
-                                          const uint16_t (&pres)[4], uint16_t pnw) {
+                                          const uint32_t (&pres)[4], uint32_t pnw) {
   f4* red = reinterpret_cast<f4*>(smem);  // [3][64]
   __syncthreads();                         // every wave is done with the stages
   if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
@@ -430,7 +430,9 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
   if (wave != 0) return;
   const int n16 = lane & 15, g = lane >> 4, n = n0 + n16;
   const float sc = scale_value(sc_bits, skind);
-  const float wn = T::to_f32(pnw);
+  uint32_t pw = pnw;
+  asm volatile("" : "+v"(pw));  // the conversion stays here, after the loads are long in
+  const float wn = T::to_f32((uint16_t)pw);
   f4 c = acc;
 #pragma unroll
   for (int w = 0; w < 3; ++w) c += red[w * 64 + lane];
@@ -439,7 +441,7 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
   for (int v = 0; v < 4; ++v) {
     const int m = g * 4 + v;
     const float o = T::to_f32(T::from_f32(f32_round(c[v] * sc)));
-    const float sv = o + T::to_f32(pres[v]);
+    const float sv = o + T::to_f32((uint16_t)pres[v]);
     const uint16_t rp = T::from_f32(sv);
     s2[v] = f32_round(sv * sv);  // rounded before the sums (no fma contraction)
     if (n < N && m < M) {
@@ -833,15 +835,18 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   // lane & 15 of the tile) and norm weight that wave 0's epilogue uses, raw,
   // loaded before the weight prologue so that the epilogue does not wait
   // for them
-  // (every wave loads them: a branch would merge the 16-bit values, which
-  // makes the compiler wait for them there)
-  [[maybe_unused]] uint16_t pres[4];
-  [[maybe_unused]] uint16_t pnw;
+  // (wave 0 only, under a wave-uniform branch, each value zero-extended to
+  // 32 bits: 16-bit values merged at the branch's end get packed in pairs,
+  // which makes the compiler wait for the loads there)
+  [[maybe_unused]] uint32_t pres[4];  // (set in wave 0 only, used there only)
+  [[maybe_unused]] uint32_t pnw;
   if constexpr (EPI == EPI_ADDNORM) {
-    const int n = min(nw + n16, N - 1);
-    pnw = na.w[n];
+    if (wave_u == 0) {
+      const int n = min(nw + n16, N - 1);
+      pnw = na.w[n];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) pres[v] = na.r_out[(size_t)min(g * 4 + v, M - 1) * N + n];
+      for (int v = 0; v < 4; ++v) pres[v] = na.r_out[(size_t)min(g * 4 + v, M - 1) * N + n];
+    }
     asm volatile("" ::: "memory");  // before the weight prologue
   }
   // EPI_ROWSCALE: wave 0's epilogue row scales, sc_m[0][v] = inv of row 4 (lane >> 4) + v

@@ -311,11 +311,19 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_lds_kernel(
 //   MI355X put 530-840 of a step's ~2500 cycles there, with both waves of a
 //   SIMD stalled at once.  With loader waves the SIMD's other wave keeps the
 //   MFMA pipe busy meanwhile (M = 2048: 5-14% faster than all waves loading).
+// * The loads are MUBUF buffer loads with the LDS bit (buffer resources over
+//   A and B), not global_load_lds: the compiler counts a global_load_lds as
+//   an outstanding LDS event as well, so every fragment read behind one waited
+//   for lgkmcnt(0); with buffer loads it waits only for its own fragment.
+// * With NCH > 1 (8-wave tiles) a loader issues only the first of NCH chunks
+//   of its loads after the barrier and the others in the next step's first
+//   NCH - 1 MFMA groups, so that it is not stalled behind the load path for
+//   the whole batch (M = 2048, weights from HBM: 3-5% faster, NCH = 3 best).
 // The barrier orders, for all waves: step k + 1's rows have landed (the
 // loaders' only outstanding loads), every read of step k's slots is done
 // (lgkmcnt(0)), so they may be overwritten.
 // Requires K % 128 == 0, FM even, M >= BM, N >= BN, 16-byte aligned A and B,
-// each below 4 GB.
+// each below 4 GB (the buffer resources' 32-bit byte range).
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN>
 struct PipeCfg {
@@ -362,56 +370,68 @@ __device__ inline void barrier_upto(int steps) {
   barrier_vmcnt<0>();
 }
 
-// Direct-to-LDS loads of one K step (128 bytes) of CH 1 KB row chunks into a
-// slot: chunks j = w + STRIDE i (rows 8 j .. 8 j + 7) of loader w.
-template <int CH, int STRIDE>
-__device__ inline void a8w8_issue_rows(uint8_t* slot, int kb, int w, const uint8_t* const (&gp)[CH]) {
-#if defined(__HIP_DEVICE_COMPILE__)
-#pragma unroll
-  for (int i = 0; i < CH; ++i)
-    __builtin_amdgcn_global_load_lds(gp[i] + kb, (lds_ptr_t)(slot + (w + STRIDE * i) * 1024), 16, 0, 0);
-#endif
+// Buffer resource over n bytes at p (raw, stride 0); loads beyond n return 0.
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)n, 0x00020000);
 }
 
-// The same from one 32-bit byte offset off a matrix base: chunk i's rows are
-// STRIDE * 8 rows (a uniform byte stride) after chunk 0's, so a lane keeps
-// one VGPR for all of its loads (the caller checks that the matrix is below
-// 4 GB and that every addressed row exists).
-template <int CH, int STRIDE>
-__device__ inline void a8w8_issue_off(uint8_t* slot, int kb, int w, const uint8_t* base, int K, uint32_t off) {
+// Direct-to-LDS loads of chunk ch (of NCH) of one K step (128 bytes of each
+// row) by loader w: its BL B loads, then its AL A loads, cut into NCH runs of
+// ceil((AL + BL) / NCH).  Load i of a kind moves rows 8 j .. 8 j + 7, j = w +
+// LW i, into 1 KB piece j of the slot; the lane's byte offset (ga / gb, one
+// VGPR) plus kb addresses chunk 0's row and i * LW * 8 * K (a uniform
+// SGPR offset) the row of load i.
+template <int AL, int BL, int LW, int NCH>
+__device__ __forceinline__ void a8w8_issue_chunk(int ch, uint8_t* sB, uint8_t* sA, int kb, int w, __amdgpu_buffer_rsrc_t rA,
+                                                 __amdgpu_buffer_rsrc_t rB, int K, uint32_t ga, uint32_t gb) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int T = AL + BL, CS = (T + NCH - 1) / NCH;
 #pragma unroll
-  for (int i = 0; i < CH; ++i)
-    __builtin_amdgcn_global_load_lds(base + (size_t)i * STRIDE * 8 * K + (off + (uint32_t)kb),
-                                     (lds_ptr_t)(slot + (w + STRIDE * i) * 1024), 16, 0, 0);
+  for (int i = 0; i < T; ++i) {
+    if (i < ch * CS || i >= ch * CS + CS) continue;
+    if (i < BL)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr_t)(sB + (w + LW * i) * 1024), 16, gb + (uint32_t)kb,
+                                               i * LW * 8 * K, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr_t)(sA + (w + LW * (i - BL)) * 1024), 16, ga + (uint32_t)kb,
+                                               (i - BL) * LW * 8 * K, 0, 0);
+  }
 #endif
 }
 
 // One K step kt from ring slot c (the next step's slot cn).  Its barrier
 // (before the last MFMA group) waits for step kt + 1's loads, leaves up to
-// RING - 2 later steps' in flight, and refills slot c -- fully read by then --
-// with step kt + RING.
-template <int BM, int BN, int WM, int WN, int LW, int RING>
+// RING - 2 later steps' in flight, and is followed by chunk 0 of step
+// kt + RING into slot c (fully read by then); chunks 1 .. NCH - 1 of step
+// kt + RING - 1 (whose chunk 0 went out after the previous step's barrier)
+// go out in groups 0 .. NCH - 2.  Steps 0 .. RING - 1 are loaded whole by the
+// prologue, hence kt >= 1 for the chunks.
+template <int BM, int BN, int WM, int WN, int LW, int RING, int NCH>
 __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, int c, int cn, uint8_t* sAr, uint8_t* sBr, bool loader, int wave,
-                                               int wm, int wn, int r16, int p0, int p1, const uint8_t* A, const uint8_t* B,
-                                               int K, uint32_t ga, uint32_t gb,
+                                               int wm, int wn, int r16, int p0, int p1, __amdgpu_buffer_rsrc_t rA,
+                                               __amdgpu_buffer_rsrc_t rB, int K, uint32_t ga, uint32_t gb,
                                                f4 (&acc)[PipeCfg<BM, BN, WM, WN>::FM][PipeCfg<BM, BN, WM, WN>::FN],
                                                i8 (&a)[2], const i8 (&bc)[PipeCfg<BM, BN, WM, WN>::FN],
                                                i8 (&bn)[PipeCfg<BM, BN, WM, WN>::FN]) {
   using C = PipeCfg<BM, BN, WM, WN>;
   using L = LoadSplit<BM, BN, LW>;
   constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
+  static_assert(NCH >= 1 && NCH <= FM, "chunks 1 .. NCH - 1 go out in the groups before the barrier");
   const uint8_t* sA = sAr + c * C::ASLOT + (wm * TM + r16) * BK;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     if (i + 1 < FM) {
       a[(i + 1) & 1] = lds_frag(sA + (i + 1) * 16 * BK, p0, p1);
+      if (i < NCH - 1 && loader && kt >= 1 && kt + RING - 1 < KT) {
+        const int cl = c == 0 ? RING - 1 : c - 1;  // slot of step kt + RING - 1
+        a8w8_issue_chunk<L::AL, L::BL, LW, NCH>(i + 1, sBr + cl * C::BSLOT, sAr + cl * C::ASLOT, (kt + RING - 1) * BK,
+                                                wave, rA, rB, K, ga, gb);
+      }
     } else if (kt + 1 < KT) {
       barrier_upto<RING - 2, L::AL + L::BL>(KT - 2 - kt);
-      if (loader && kt + RING < KT) {
-        a8w8_issue_off<L::BL, LW>(sBr + c * C::BSLOT, (kt + RING) * BK, wave, B, K, gb);
-        a8w8_issue_off<L::AL, LW>(sAr + c * C::ASLOT, (kt + RING) * BK, wave, A, K, ga);
-      }
+      if (loader && kt + RING < KT)
+        a8w8_issue_chunk<L::AL, L::BL, LW, NCH>(0, sBr + c * C::BSLOT, sAr + c * C::ASLOT, (kt + RING) * BK, wave, rA, rB,
+                                                K, ga, gb);
       const uint8_t* nA = sAr + cn * C::ASLOT + (wm * TM + r16) * BK;
       const uint8_t* nB = sBr + cn * C::BSLOT + (wn * TN + r16) * BK;
 #pragma unroll
@@ -430,8 +450,9 @@ __device__ __forceinline__ void a8w8_pipe_step(int kt, int KT, int c, int cn, ui
 // ((K / SPLIT) % 128 == 0) and stores its unscaled fp32 sums to part
 // P[b % SPLIT] of the [SPLIT][M][N] workspace P; gemm_splitk_finalize then
 // adds the parts in order, scales and converts.
-// RING: slots of the A and B rings (loads run RING - 1 steps ahead).
-template <typename T, int BM, int BN, int WM, int WN, int OCC, int LW, int SPLIT = 1, int RING = 2>
+// RING: slots of the A and B rings (loads run RING - 1 steps ahead).  NCH:
+// chunks a loader's loads of a step are issued in (a8w8_pipe_step).
+template <typename T, int BM, int BN, int WM, int WN, int OCC, int LW, int SPLIT = 1, int RING = 2, int NCH = 1>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sa,
     const uint8_t* __restrict__ B, const float* __restrict__ sb,
@@ -464,15 +485,21 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   // before are the previous tile's, which computes the same values.
   const int mlo = tm * BM, nlo = tn * BN;
   const int m0 = min(mlo, M - BM), n0 = min(nlo, N - BN);
+  const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)((size_t)M * K));
+  const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B, (uint32_t)((size_t)N * K));
   // The epilogue's scales go to LDS first, by 4-byte direct-to-LDS loads
   // (one instruction per wave for 64 of them), so that the prologue's wait
   // covers their latency; register loads mixed with the direct-to-LDS ones
-  // would make the compiler drain every load before using them.
+  // would make the compiler drain every load before using them.  Waves
+  // 0 .. BM / 64 - 1 load row scales, the rest column scales.
+  static_assert(BM % 64 == 0, "a wave's scales come from one of sa, sb");
   if (64 * wave < BM + BN) {
     const int t = min(64 * wave + lane, BM + BN - 1);
-    const float* src = t < BM ? sa + m0 + t : sb + n0 + t - BM;
+    const bool rows = 64 * wave < BM;
 #if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(sc + 64 * wave), 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(rows ? sa : sb, (uint32_t)(rows ? M : N) * 4u),
+                                             (lds_ptr_t)(sc + 64 * wave), 4,
+                                             (uint32_t)(rows ? m0 + t : n0 + t - BM) * 4u, 0, 0, 0);
 #endif
   }
 
@@ -501,8 +528,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
 #pragma unroll
     for (int s = 0; s < RING; ++s)
       if (s == 0 || s < KT) {
-        a8w8_issue_off<BL, LW>(sBr + s * C::BSLOT, s * BK, wave, B, K, gb);
-        a8w8_issue_off<AL, LW>(sAr + s * C::ASLOT, s * BK, wave, A, K, ga);
+        a8w8_issue_chunk<AL, BL, LW, 1>(0, sBr + s * C::BSLOT, sAr + s * C::ASLOT, s * BK, wave, rA, rB, K, ga, gb);
       }
   }
   barrier_upto<RING - 1, AL + BL>(KT - 1);
@@ -518,15 +544,15 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   auto nxt = [](int v) { return v + 1 == RING ? 0 : v + 1; };
   for (; kt + 1 < KT; kt += 2) {
     const int c1 = RING == 2 ? 1 : nxt(c), c2 = RING == 2 ? 0 : nxt(c1);
-    a8w8_pipe_step<BM, BN, WM, WN, LW, RING>(kt, KT, RING == 2 ? 0 : c, c1, sAr, sBr, loader, wave, wm, wn, r16, p0,
-                                             p1, A, B, K, ga, gb, acc, a, b0, b1);
-    a8w8_pipe_step<BM, BN, WM, WN, LW, RING>(kt + 1, KT, c1, c2, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, A, B,
-                                             K, ga, gb, acc, a, b1, b0);
+    a8w8_pipe_step<BM, BN, WM, WN, LW, RING, NCH>(kt, KT, RING == 2 ? 0 : c, c1, sAr, sBr, loader, wave, wm, wn, r16,
+                                                  p0, p1, rA, rB, K, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW, RING, NCH>(kt + 1, KT, c1, c2, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, rA,
+                                                  rB, K, ga, gb, acc, a, b1, b0);
     c = c2;
   }
   if (kt < KT)
-    a8w8_pipe_step<BM, BN, WM, WN, LW, RING>(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), sAr, sBr, loader, wave,
-                                             wm, wn, r16, p0, p1, A, B, K, ga, gb, acc, a, b0, b1);
+    a8w8_pipe_step<BM, BN, WM, WN, LW, RING, NCH>(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), sAr, sBr, loader,
+                                                  wave, wm, wn, r16, p0, p1, rA, rB, K, ga, gb, acc, a, b0, b1);
   // every wave's loads (a non-loader's scale load included) are complete
   // here: step KT - 2's barrier (the last) waited for vmcnt(0), and with
   // KT == 1 the prologue's did
@@ -1548,13 +1574,13 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
 #define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, LW, RING)                                                \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, 1, RING>                                       \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, 1, RING, WM * WN == 8 ? 3 : 1>                 \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, nullptr, M, N, K, tm, tn); \
   } while (0)
 #define CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, SP, RING)                                          \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, SP, RING>                                      \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, SP, RING, WM * WN == 8 ? 3 : 1>                \
         <<<dim3((unsigned)(tm * tn * SP)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, ws, M, N, K, tm, tn); \
     gemm_splitk_finalize<TY, SP><<<dim3((unsigned)((N + 2047) / 2048), (unsigned)(M < 65535 ? M : 65535)), \
                                    256, 0, st>>>(ws, sa, sb, yp, (int)M, (int)N);                       \

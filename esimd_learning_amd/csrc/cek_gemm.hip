@@ -708,21 +708,28 @@ __device__ inline void w8a16_issue(uint8_t* smem, int stage, int kb, int wave,
 #endif
 }
 
-// Same loads from 32-bit byte offsets off the matrix bases (one VGPR per
-// load instead of a 64-bit pointer; the caller checks that both matrices
-// are below 4 GB).
-template <int BM, int BN, int ACH, int BCH, int STRIDE>
-__device__ inline void w8a16_issue_off(uint8_t* smem, int stage, int kb, int wave, const uint8_t* Xb, const uint8_t* W,
-                                       const uint32_t (&oa)[ACH], const uint32_t (&ob)[BCH]) {
+// Same loads from 32-bit byte offsets (one VGPR per load instead of a 64-bit
+// pointer; the caller checks that both matrices are below 4 GB) as buffer
+// loads over resources rX, rW, chunk ch of NCH: the loader's ACH A loads,
+// then its BCH B loads, cut into NCH runs of ceil((ACH + BCH) / NCH).
+template <int BM, int BN, int ACH, int BCH, int STRIDE, int NCH>
+__device__ __forceinline__ void w8a16_issue_chunk(int ch, uint8_t* smem, int stage, int kb, int wave,
+                                                  __amdgpu_buffer_rsrc_t rX, __amdgpu_buffer_rsrc_t rW,
+                                                  const uint32_t (&oa)[ACH], const uint32_t (&ob)[BCH]) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int T = ACH + BCH, CS = (T + NCH - 1) / NCH;
   uint8_t* sA = smem + stage * (BM * 128 + BN * 64);
   uint8_t* sB = sA + BM * 128;
 #pragma unroll
-  for (int i = 0; i < ACH; ++i)
-    __builtin_amdgcn_global_load_lds(Xb + (oa[i] + 2u * (uint32_t)kb), (lds_ptr_t)(sA + (wave + STRIDE * i) * 1024), 16, 0, 0);
-#pragma unroll
-  for (int i = 0; i < BCH; ++i)
-    __builtin_amdgcn_global_load_lds(W + (ob[i] + (uint32_t)kb), (lds_ptr_t)(sB + (wave + STRIDE * i) * 1024), 16, 0, 0);
+  for (int i = 0; i < T; ++i) {
+    if (i < ch * CS || i >= ch * CS + CS) continue;
+    if (i < ACH)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, (lds_ptr_t)(sA + (wave + STRIDE * i) * 1024), 16,
+                                               oa[i] + 2u * (uint32_t)kb, 0, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr_t)(sB + (wave + STRIDE * (i - ACH)) * 1024), 16,
+                                               ob[i - ACH] + (uint32_t)kb, 0, 0, 0);
+  }
 #endif
 }
 
@@ -807,11 +814,13 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
 // sits before the last group, after which the loader waves (the first LW)
 // issue the loads of step k + RING into the stage step k used and every wave
 // reads and decodes step k + 1's B fragments and first A fragment behind the
-// last group's MFMAs.  Loader waves and ring slots (RING stages, loads
-// RING - 1 steps ahead) as in gemm_a8w8_pipe_kernel.
+// last group's MFMAs.  Loader waves, ring slots (RING stages, loads RING - 1
+// steps ahead) and buffer loads as in gemm_a8w8_pipe_kernel.  NCH > 1 (the
+// loads in chunks over the MFMA groups) measured 1-4% slower here than all
+// of a step's loads after the barrier, so the launches use NCH = 1.
 // Requires K % 64 == 0, FM even, 16-byte aligned X and W.
 // ---------------------------------------------------------------------------
-template <typename T, int FMT, int BM, int BN, int WM, int WN, int LW, int RING = 2>
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int LW, int RING = 2, int NCH = 1>
 struct W8Pipe {
   static constexpr int BK = 64;
   static constexpr int NW = WM * WN;
@@ -834,22 +843,27 @@ struct W8Pipe {
     for (int j = 0; j < FN; ++j) decode16<T, FMT>(*reinterpret_cast<const u4*>(sB + j * 16 * 64 + pb * 16), b[j][0], b[j][1]);
   }
 
-  // step kt from ring slot c (the next step's slot cn)
+  // step kt from ring slot c (the next step's slot cn); the loads are issued
+  // in NCH chunks as in a8w8_pipe_step
   __device__ static __forceinline__ void step(int kt, int KT, int c, int cn, uint8_t* smem, bool loader, int wave, int wm,
-                                              int wn, int r16, int pa0, int pa1, int pb, const uint8_t* Xb,
-                                              const uint8_t* W, const uint32_t (&ga)[ACH], const uint32_t (&gb)[BCH],
-                                              f4 (&acc)[FM][FN], u4 (&a)[2][2], const u4 (&bc)[FN][2],
-                                              u4 (&bn)[FN][2]) {
+                                              int wn, int r16, int pa0, int pa1, int pb, __amdgpu_buffer_rsrc_t rX,
+                                              __amdgpu_buffer_rsrc_t rW, const uint32_t (&ga)[ACH],
+                                              const uint32_t (&gb)[BCH], f4 (&acc)[FM][FN], u4 (&a)[2][2],
+                                              const u4 (&bc)[FN][2], u4 (&bn)[FN][2]) {
+    static_assert(NCH >= 1 && NCH <= FM, "chunks 1 .. NCH - 1 go out in the groups before the barrier");
     const uint8_t* sA = smem + c * STAGE + (wm * TM + r16) * 128;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       if (i + 1 < FM) {
         read_a(sA + (i + 1) * 16 * 128, pa0, pa1, a[(i + 1) & 1]);
+        if (i < NCH - 1 && loader && kt >= 1 && kt + RING - 1 < KT)
+          w8a16_issue_chunk<BM, BN, ACH, BCH, LW, NCH>(i + 1, smem, c == 0 ? RING - 1 : c - 1, (kt + RING - 1) * BK, wave,
+                                                       rX, rW, ga, gb);
       } else if (kt + 1 < KT) {
         // step k + 1 has landed (later steps' loads may fly); slot c is free
         barrier_upto<RING - 2, ACH + BCH>(KT - 2 - kt);
         if (loader && kt + RING < KT)
-          w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, c, (kt + RING) * BK, wave, Xb, W, ga, gb);
+          w8a16_issue_chunk<BM, BN, ACH, BCH, LW, NCH>(0, smem, c, (kt + RING) * BK, wave, rX, rW, ga, gb);
         const uint8_t* nxt = smem + cn * STAGE;
         read_b(nxt + BM * 128 + (wn * TN + r16) * 64, pb, bn);
         read_a(nxt + (wm * TM + r16) * 128, pa0, pa1, a[0]);
@@ -868,11 +882,11 @@ struct W8Pipe {
 // of part b % SPLIT ((K / SPLIT) % 64 == 0) and stores its unscaled fp32
 // sums to part P[b % SPLIT] of the [SPLIT][M][N] workspace P;
 // gemm_splitk_finalize_w then adds the parts in order and scales.
-template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN, int LW, int SPLIT = 1, int RING = 2>
+template <typename T, int FMT, int BM, int BN, int OCC, int WM, int WN, int LW, int SPLIT = 1, int RING = 2, int NCH = 1>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ scale, int skind,
     uint16_t* __restrict__ Y, float* __restrict__ Pw, int M, int N, int K, int tiles_m, int tiles_n) {
-  using P = W8Pipe<T, FMT, BM, BN, WM, WN, LW, RING>;
+  using P = W8Pipe<T, FMT, BM, BN, WM, WN, LW, RING, NCH>;
   constexpr int BK = P::BK, NW = P::NW, TM = P::TM, TN = P::TN, FM = P::FM, FN = P::FN, STAGE = P::STAGE;
   constexpr int ACH = P::ACH, BCH = P::BCH;
   static_assert(RING >= 2 && RING <= 4, "ring slots");
@@ -886,7 +900,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
   int tm, tn;
   tile_of<BM, BN, 8>(SPLIT > 1 ? blockIdx.x / SPLIT : blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const uint8_t* Xb = reinterpret_cast<const uint8_t*>(X);
+  const __amdgpu_buffer_rsrc_t rX = buf_rsrc(X, (uint32_t)((size_t)M * K * 2));
+  const __amdgpu_buffer_rsrc_t rW = buf_rsrc(W, (uint32_t)((size_t)N * K));
 
   // A writer chunk j = wave + LW i: lane l -> row 8 j + (l >> 3), position l & 7
   // B writer chunk j = wave + LW i: lane l -> row 16 j + (l >> 2), position l & 3
@@ -916,7 +931,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
   if (loader) {
 #pragma unroll
     for (int s = 0; s < RING; ++s)
-      if (s == 0 || s < KT) w8a16_issue_off<BM, BN, ACH, BCH, LW>(smem, s, s * BK, wave, Xb, W, ga, gb);
+      if (s == 0 || s < KT) w8a16_issue_chunk<BM, BN, ACH, BCH, LW, 1>(0, smem, s, s * BK, wave, rX, rW, ga, gb);
   }
   barrier_upto<RING - 1, ACH + BCH>(KT - 1);
   u4 a[2][2], b0[FN][2], b1[FN][2];
@@ -926,13 +941,13 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
   auto nxt = [](int v) { return v + 1 == RING ? 0 : v + 1; };
   for (; kt + 1 < KT; kt += 2) {
     const int c1 = RING == 2 ? 1 : nxt(c), c2 = RING == 2 ? 0 : nxt(c1);
-    P::step(kt, KT, RING == 2 ? 0 : c, c1, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b0,
+    P::step(kt, KT, RING == 2 ? 0 : c, c1, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, rX, rW, ga, gb, acc, a, b0,
             b1);
-    P::step(kt + 1, KT, c1, c2, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W, ga, gb, acc, a, b1, b0);
+    P::step(kt + 1, KT, c1, c2, smem, loader, wave, wm, wn, r16, pa0, pa1, pb, rX, rW, ga, gb, acc, a, b1, b0);
     c = c2;
   }
   if (kt < KT)
-    P::step(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), smem, loader, wave, wm, wn, r16, pa0, pa1, pb, Xb, W,
+    P::step(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), smem, loader, wave, wm, wn, r16, pa0, pa1, pb, rX, rW,
             ga, gb, acc, a, b0, b1);
 
   static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");

@@ -340,13 +340,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
 // row (measured on MI355X: 6.4 TB/s, against 4.0-5.3 TB/s when an instruction
 // gathers 64-512-byte pieces of 16 rows, which is what an MFMA operand needs).
 // So the weights go through LDS: stage i holds bytes [1024 i, 1024 i + 1024)
-// of the workgroup's 16*NT rows, each row filled by one direct-to-LDS load
-// (global_load_lds_dwordx4; lane j's 16 bytes land at row base + 16 j).  Lane j
-// fetches 16-byte unit j ^ (row & 15) instead of unit j -- the same 1 KB --
-// so unit v of row r sits at slot v ^ (r & 15), and the sixteen rows an MFMA
-// fragment read touches fall in sixteen different bank groups.  Two stages
-// alternate: the next stage's loads are issued right after the barrier that
-// publishes the current one and run under its arithmetic.
+// of the workgroup's 16*NT rows, each row fetched by one 1 KB load instruction
+// into registers (16 bytes per lane), D stages ahead, and written to LDS
+// (lane j's 16 bytes at row base + 16 j) just before the stage's barrier.
+// Lane j fetches 16-byte unit j ^ (row & 15) instead of unit j -- the same
+// 1 KB -- so unit v of row r sits at slot v ^ (r & 15), and the sixteen rows
+// an MFMA fragment read touches fall in sixteen different bank groups.  Two
+// LDS stages alternate; the loads of stage i + D are issued right after the
+// barrier that publishes stage i and run under its arithmetic.
 //
 // The activations (a few hundred KB at most) are read from L2 straight into
 // MFMA operand layout, before the next stage's weights so that waiting for

@@ -1102,14 +1102,12 @@ __global__ __launch_bounds__(256) void gemm_w8a16_simple_kernel(
 
 using namespace cek;
 
-#ifndef CEK_W8A16_LW
-#define CEK_W8A16_LW 4
-#endif
-#ifndef CEK_A8W8_LAYOUT
-#define CEK_A8W8_LAYOUT 1
-#endif
-
 namespace cek {
+
+// loader waves of the score-picked w8a16 pipelined launches (one per SIMD),
+// and the row layout of gemm_a8w8_lds_kernel's launches
+constexpr int kW8a16Loaders = 4;
+constexpr int kA8w8LdsLayout = 1;
 
 // w8a16 product for any M with a weight scale of kind skind (ScaleKind):
 // M <= 16 the GEMV kernels, N <= 16 the activation-streaming kernel,
@@ -1284,7 +1282,7 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
 #define CEK_W8A16_PIPE(TY, F, BM, BN, OCC, WM, WN)                                                                 \
   do {                                                                                                         \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                                    \
-    gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN, CEK_W8A16_LW>                                                         \
+    gemm_w8a16_pipe_kernel<TY, F, BM, BN, OCC, WM, WN, kW8a16Loaders>                                                        \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(xp, wp, scale, skind, yp, nullptr, M, N, K, tm, tn); \
   } while (0)
 #define CEK_W8A16(TY, F)                                          \
@@ -1583,7 +1581,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
 #define CEK_A8W8(TY, BM, BN, WM, WN, OCC)                                                               \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_lds_kernel<TY, BM, BN, WM, WN, CEK_A8W8_LAYOUT, OCC>                                    \
+    gemm_a8w8_lds_kernel<TY, BM, BN, WM, WN, kA8w8LdsLayout, OCC>                                     \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
 #define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, LW, RING)                                                \

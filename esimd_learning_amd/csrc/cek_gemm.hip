@@ -380,7 +380,7 @@ __device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t n) {
 // ceil((AL + BL) / NCH).  Load i of a kind moves rows 8 j .. 8 j + 7, j = w +
 // LW i, into 1 KB piece j of the slot; the lane's byte offset (ga / gb, one
 // VGPR) plus kb addresses chunk 0's row and i * LW * 8 * K (a uniform
-// SGPR offset) the row of load i.
+// SGPR offset, unsigned 32-bit like the whole offset) the row of load i.
 template <int AL, int BL, int LW, int NCH>
 __device__ __forceinline__ void a8w8_issue_chunk(int ch, uint8_t* sB, uint8_t* sA, int kb, int w, __amdgpu_buffer_rsrc_t rA,
                                                  __amdgpu_buffer_rsrc_t rB, int K, uint32_t ga, uint32_t gb) {
@@ -391,10 +391,10 @@ __device__ __forceinline__ void a8w8_issue_chunk(int ch, uint8_t* sB, uint8_t* s
     if (i < ch * CS || i >= ch * CS + CS) continue;
     if (i < BL)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr_t)(sB + (w + LW * i) * 1024), 16, gb + (uint32_t)kb,
-                                               i * LW * 8 * K, 0, 0);
+                                               (int)((uint32_t)(i * LW * 8) * (uint32_t)K), 0, 0);
     else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr_t)(sA + (w + LW * (i - BL)) * 1024), 16, ga + (uint32_t)kb,
-                                               (i - BL) * LW * 8 * K, 0, 0);
+                                               (int)((uint32_t)((i - BL) * LW * 8) * (uint32_t)K), 0, 0);
   }
 #endif
 }

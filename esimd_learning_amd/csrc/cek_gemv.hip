@@ -84,7 +84,7 @@ struct NormArgs {
   float* s_out;       // per-row scales [M] (quant form), workgroup 0
   float eps;
   TailArgs tail;      // epilogue arguments (TAIL forms only)
-  float* ss_out;      // EPI_ADDNORM: per-tile sums of squares [M][N / 16]
+  float* ss_out;      // EPI_ADDNORM(12): per-tile sums of squares [M][N / tile rows]
   const float* ss_in; // EPI_ROWSCALE: the producer's [M][nss] sums of squares
   int nss;
 };
@@ -94,11 +94,15 @@ struct NormArgs {
 // Out(sum * scale) as usual, then s = o + r (fp32), r = Out(s) in place,
 // y = Out(f32(r) * w[n]) -- the norm's weight product without its 1 / rms
 // -- and the tile's sum of s^2 per row to ss_out[m][tile].
+// EPI_ADDNORM12: the same producer with 12-row tiles, for N whose 16-row
+// tiles leave CUs idle (N = 3072: 256 workgroups instead of 192; each
+// wave streams 3 rows, lanes 12-15 of the MFMA operand repeat row 11 and
+// are dropped in the epilogue).
 // EPI_ROWSCALE (the consumer, e.g. gate/up): x holds the producer's y; every
 // workgroup's wave 0 sums the nss partials of each row in a fixed order
 // (nss <= 256 and a multiple of 4, M <= 4), inv = rsqrt(sum / K + eps), and
 // scales its outputs by inv[m].
-enum EpiKind { EPI_NONE = 0, EPI_ADDNORM = 1, EPI_ROWSCALE = 2 };
+enum EpiKind { EPI_NONE = 0, EPI_ADDNORM = 1, EPI_ROWSCALE = 2, EPI_ADDNORM12 = 3 };
 
 struct SegRef {
   const uint8_t* w;
@@ -417,10 +421,11 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
   }
 }
 
-// EPI_ADDNORM epilogue of one 16-row tile (M <= 16): the cross-wave sum,
-// o = Out(sum * scale), then the residual add, the norm weight product and
-// the tile's per-row sum of squares (see EpiKind).
-template <typename T>
+// EPI_ADDNORM(12) epilogue of one tile of ROWS (16 or 12) rows (M <= 16):
+// the cross-wave sum, o = Out(sum * scale), then the residual add, the norm
+// weight product and the tile's per-row sum of squares (see EpiKind) to
+// ss_out[m][n0 / ROWS] of N / ROWS per row; columns past ROWS (and N) add 0.
+template <typename T, int ROWS>
 __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave, int lane, int n0, int N, int M,
                                           const SegRef& sr, int skind, uint32_t sc_bits, const NormArgs& na,
                                           const uint32_t (&pres)[4], uint32_t pnw) {
@@ -430,6 +435,7 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
   __syncthreads();
   if (wave != 0) return;
   const int n16 = lane & 15, g = lane >> 4, n = n0 + n16;
+  const bool col = n16 < ROWS && n < N;  // a column of this tile
   const float sc = scale_value(sc_bits, skind);
   uint32_t pw = pnw;
   asm volatile("" : "+v"(pw));  // the conversion stays here, after the loads are long in
@@ -444,13 +450,13 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
     const float o = T::to_f32(T::from_f32(f32_round(c[v] * sc)));
     const float sv = o + T::to_f32((uint16_t)pres[v]);
     const uint16_t rp = T::from_f32(sv);
-    s2[v] = f32_round(sv * sv);  // rounded before the sums (no fma contraction)
-    if (n < N && m < M) {
+    s2[v] = col ? f32_round(sv * sv) : 0.f;  // rounded before the sums (no fma contraction)
+    if (col && m < M) {
       na.r_out[(size_t)m * N + n] = rp;
       sr.y[(size_t)m * N + n] = T::from_f32(f32_round(T::to_f32(rp) * wn));
     }
   }
-  // each D row (one 16-lane DPP row): the tile's 16 columns, pairwise
+  // each D row (one 16-lane DPP row): the tile's 16 lanes, pairwise
   // ((c0 + c1) + (c2 + c3)) + ... through xor 1, xor 2, half mirror, mirror
 #pragma unroll
   for (int v = 0; v < 4; ++v) s2[v] += CEK_DPP_F32(s2[v], 0xB1);
@@ -462,7 +468,7 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
   for (int v = 0; v < 4; ++v) s2[v] += CEK_DPP_F32(s2[v], 0x140);
 #pragma unroll
   for (int v = 0; v < 4; ++v)
-    if (n16 == 0 && g * 4 + v < M) na.ss_out[(size_t)(g * 4 + v) * (N >> 4) + (n0 >> 4)] = s2[v];
+    if (n16 == 0 && g * 4 + v < M) na.ss_out[(size_t)(g * 4 + v) * (N / ROWS) + n0 / ROWS] = s2[v];
 }
 
 // LDS writes of this wave done, then a workgroup barrier -- without the
@@ -669,7 +675,8 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
 template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
           bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0, bool ROT = false, int EPI = EPI_NONE>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M, NormArgs na) {
-  static_assert(EPI != EPI_ADDNORM || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !XF8 &&
+  constexpr bool PROD = EPI == EPI_ADDNORM || EPI == EPI_ADDNORM12;  // deferred-norm producer
+  static_assert(!PROD || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !XF8 &&
                                        std::is_same<T, TO>::value),
                 "deferred norm producer: one 16-row tile, fp16 / bf16");
   static_assert(EPI != EPI_ROWSCALE || (MB == 1 && !NORM && !XF8), "deferred norm consumer: fp16 / bf16, M <= 16");
@@ -683,7 +690,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
                                       std::is_same<T, TO>::value),
                 "tails: one 16-row tile per workgroup, fp16 / bf16 activations");
   constexpr int K = STEPS * 1024;
-  constexpr int ROWS = 16 * NT, S = D + 1, STAGE = ROWS * 1024;
+  constexpr int ROWS = EPI == EPI_ADDNORM12 ? 12 : 16 * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
   constexpr int XB = XF8 ? 1 : 2;  // activation bytes per value
   constexpr int LW = ROWS / 4;     // weight rows per wave and stage
@@ -706,6 +713,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   const int N = sr.n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n16 = lane & 15, g = lane >> 4;
+  const int wn16 = ROWS < 16 ? min(n16, ROWS - 1) : n16;  // this lane's weight row of the stage (MFMA operand)
   const int half = GLU ? N >> 1 : 0;                 // GLU: d, the up rows' offset
   const int nw = sr.group * ROWS * (GLU ? 1 : TPW);  // first row of the workgroup
   // first row of tile t
@@ -716,7 +724,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
     if constexpr (!ROT) {
       return s;
     } else {
-      const int r = (tile_row(i / STEPS) >> 4) % STEPS;
+      const int r = (EPI == EPI_ADDNORM12 ? sr.group : tile_row(i / STEPS) >> 4) % STEPS;
       return s + r >= STEPS ? s + r - STEPS : s + r;
     }
   };
@@ -841,7 +849,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   // which makes the compiler wait for the loads there)
   [[maybe_unused]] uint32_t pres[4];  // (set in wave 0 only, used there only)
   [[maybe_unused]] uint32_t pnw;
-  if constexpr (EPI == EPI_ADDNORM) {
+  if constexpr (PROD) {
     if (wave_u == 0) {
       const int n = min(nw + n16, N - 1);
       pnw = na.w[n];
@@ -1062,10 +1070,10 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const uint8_t* rw = sw + (16 * t + n16) * 1024;  // row 16 t + n16: slots are v ^ n16
+        const uint8_t* rw = sw + (16 * t + wn16) * 1024;  // row 16 t + wn16: slots are v ^ wn16
         if constexpr (XF8) {
-          const i8 bf = cat_i8(*reinterpret_cast<const u4*>(rw + 16 * (v ^ n16)),
-                               *reinterpret_cast<const u4*>(rw + 16 * ((v + 1) ^ n16)));
+          const i8 bf = cat_i8(*reinterpret_cast<const u4*>(rw + 16 * (v ^ wn16)),
+                               *reinterpret_cast<const u4*>(rw + 16 * ((v + 1) ^ wn16)));
 #pragma unroll
           for (int b = 0; b < MB; ++b) {
             if constexpr (MX > 0) acc[t][b] = mfma_fp8_16x16x128(cat_i8(xa0, xa1), bf, acc[t][b]);
@@ -1073,7 +1081,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           }
         } else {
           u4 lo, hi;
-          decode16<T, FMT>(*reinterpret_cast<const u4*>(rw + 16 * (v ^ n16)), lo, hi);
+          decode16<T, FMT>(*reinterpret_cast<const u4*>(rw + 16 * (v ^ wn16)), lo, hi);
 #pragma unroll
           for (int b = 0; b < MB; ++b) {
             if constexpr (MX > 0) {
@@ -1120,8 +1128,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       }
     }
   }
-  if constexpr (EPI == EPI_ADDNORM)
-    lds_reduce_addnorm<T>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
+  if constexpr (PROD)
+    lds_reduce_addnorm<T, ROWS>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
   else if constexpr (TPW == 1)
     lds_reduce_store<NT, MB, TAIL != TAIL_NONE>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
                                                 XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
@@ -1652,15 +1660,22 @@ int launch_gemv_tail(const void* x, const void* w, const void* scale, int skind,
   return check_launch();
 }
 
-// Deferred RMSNorm producer (EPI_ADDNORM) and plain consumer
-// (EPI_ROWSCALE): M <= 4 rows staged through LDS, one 16-row tile per
-// workgroup, rotated K order, e4m3 weights, K in {2, 3, 4, 5, 14, 24} KiB
-// values.
+// Deferred RMSNorm producer (EPI_ADDNORM, EPI_ADDNORM12) and plain consumer
+// (EPI_ROWSCALE): M <= 4 rows staged through LDS, one 16-row (12-row) tile
+// per workgroup, rotated K order, e4m3 weights, K in {2, 3, 4, 5, 14, 24}
+// KiB values.
 template <typename T, int EPI, int S>
 static void launch_defer_t(const void* x, GemvSegs& sg, int skind, int M, const NormArgs& na, hipStream_t st) {
   gemv_lds_kernel<T, T, CEK_E4M3, false, 1, 1, (S >= 3 ? 3 : 2), S, 4, 1, false, false, TAIL_NONE, 0, true, EPI>
-      <<<dim3(seg_grid(sg, 16)), 256, 0, st>>>(x, sg, skind, M, na);
+      <<<dim3(seg_grid(sg, EPI == EPI_ADDNORM12 ? 12 : 16)), 256, 0, st>>>(x, sg, skind, M, na);
 }
+
+// Rows per producer tile for N (a multiple of 16): 12 where the 16-row tiles
+// would leave CUs idle (fewer than 256 of them) and N / 12 is a valid
+// partial-sum count for the consumers (a multiple of 4, at most 256), else
+// 16.  M = 4, K = 24576, N = 3072: 16.5 us with 192 16-row tiles, against
+// 18.4 us for 256 tiles at N = 4096 (a third more bytes).
+static int defer_rows(int64_t N) { return N % 48 == 0 && N / 16 < 256 && N / 12 <= 256 ? 12 : 16; }
 
 template <typename T, int EPI>
 static bool launch_defer_k(const void* x, GemvSegs& sg, int skind, int M, int K, const NormArgs& na, hipStream_t st) {
@@ -1698,11 +1713,11 @@ int launch_gemv_addnorm(const void* x, const void* w, const void* scale, int ski
   if (!residual || !norm_weight || !ss_out) return CEK_ERR_INVALID;
   // other workgroups still read x and w while one writes y, the residual
   // and the partial sums
-  const int64_t yb = M * N * 2;
-  for (const auto& [p, b] : {std::pair<const void*, int64_t>{y, yb}, {residual, yb}, {ss_out, M * (N / 16) * 4}})
+  const int rows = defer_rows(N);
+  const int64_t yb = M * N * 2, sb = M * (N / rows) * 4;
+  for (const auto& [p, b] : {std::pair<const void*, int64_t>{y, yb}, {residual, yb}, {ss_out, sb}})
     if (overlaps(p, b, x, M * K * 2) || overlaps(p, b, w, N * K)) return CEK_ERR_UNSUPPORTED;
-  if (overlaps(y, yb, residual, yb) || overlaps(ss_out, M * (N / 16) * 4, y, yb) ||
-      overlaps(ss_out, M * (N / 16) * 4, residual, yb))
+  if (overlaps(y, yb, residual, yb) || overlaps(ss_out, sb, y, yb) || overlaps(ss_out, sb, residual, yb))
     return CEK_ERR_UNSUPPORTED;
   GemvSegs sg{};
   sg.count = 1;
@@ -1714,10 +1729,15 @@ int launch_gemv_addnorm(const void* x, const void* w, const void* scale, int ski
   na.r_out = static_cast<uint16_t*>(residual);
   na.w = static_cast<const uint16_t*>(norm_weight);
   na.ss_out = ss_out;
-  const bool ok = io_dtype == CEK_F16 ? launch_defer_k<F16, EPI_ADDNORM>(x, sg, skind, (int)M, (int)K, na, st)
-                                      : launch_defer_k<BF16, EPI_ADDNORM>(x, sg, skind, (int)M, (int)K, na, st);
+  const bool f16 = io_dtype == CEK_F16;
+  const bool ok = rows == 12 ? (f16 ? launch_defer_k<F16, EPI_ADDNORM12>(x, sg, skind, (int)M, (int)K, na, st)
+                                    : launch_defer_k<BF16, EPI_ADDNORM12>(x, sg, skind, (int)M, (int)K, na, st))
+                             : (f16 ? launch_defer_k<F16, EPI_ADDNORM>(x, sg, skind, (int)M, (int)K, na, st)
+                                    : launch_defer_k<BF16, EPI_ADDNORM>(x, sg, skind, (int)M, (int)K, na, st));
   return ok ? check_launch() : CEK_ERR_UNSUPPORTED;
 }
+
+int64_t defer_groups(int64_t N) { return N > 0 && N % 16 == 0 ? N / defer_rows(N) : 0; }
 
 // The row-scale arguments of the deferred-norm consumers; CEK_OK or the status.
 static int rowscale_args(const float* row_ss, int64_t n_ss, float row_eps, int64_t M, NormArgs& na) {
@@ -1750,6 +1770,8 @@ int launch_gemv_rowscale(const void* x, const void* w, const void* scale, int sk
 }
 
 }  // namespace cek
+
+extern "C" int64_t cek_gemv_fp8_add_rms_norm_defer_groups(int64_t N) { return cek::defer_groups(N); }
 
 extern "C" int cek_gemv_fp8_add_rms_norm_defer(const void* x, const void* w, const void* scale, void* residual,
                                                const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N,

@@ -563,8 +563,8 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
 // Deferred RMSNorm between two decode GEMVs (up to four rows, e4m3
 // weights).  The producer GEMV (e.g. o_proj) adds its rounded output into
 // the residual in place, writes output = residual * norm_weight (the norm
-// without its 1 / rms) and row_ss [M, N / 16], the per-16-column sums of
-// squares of the unrounded sums; the consumer ops below (the plain GEMV,
+// without its 1 / rms) and row_ss [M, G], G = defer_groups(N), the sums of
+// squares of the unrounded sums over G equal runs of columns; the consumer ops below (the plain GEMV,
 // gate/up with gelu_and_mul, QKV with QK-norm + RoPE) take that output and
 // row_ss and scale their rows by rsqrt(sum / K + eps).  No fallback: shapes
 // the kernels do not take raise, and the caller runs the unfused ops.
@@ -593,6 +593,8 @@ static void check_row_ss(const at::Tensor& row_ss, const at::Tensor& input, int6
   TORCH_CHECK(row_ss.dim() == 2 && row_ss.size(0) == M && row_ss.size(1) > 0, op, ": row_ss must be [M, n]");
 }
 
+int64_t esimd_gemv_fp8_add_rms_norm_defer_groups(int64_t N) { return cek_gemv_fp8_add_rms_norm_defer_groups(N); }
+
 void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
                                        at::Tensor residual, at::Tensor norm_weight, at::Tensor output,
                                        at::Tensor row_ss) {
@@ -612,7 +614,8 @@ void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::
   TORCH_CHECK(row_ss.scalar_type() == at::ScalarType::Float, op, ": row_ss must be fp32");
   check_device(row_ss, input, op, "row_ss");
   check_contig(row_ss, op, "row_ss");
-  TORCH_CHECK(row_ss.numel() == M * (N / 16), op, ": row_ss must be [M, N / 16]");
+  TORCH_CHECK(row_ss.numel() == M * cek_gemv_fp8_add_rms_norm_defer_groups(N), op,
+              ": row_ss must be [M, esimd_gemv_fp8_add_rms_norm_defer_groups(N)]");
   const int scale_code = scale_code_of(weight_scale, N, op);
   c10::OptionalDeviceGuard guard(input.device());
   check_rc(cek_gemv_fp8_add_rms_norm_defer(input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(),

@@ -63,6 +63,7 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
         "bool is_neox, Tensor(b!) counters, Tensor(c!)? q_out=None) -> ()");
   m.impl("esimd_gemv_fp8_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope);
 
+  m.def("esimd_gemv_fp8_add_rms_norm_defer_groups(int N) -> int", &esimd_gemv_fp8_add_rms_norm_defer_groups);
   m.def("esimd_gemv_fp8_add_rms_norm_defer(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) residual, "
         "Tensor norm_weight, Tensor(b!) output, Tensor(c!) row_ss) -> ()");
   m.impl("esimd_gemv_fp8_add_rms_norm_defer", c10::DispatchKey::CUDA, &esimd_gemv_fp8_add_rms_norm_defer);

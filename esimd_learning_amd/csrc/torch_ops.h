@@ -62,6 +62,7 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
 
 // Deferred RMSNorm between two decode GEMVs: the producer (residual add,
 // norm weight, per-tile sums of squares) and the row-scaled consumers.
+int64_t esimd_gemv_fp8_add_rms_norm_defer_groups(int64_t N);
 void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
                                        at::Tensor residual, at::Tensor norm_weight, at::Tensor output,
                                        at::Tensor row_ss);

@@ -102,7 +102,8 @@ class GemmaDecodeLayer:
         self.defer_norm = (defer_norm and dtype == torch.float16 and M <= 4 and e4m3 and self.fuse_tails and fuse_glu
                            and shapes)
         if self.defer_norm:
-            ss = lambda: torch.empty(M, self.hidden // 16, dtype=torch.float32, device=device)  # noqa: E731
+            groups = self.ops.esimd_gemv_fp8_add_rms_norm_defer_groups(self.hidden)
+            ss = lambda: torch.empty(M, groups, dtype=torch.float32, device=device)  # noqa: E731
             self.ss_o, self.ss_d = ss(), ss()    # after o_proj; after down (the next layer's input norm)
         if act_fp8:
             if self.Wqkv.dtype != torch.float8_e4m3fn or self.Wgu.dtype != torch.float8_e4m3fn:

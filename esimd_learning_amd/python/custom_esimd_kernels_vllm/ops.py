@@ -168,6 +168,14 @@ def esimd_gemv_fp8_qk_norm_rope(
                                      eps, theta, is_neox, counters, q_out)
 
 
+def esimd_gemv_fp8_add_rms_norm_defer_groups(N: int) -> int:
+    """G, the number of partial sums of squares per row that
+    esimd_gemv_fp8_add_rms_norm_defer writes for N output columns (N / 16,
+    or N / 12 where that fills more CUs: N = 3072 -> 256); 0 if N is not a
+    multiple of 16."""
+    return _ops.esimd_gemv_fp8_add_rms_norm_defer_groups(N)
+
+
 def esimd_gemv_fp8_add_rms_norm_defer(
     input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, residual: torch.Tensor,
     norm_weight: torch.Tensor, output: torch.Tensor, row_ss: torch.Tensor,
@@ -175,9 +183,10 @@ def esimd_gemv_fp8_add_rms_norm_defer(
     """The producer half of an add + RMSNorm deferred into the next GEMV
     (up to four rows, e4m3 weights): o = the GEMV's rounded output; residual
     += o in place; output = residual * norm_weight (rounded; the norm
-    without its 1 / rms); row_ss [M, N / 16] fp32 = the sums of squares of
-    the unrounded o + residual over each 16 columns.  Feed output and row_ss
-    to a ``*_rs`` op, which applies rsqrt(sum(row_ss[m]) / N + eps)."""
+    without its 1 / rms); row_ss [M, G] fp32, G =
+    ``esimd_gemv_fp8_add_rms_norm_defer_groups(N)``, = the sums of squares of
+    the unrounded o + residual over G equal runs of columns.  Feed output and
+    row_ss to a ``*_rs`` op, which applies rsqrt(sum(row_ss[m]) / N + eps)."""
     _ops.esimd_gemv_fp8_add_rms_norm_defer(input, weight, weight_scale, residual, norm_weight, output, row_ss)
 
 

@@ -268,20 +268,25 @@ int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, v
  * Producer, cek_gemv_fp8_add_rms_norm_defer: o = the GEMV's rounded output
  * [M, N]; s = o + residual (fp32); residual = round(s) in place;
  * y = round(residual * norm_weight[n]) -- the norm without its 1 / rms --
- * and ss_out [M][N / 16] = sum over each 16 columns of s^2.  y, residual and
- * ss_out must not overlap each other, x or w.
+ * and ss_out [M][G], G = cek_gemv_fp8_add_rms_norm_defer_groups(N): the sums
+ * of s^2 over each of G equal runs of N / G columns (G = N / 16, or N / 12
+ * where 16-column runs would give fewer than 256 workgroups and N is a
+ * multiple of 48: N = 3072 -> 256).  y, residual and ss_out must not overlap
+ * each other, x or w.
  *
  * Consumers (_rs): the named op over x = the producer's y, with each output
  * row m scaled, before rounding (and before gelu_and_mul, QK-norm and RoPE),
  * by inv[m] = rsqrt(sum_j row_ss[m][j] / K + row_eps); n_ss = the producer's
- * N / 16 (<= 256, a multiple of 4, row_ss 16-byte aligned), summed in a fixed order.  The result equals the unfused
- * norm -> GEMV to within the rounding of the moved 1 / rms (not bit for bit).
+ * G (<= 256, a multiple of 4, row_ss 16-byte aligned), summed in a fixed
+ * order.  The result equals the unfused norm -> GEMV to within the rounding
+ * of the moved 1 / rms (not bit for bit).
  *
  * All: M <= 4, K a multiple of 1024 (producer and plain consumer: K / 1024
  * in {2, 3, 4, 5, 14, 24}; gate/up and QKV: 3072, 4096, 5120), N % 16 == 0,
  * e4m3 weights, 16-byte aligned x and w; CEK_ERR_UNSUPPORTED otherwise (no
  * fallback: run the unfused ops).
  */
+int64_t cek_gemv_fp8_add_rms_norm_defer_groups(int64_t N);  /* G for N (a multiple of 16), else 0 */
 int cek_gemv_fp8_add_rms_norm_defer(const void* x, const void* w, const void* scale, void* residual,
                                     const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N, int64_t K,
                                     int io_dtype, int fp8_fmt, int scale_dtype, void* stream);

@@ -56,6 +56,17 @@ def test_library_loads_and_reports():
     assert lib.cek_last_hip_error() == b""
 
 
+def test_defer_norm_groups():
+    """Partial sums per row of the deferred-norm producer: N / 12 where the
+    16-column runs give fewer than 256 workgroups and N is a multiple of 48
+    (the consumers take a multiple of 4, at most 256), else N / 16; 0 for N
+    not a multiple of 16.  Host arithmetic only."""
+    lib = cabi.load()
+    g = lib.cek_gemv_fp8_add_rms_norm_defer_groups
+    assert [g(n) for n in (3072, 1536, 4096, 512, 2048, 5120, 48 * 100)] == [256, 128, 256, 32, 128, 320, 300]
+    assert [g(n) for n in (0, 100, -16)] == [0, 0, 0]
+
+
 def test_host_rejects_invalid_arguments():
     """Argument checks return before any HIP call, so they run without a GPU."""
     lib = cabi.load()

@@ -8,7 +8,9 @@ esimd_gemv_fp8_gelu_and_mul_rs, esimd_gemv_fp8_qk_norm_rope_rs.
 * The producer's GEMV part is checked against the oracle GEMV through a
   call with a zero residual (then residual_out = o exactly); its residual,
   output and sums are then checked bit for bit against the same fp32
-  arithmetic done on the host from o (the sums' butterfly order included).
+  arithmetic done on the host from o (the sums' butterfly order included,
+  over 16-column runs or, N = 1536 and 3072, 12-column runs padded to 16
+  with zeros).
 * The plain consumer is checked against the oracle composition: the norm
   of the reference (x * w / rms, oracle/norm.py) then the oracle GEMV,
   to the op pack's tolerance -- the moved 1 / rms changes the rounding, so
@@ -43,12 +45,16 @@ def _say(msg):
     sys.stdout.flush()
 
 
-def _butterfly16(sq):
-    """The producer's per-tile sum of 16 fp32 squares, pairwise:
+def _butterfly16(sq, groups):
+    """The producer's per-tile sum of the fp32 squares of N / groups columns
+    (16 or 12; 12 padded with four zeros to the 16 lanes), pairwise:
     ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then the two halves
     (xor-partner adds over offsets 1, 2, 4, 8).  sq: float32 [M, N]."""
     M, N = sq.shape
-    a = sq.reshape(M, N // 16, 16).astype(np.float32)
+    rows = N // groups
+    assert rows in (12, 16) and rows * groups == N
+    a = np.zeros((M, groups, 16), dtype=np.float32)
+    a[..., :rows] = sq.reshape(M, groups, rows)
     idx = np.arange(16)
     for off in (1, 2, 4, 8):
         a = (a + a[..., idx ^ off]).astype(np.float32)
@@ -59,14 +65,15 @@ def _producer(ops, x, W, s, r, w, dtype, dev):
     M, N = x.shape[0], W.shape[0]
     rd = r.to(dev).clone()
     y = torch.full((M, N), float("nan"), dtype=dtype, device=dev)
-    ss = torch.full((M, N // 16), float("nan"), dtype=torch.float32, device=dev)
+    ss = torch.full((M, ops.esimd_gemv_fp8_add_rms_norm_defer_groups(N)), float("nan"), dtype=torch.float32,
+                    device=dev)
     ops.esimd_gemv_fp8_add_rms_norm_defer(x.to(dev), W.to(dev), s.to(dev), rd, w.to(dev), y, ss)
     torch.cuda.synchronize()
     return rd.cpu(), y.cpu(), ss.cpu()
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("K,N", [(4096, 3072), (2048, 512), (24576, 3072), (5120, 4096)])
+@pytest.mark.parametrize("K,N", [(4096, 3072), (2048, 512), (24576, 3072), (5120, 4096), (3072, 1536)])
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_producer(ops, dev, M, K, N, dtype):
     _say(f"defer producer M={M} K={K} N={N} {dtype}")
@@ -80,14 +87,16 @@ def test_producer(ops, dev, M, K, N, dtype):
     of = o.float().numpy()
     wf = w.float().numpy()
     assert torch.equal(y0, torch.from_numpy(of * wf).to(dtype))
-    assert torch.equal(ss0, torch.from_numpy(_butterfly16(of * of)))
+    G = ss0.shape[1]
+    assert G == (N // 12 if N in (1536, 3072) else N // 16)
+    assert torch.equal(ss0, torch.from_numpy(_butterfly16(of * of, G)))
     # with the residual: the same o, then the host's fp32 arithmetic
     r1, y1, ss1 = _producer(ops, x, W, s, r, w, dtype, dev)
     sv = (of + r.float().numpy()).astype(np.float32)
     r_ref = torch.from_numpy(sv).to(dtype)
     assert torch.equal(r1, r_ref)
     assert torch.equal(y1, torch.from_numpy(r_ref.float().numpy() * wf).to(dtype))
-    assert torch.equal(ss1, torch.from_numpy(_butterfly16(sv * sv)))
+    assert torch.equal(ss1, torch.from_numpy(_butterfly16(sv * sv, G)))
 
 
 def _ss_of(v, nss):
@@ -174,7 +183,7 @@ def test_empty_batch_is_a_no_op(ops, dev):
     x = torch.empty(0, K, dtype=torch.float16, device=dev)
     res = torch.empty(0, N, dtype=torch.float16, device=dev)
     y = torch.empty(0, N, dtype=torch.float16, device=dev)
-    ss = torch.empty(0, N // 16, dtype=torch.float32, device=dev)
+    ss = torch.empty(0, ops.esimd_gemv_fp8_add_rms_norm_defer_groups(N), dtype=torch.float32, device=dev)
     nw = synthetic.norm_weight(N, seed=5).to(dev)
     ops.esimd_gemv_fp8_add_rms_norm_defer(x, Wd, sd, res, nw, y, ss)
     ops.esimd_gemv_fp8_pern_rs(x, Wd, sd, y, ss, EPS)
@@ -186,15 +195,20 @@ def test_empty_batch_is_a_no_op(ops, dev):
 
 def test_producer_refuses_aliased_outputs(ops, dev):
     """The producer's output must not share memory with the residual it
-    updates (other workgroups still read it): the op raises."""
+    updates (other workgroups still read it), and row_ss must hold this N's
+    partial-sum count: the op raises."""
     M, K, N = 2, 4096, 3072
     W, s = synthetic.weight_fp8(N, K, seed=6)
     x = synthetic.activations(M, K, seed=7).to(dev)
     res = synthetic.activations(M, N, seed=8).to(dev)
     nw = synthetic.norm_weight(N, seed=9).to(dev)
-    ss = torch.empty(M, N // 16, dtype=torch.float32, device=dev)
+    ss = torch.empty(M, ops.esimd_gemv_fp8_add_rms_norm_defer_groups(N), dtype=torch.float32, device=dev)
     with pytest.raises(RuntimeError):
         ops.esimd_gemv_fp8_add_rms_norm_defer(x, W.to(dev), s.to(dev), res, nw, res, ss)
+    with pytest.raises(RuntimeError):   # row_ss of the 16-column runs: not this N's G
+        ops.esimd_gemv_fp8_add_rms_norm_defer(x, W.to(dev), s.to(dev), res, nw,
+                                              torch.empty(M, N, dtype=torch.float16, device=dev),
+                                              torch.empty(M, N // 16, dtype=torch.float32, device=dev))
 
 
 def test_unsupported_shapes_raise(ops, dev):

@@ -678,7 +678,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   constexpr bool PROD = EPI == EPI_ADDNORM || EPI == EPI_ADDNORM12;  // deferred-norm producer
   static_assert(!PROD || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !XF8 &&
                                        std::is_same<T, TO>::value),
-                "deferred norm producer: one 16-row tile, fp16 / bf16");
+                "deferred norm producer: one 16- or 12-row tile, fp16 / bf16");
   static_assert(EPI != EPI_ROWSCALE || (MB == 1 && !NORM && !XF8), "deferred norm consumer: fp16 / bf16, M <= 16");
   static_assert(EPI != EPI_ROWSCALE || STEPS >= 2, "deferred norm consumer: row scales at stage 1, before tile 0 ends");
   constexpr int NS = STEPS * TPW;  // stages of the workgroup

@@ -1411,7 +1411,10 @@ static A8w8Plan plan_a8w8_rounds(int64_t M, int64_t N, int64_t K, bool allow_spl
 // pipelined path, and 10% faster than the best unsplit plan.  At M = 64
 // (config 3's prefill-sized decode) the split plans measured 1.2-1.8x faster
 // than the weight-streaming kernels, and 8 parts of 512 K values slower than
-// 4 (M = 64, K = 4096: 13.8 against 11.2 us).
+// 4 (M = 64, K = 4096: 13.8 against 11.2 us).  The split 64 x 128 launches
+// run a 3-slot ring (72 KB per workgroup, two per CU): M = 64, N = 6144,
+// weights from HBM, K = 4096 15.3 -> 13.2 us, K = 5120 16.0 -> 13.2 us; M = 96
+// 17.4 -> 16.4 us.
 static A8w8Plan plan_a8w8(int64_t M, int64_t N, int64_t K, bool pipe_ok, bool allow_split) {
   if (pipe_ok && M >= 128 && N >= 128) return plan_a8w8_rounds(M, N, K, allow_split);
   A8w8Plan best{0, 1};
@@ -1610,7 +1613,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
       if (cfg == 6) CEK_A8W8_SPLITS(TY, 256, 128, 2, 4, 1, 4, 3);                      \
       else if (cfg == 5) CEK_A8W8_SPLITS(TY, 128, 256, 2, 4, 1, 4, 3);                 \
       else if (cfg == 1) CEK_A8W8_SPLITS(TY, 128, 128, 2, 2, 2, 4, 2);                 \
-      else CEK_A8W8_SPLITS(TY, 64, 128, 2, 2, 2, 2, 2);                                \
+      else CEK_A8W8_SPLITS(TY, 64, 128, 2, 2, 2, 2, 3);                                \
     } else if (cfg == 6) {                                                             \
       CEK_A8W8_PIPE(TY, 256, 128, 2, 4, 1, 4, 3);                                      \
     } else if (cfg == 5) {                                                             \

@@ -39,6 +39,9 @@ int main(void) {
   expect(cek_gelu_and_mul(p, p, 4, 64, 100, 64, CEK_F16, NULL), CEK_ERR_INVALID, "gelu x stride");
   expect(cek_qk_norm_rope(p, p, p, p, NULL, 4, 2, 2, 1024, 2048, 2048, 1e-6f, 1e4f, 1, CEK_F16, NULL),
          CEK_ERR_INVALID, "rope head_dim");
+  expect((int)cek_gemv_fp8_add_rms_norm_defer_groups(3072), 256, "defer groups N = 3072 (12-column runs)");
+  expect((int)cek_gemv_fp8_add_rms_norm_defer_groups(4096), 256, "defer groups N = 4096 (16-column runs)");
+  expect((int)cek_gemv_fp8_add_rms_norm_defer_groups(100), 0, "defer groups N % 16");
   if (fails == 0) printf("ok\n");
   return fails != 0;
 }

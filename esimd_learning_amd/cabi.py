@@ -45,7 +45,8 @@ SIGNATURES = {
     "cek_gemv_fp8_qk_norm_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _p, _i64, _i64,
                                        _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_add_rms_norm_defer_groups": (_i64, [_i64]),
-    "cek_gemv_fp8_add_rms_norm_defer": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _i, _i, _p]),
+    "cek_defer_norm_shift": (_i, [_f]),
+    "cek_gemv_fp8_add_rms_norm_defer": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_pern_rs": (_i, [_p, _p, _p, _p, _p, _i64, _f, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_gelu_and_mul_rs": (_i, [_p, _p, _p, _p, _p, _i64, _f, _i64, _i64, _i64, _i, _i, _i, _p]),
     "cek_gemv_fp8_qk_norm_rope_rs": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _p, _p,

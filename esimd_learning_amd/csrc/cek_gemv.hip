@@ -87,13 +87,18 @@ struct NormArgs {
   float* ss_out;      // EPI_ADDNORM(12): per-tile sums of squares [M][N / tile rows]
   const float* ss_in; // EPI_ROWSCALE: the producer's [M][nss] sums of squares
   int nss;
+  float yscale = 1.f; // EPI_ADDNORM(12): 2^-shift, applied to y and (squared) to the sums
 };
 
 // Deferred RMSNorm between two GEMVs (EPI in gemv_lds_kernel).
 // EPI_ADDNORM (the producer, e.g. o_proj): after the tile's sums, o =
 // Out(sum * scale) as usual, then s = o + r (fp32), r = Out(s) in place,
-// y = Out(f32(r) * w[n]) -- the norm's weight product without its 1 / rms
-// -- and the tile's sum of s^2 per row to ss_out[m][tile].
+// y = Out(f32(r) * w[n] * 2^-E) -- the norm's weight product without its
+// 1 / rms -- and the tile's sum of (s * 2^-E)^2 per row to ss_out[m][tile]
+// (E = the caller's shift, yscale = 2^-E: both products are exact in fp32,
+// so only the final rounding differs from E = 0, and with 2^E >= max |w|
+// no y can exceed |r| <= the largest finite value of Out; the consumer,
+// given eps * 4^-E, then computes the same 1 / rms times 2^E).
 // EPI_ADDNORM12: the same producer with 12-row tiles, for N whose 16-row
 // tiles leave CUs idle (N = 3072: 256 workgroups instead of 192; each
 // wave streams 3 rows, lanes 12-15 of the MFMA operand repeat row 11 and
@@ -440,6 +445,7 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
   uint32_t pw = pnw;
   asm volatile("" : "+v"(pw));  // the conversion stays here, after the loads are long in
   const float wn = T::to_f32((uint16_t)pw);
+  const float ys = na.yscale, ys2 = ys * ys;  // powers of two: exact products
   f4 c = acc;
 #pragma unroll
   for (int w = 0; w < 3; ++w) c += red[w * 64 + lane];
@@ -450,10 +456,10 @@ __device__ inline void lds_reduce_addnorm(const f4& acc, uint8_t* smem, int wave
     const float o = T::to_f32(T::from_f32(f32_round(c[v] * sc)));
     const float sv = o + T::to_f32((uint16_t)pres[v]);
     const uint16_t rp = T::from_f32(sv);
-    s2[v] = col ? f32_round(sv * sv) : 0.f;  // rounded before the sums (no fma contraction)
+    s2[v] = col ? f32_round(sv * sv) * ys2 : 0.f;  // rounded before the sums (no fma contraction)
     if (col && m < M) {
       na.r_out[(size_t)m * N + n] = rp;
-      sr.y[(size_t)m * N + n] = T::from_f32(f32_round(T::to_f32(rp) * wn));
+      sr.y[(size_t)m * N + n] = T::from_f32(f32_round(f32_round(T::to_f32(rp) * wn) * ys));
     }
   }
   // each D row (one 16-lane DPP row): the tile's 16 lanes, pairwise
@@ -1356,8 +1362,10 @@ static void launch_norm_t(GemvSegs& sg, const NormArgs& na, int skind, int M, in
   else by_rows(std::integral_constant<int, 5>{});
 }
 
-// Whether [a, a + a_bytes) and [b, b + b_bytes) share a byte.
+// Whether [a, a + a_bytes) and [b, b + b_bytes) share a byte (an empty
+// range shares none).
 static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
+  if (a_bytes <= 0 || b_bytes <= 0 || !a || !b) return false;
   const char* pa = static_cast<const char*>(a);
   const char* pb = static_cast<const char*>(b);
   return pa < pb + b_bytes && pb < pa + a_bytes;
@@ -1628,13 +1636,20 @@ int launch_gemv_tail(const void* x, const void* w, const void* scale, int skind,
   if (M > 4 || (K != 3072 && K != 4096 && K != 5120) || fp8_fmt != CEK_E4M3 || N % 16 != 0) return CEK_ERR_UNSUPPORTED;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16)) return CEK_ERR_UNSUPPORTED;
   // the output is re-read by the tail: it must not share memory with the
-  // inputs, nor with the q copy that other heads' tails write meanwhile
-  if (overlaps(y, M * N * 2, x, M * K * 2) || overlaps(y, M * N * 2, w, N * K)) return CEK_ERR_UNSUPPORTED;
-  if (na.tail.qcopy) {
-    const int64_t qb = M * na.tail.nq * 16 * tp * 2;
-    if (overlaps(na.tail.qcopy, qb, y, M * N * 2) || overlaps(na.tail.qcopy, qb, x, M * K * 2) ||
-        overlaps(na.tail.qcopy, qb, w, N * K))
-      return CEK_ERR_UNSUPPORTED;
+  // inputs, nor with the q copy that other heads' tails write meanwhile;
+  // every workgroup reads the weight scale, the q / k norm weights, the
+  // positions and (deferred norm) the partial sums while others write the
+  // output and the q copy
+  {
+    const int64_t hd = 16 * (int64_t)tp;
+    const int64_t scb = N * (skind == SK_F32 ? 4 : 2);
+    const int64_t qb = na.tail.qcopy ? M * na.tail.nq * hd * 2 : 0;
+    const std::pair<const void*, int64_t> ins[] = {
+        {x, M * K * 2}, {w, N * K}, {scale, scb}, {na.tail.qw, na.tail.nq > 0 ? hd * 2 : 0},
+        {na.tail.kw, na.tail.nk > 0 ? hd * 2 : 0}, {na.tail.pos, M * 8}, {na.ss_in, na.ss_in ? M * na.nss * 4 : 0}};
+    for (const auto& [p, b] : ins)
+      if (overlaps(y, M * N * 2, p, b) || (qb && overlaps(na.tail.qcopy, qb, p, b))) return CEK_ERR_UNSUPPORTED;
+    if (qb && overlaps(na.tail.qcopy, qb, y, M * N * 2)) return CEK_ERR_UNSUPPORTED;
   }
   GemvSegs sg{};
   sg.count = 1;
@@ -1706,17 +1721,21 @@ static int defer_checks(const void* x, const void* w, const void* scale, int ski
 }
 
 int launch_gemv_addnorm(const void* x, const void* w, const void* scale, int skind, void* residual,
-                        const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N, int64_t K,
-                        int io_dtype, int fp8_fmt, hipStream_t st) {
+                        const void* norm_weight, void* y, float* ss_out, int norm_shift, int64_t M, int64_t N,
+                        int64_t K, int io_dtype, int fp8_fmt, hipStream_t st) {
+  if (norm_shift < -24 || norm_shift > 24) return CEK_ERR_INVALID;
   const int rc = defer_checks(x, w, scale, skind, y, M, N, K, io_dtype, fp8_fmt);
   if (rc != CEK_OK || M == 0 || N == 0) return rc;
   if (!residual || !norm_weight || !ss_out) return CEK_ERR_INVALID;
-  // other workgroups still read x and w while one writes y, the residual
-  // and the partial sums
+  // other workgroups still read x, w, the weight scale and the norm weight
+  // while one writes y, the residual and the partial sums
   const int rows = defer_rows(N);
   const int64_t yb = M * N * 2, sb = M * (N / rows) * 4;
+  const int64_t scb = skind == SK_F32_SCALAR ? 4 : N * (skind == SK_F32 ? 4 : 2);
   for (const auto& [p, b] : {std::pair<const void*, int64_t>{y, yb}, {residual, yb}, {ss_out, sb}})
-    if (overlaps(p, b, x, M * K * 2) || overlaps(p, b, w, N * K)) return CEK_ERR_UNSUPPORTED;
+    if (overlaps(p, b, x, M * K * 2) || overlaps(p, b, w, N * K) || overlaps(p, b, scale, scb) ||
+        overlaps(p, b, norm_weight, N * 2))
+      return CEK_ERR_UNSUPPORTED;
   if (overlaps(y, yb, residual, yb) || overlaps(ss_out, sb, y, yb) || overlaps(ss_out, sb, residual, yb))
     return CEK_ERR_UNSUPPORTED;
   GemvSegs sg{};
@@ -1729,6 +1748,7 @@ int launch_gemv_addnorm(const void* x, const void* w, const void* scale, int ski
   na.r_out = static_cast<uint16_t*>(residual);
   na.w = static_cast<const uint16_t*>(norm_weight);
   na.ss_out = ss_out;
+  na.yscale = ldexpf(1.f, -norm_shift);
   const bool f16 = io_dtype == CEK_F16;
   const bool ok = rows == 12 ? (f16 ? launch_defer_k<F16, EPI_ADDNORM12>(x, sg, skind, (int)M, (int)K, na, st)
                                     : launch_defer_k<BF16, EPI_ADDNORM12>(x, sg, skind, (int)M, (int)K, na, st))
@@ -1773,11 +1793,22 @@ int launch_gemv_rowscale(const void* x, const void* w, const void* scale, int sk
 
 extern "C" int64_t cek_gemv_fp8_add_rms_norm_defer_groups(int64_t N) { return cek::defer_groups(N); }
 
+extern "C" int cek_defer_norm_shift(float max_abs_norm_weight) {
+  const float m = fabsf(max_abs_norm_weight);
+  if (!(m > 0.f)) return 0;  // zero or NaN
+  if (m > 0x1p24f) return 24;
+  int e;
+  const float f = frexpf(m, &e);  // m = f 2^e, f in [0.5, 1): 2^e > m >= 2^(e-1)
+  const int s = f == 0.5f ? e - 1 : e;
+  return s < -24 ? -24 : s;
+}
+
 extern "C" int cek_gemv_fp8_add_rms_norm_defer(const void* x, const void* w, const void* scale, void* residual,
-                                               const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N,
-                                               int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream) {
-  return cek::launch_gemv_addnorm(x, w, scale, cek::scale_kind(scale_dtype), residual, norm_weight, y, ss_out, M, N, K,
-                                  io_dtype, fp8_fmt, (hipStream_t)stream);
+                                               const void* norm_weight, void* y, float* ss_out, int norm_shift,
+                                               int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt,
+                                               int scale_dtype, void* stream) {
+  return cek::launch_gemv_addnorm(x, w, scale, cek::scale_kind(scale_dtype), residual, norm_weight, y, ss_out,
+                                  norm_shift, M, N, K, io_dtype, fp8_fmt, (hipStream_t)stream);
 }
 
 extern "C" int cek_gemv_fp8_pern_rs(const void* x, const void* w, const void* scale, void* y, const float* row_ss,

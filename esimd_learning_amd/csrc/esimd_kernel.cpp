@@ -562,12 +562,14 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
 
 // Deferred RMSNorm between two decode GEMVs (up to four rows, e4m3
 // weights).  The producer GEMV (e.g. o_proj) adds its rounded output into
-// the residual in place, writes output = residual * norm_weight (the norm
-// without its 1 / rms) and row_ss [M, G], G = defer_groups(N), the sums of
-// squares of the unrounded sums over G equal runs of columns; the consumer ops below (the plain GEMV,
-// gate/up with gelu_and_mul, QKV with QK-norm + RoPE) take that output and
-// row_ss and scale their rows by rsqrt(sum / K + eps).  No fallback: shapes
-// the kernels do not take raise, and the caller runs the unfused ops.
+// the residual in place, writes output = residual * norm_weight * 2^-shift
+// (the norm without its 1 / rms; the shift keeps it finite) and row_ss
+// [M, G], G = defer_groups(N), the sums of squares of the unrounded sums
+// times 2^-shift over G equal runs of columns; the consumer ops below (the
+// plain GEMV, gate/up with gelu_and_mul, QKV with QK-norm + RoPE) take that
+// output and row_ss and scale their rows by rsqrt(sum / K + eps), with
+// eps * 4^-shift for the norm's eps.  No fallback: shapes the kernels do not
+// take raise, and the caller runs the unfused ops.
 static void check_defer_common(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& weight_scale,
                                const at::Tensor& output, const char* op, int64_t& M, int64_t& N, int64_t& K) {
   check_gemv_io(input, output, op);
@@ -595,9 +597,13 @@ static void check_row_ss(const at::Tensor& row_ss, const at::Tensor& input, int6
 
 int64_t esimd_gemv_fp8_add_rms_norm_defer_groups(int64_t N) { return cek_gemv_fp8_add_rms_norm_defer_groups(N); }
 
+int64_t esimd_defer_norm_shift(double max_abs_norm_weight) {
+  return cek_defer_norm_shift((float)max_abs_norm_weight);
+}
+
 void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
                                        at::Tensor residual, at::Tensor norm_weight, at::Tensor output,
-                                       at::Tensor row_ss) {
+                                       at::Tensor row_ss, int64_t norm_shift) {
   const char* op = "esimd_gemv_fp8_add_rms_norm_defer";
   int64_t M, N, K;
   check_defer_common(input, weight, weight_scale, output, op, M, N, K);
@@ -616,11 +622,12 @@ void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::
   check_contig(row_ss, op, "row_ss");
   TORCH_CHECK(row_ss.numel() == M * cek_gemv_fp8_add_rms_norm_defer_groups(N), op,
               ": row_ss must be [M, esimd_gemv_fp8_add_rms_norm_defer_groups(N)]");
+  TORCH_CHECK(norm_shift >= -24 && norm_shift <= 24, op, ": norm_shift must be in [-24, 24]");
   const int scale_code = scale_code_of(weight_scale, N, op);
   c10::OptionalDeviceGuard guard(input.device());
   check_rc(cek_gemv_fp8_add_rms_norm_defer(input.data_ptr(), weight.data_ptr(), weight_scale.data_ptr(),
                                            residual.data_ptr(), norm_weight.data_ptr(), output.data_ptr(),
-                                           static_cast<float*>(row_ss.data_ptr()), M, N, K,
+                                           static_cast<float*>(row_ss.data_ptr()), (int)norm_shift, M, N, K,
                                            io_code(input.scalar_type()), fp8_code(weight), scale_code,
                                            current_stream(input)),
            op);

@@ -64,8 +64,9 @@ TORCH_LIBRARY(custom_esimd_kernels_vllm, m) {
   m.impl("esimd_gemv_fp8_qk_norm_rope", c10::DispatchKey::CUDA, &esimd_gemv_fp8_qk_norm_rope);
 
   m.def("esimd_gemv_fp8_add_rms_norm_defer_groups(int N) -> int", &esimd_gemv_fp8_add_rms_norm_defer_groups);
+  m.def("esimd_defer_norm_shift(float max_abs_norm_weight) -> int", &esimd_defer_norm_shift);
   m.def("esimd_gemv_fp8_add_rms_norm_defer(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) residual, "
-        "Tensor norm_weight, Tensor(b!) output, Tensor(c!) row_ss) -> ()");
+        "Tensor norm_weight, Tensor(b!) output, Tensor(c!) row_ss, int norm_shift=0) -> ()");
   m.impl("esimd_gemv_fp8_add_rms_norm_defer", c10::DispatchKey::CUDA, &esimd_gemv_fp8_add_rms_norm_defer);
 
   m.def("esimd_gemv_fp8_pern_rs(Tensor input, Tensor weight, Tensor weight_scale, Tensor(a!) output, "

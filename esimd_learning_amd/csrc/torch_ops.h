@@ -63,9 +63,10 @@ void esimd_gemv_fp8_qk_norm_rope(at::Tensor input, at::Tensor weight, at::Tensor
 // Deferred RMSNorm between two decode GEMVs: the producer (residual add,
 // norm weight, per-tile sums of squares) and the row-scaled consumers.
 int64_t esimd_gemv_fp8_add_rms_norm_defer_groups(int64_t N);
+int64_t esimd_defer_norm_shift(double max_abs_norm_weight);
 void esimd_gemv_fp8_add_rms_norm_defer(at::Tensor input, at::Tensor weight, at::Tensor weight_scale,
                                        at::Tensor residual, at::Tensor norm_weight, at::Tensor output,
-                                       at::Tensor row_ss);
+                                       at::Tensor row_ss, int64_t norm_shift);
 void esimd_gemv_fp8_pern_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,
                             at::Tensor row_ss, double eps);
 void esimd_gemv_fp8_gelu_and_mul_rs(at::Tensor input, at::Tensor weight, at::Tensor weight_scale, at::Tensor output,

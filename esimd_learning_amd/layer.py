@@ -40,9 +40,12 @@ kernels take) each add+RMSNorm is split across the two
 GEMVs around it instead of running as a launch of its own: the producer
 GEMV (o_proj; in ``forward``, also the down projection of every layer but
 the last, for the next layer's input norm) adds its output into the
-residual, writes residual * w and per-16-column sums of squares, and the
-consumer (gate/up, the next layer's QKV) scales its rows by the 1 / rms
-those sums give (esimd_gemv_fp8_add_rms_norm_defer and the ``_rs`` ops).
+residual, writes residual * w * 2^-shift and per-16-column sums of squares
+(times 4^-shift), and the consumer (gate/up, the next layer's QKV) scales
+its rows by the 2^shift / rms those sums give with eps * 4^-shift
+(esimd_gemv_fp8_add_rms_norm_defer and the ``_rs`` ops).  The shift, the
+smallest with 2^shift >= max|w|, bounds residual * w * 2^-shift by the
+residual itself, so the hand-off cannot overflow fp16.
 Two launches fewer per layer; the values match the unfused layer to within
 the rounding of the moved 1 / rms, not bit for bit (``defer_norm=False``
 gives the step that equals the separate ops bit for bit).
@@ -102,6 +105,12 @@ class GemmaDecodeLayer:
         self.defer_norm = (defer_norm and dtype == torch.float16 and M <= 4 and e4m3 and self.fuse_tails and fuse_glu
                            and shapes)
         if self.defer_norm:
+            # the producers write residual * w * 2^-shift with 2^shift >= max|w|,
+            # which cannot overflow fp16 whatever the residual holds; the
+            # consumers then take eps * 4^-shift (the weights are read back
+            # once, here)
+            self.shift_in = self.ops.esimd_defer_norm_shift(self.w_in)
+            self.shift_post = self.ops.esimd_defer_norm_shift(self.w_post)
             groups = self.ops.esimd_gemv_fp8_add_rms_norm_defer_groups(self.hidden)
             ss = lambda: torch.empty(M, groups, dtype=torch.float32, device=device)  # noqa: E731
             self.ss_o, self.ss_d = ss(), ss()    # after o_proj; after down (the next layer's input norm)
@@ -121,10 +130,10 @@ class GemmaDecodeLayer:
         """hidden, residual: [M, hidden] (residual updated in place); returns out.
 
         defer_norm only: with ``ss_in`` (the previous layer's ss_d) hidden
-        already holds residual * w_in of the previous layer's deferred input
-        norm of this layer and residual its sum; with ``next_norm`` (the next
-        layer's w_in) the down projection produces that for the next layer
-        and ss_d."""
+        already holds residual * w_in * 2^-shift_in of the previous layer's
+        deferred input norm of this layer and residual its sum; with
+        ``next_norm`` (the next layer's (w_in, shift_in)) the down projection
+        produces that for the next layer and ss_d."""
         o, hd, nq, nk = self.ops, self.hd, self.nq, self.nk
         if self.fuse_norm:
             return self._step_fused(hidden, residual, positions)
@@ -198,13 +207,18 @@ class GemmaDecodeLayer:
                                           nq, nk, eps, self.theta, True, self.cnt_rope, self.attn)
         else:
             o.esimd_gemv_fp8_qk_norm_rope_rs(hidden, self.Wqkv, self.sqkv, self.qkv, self.qw, self.kw, positions,
-                                             nq, nk, eps, self.theta, True, self.cnt_rope, ss_in, eps, self.attn)
-        o.esimd_gemv_fp8_add_rms_norm_defer(self.attn, self.Wo, self.so, residual, self.w_post, self.o, self.ss_o)
-        o.esimd_gemv_fp8_gelu_and_mul_rs(self.o, self.Wgu, self.sgu, self.act, self.ss_o, eps)
+                                             nq, nk, eps, self.theta, True, self.cnt_rope, ss_in,
+                                             eps * 4.0 ** -self.shift_in, self.attn)
+        o.esimd_gemv_fp8_add_rms_norm_defer(self.attn, self.Wo, self.so, residual, self.w_post, self.o, self.ss_o,
+                                            self.shift_post)
+        o.esimd_gemv_fp8_gelu_and_mul_rs(self.o, self.Wgu, self.sgu, self.act, self.ss_o,
+                                         eps * 4.0 ** -self.shift_post)
         if next_norm is None:
             o.esimd_gemv_fp8_pern(self.act, self.Wd, self.sd, self.out, self.hidden, self.mlp)
         else:
-            o.esimd_gemv_fp8_add_rms_norm_defer(self.act, self.Wd, self.sd, residual, next_norm, self.out, self.ss_d)
+            w_next, shift_next = next_norm
+            o.esimd_gemv_fp8_add_rms_norm_defer(self.act, self.Wd, self.sd, residual, w_next, self.out, self.ss_d,
+                                                shift_next)
         return self.out
 
     def capture(self, hidden, residual, positions, stream=None):
@@ -236,7 +250,7 @@ def forward(layers, hidden, residual, positions):
         nxt = layers[i + 1] if i + 1 < len(layers) else None
         chain = nxt is not None and layer.defer_norm and nxt.defer_norm
         if layer.defer_norm:
-            h = layer.step(h, residual, positions, ss_in=ss, next_norm=nxt.w_in if chain else None)
+            h = layer.step(h, residual, positions, ss_in=ss, next_norm=(nxt.w_in, nxt.shift_in) if chain else None)
         else:
             h = layer.step(h, residual, positions)
         ss = layer.ss_d if chain else None

@@ -30,6 +30,7 @@ from custom_esimd_kernels_vllm.ops import (  # noqa: F401
     gemv_tail_counters,
     esimd_gemv_fp8_add_rms_norm_defer,
     esimd_gemv_fp8_add_rms_norm_defer_groups,
+    esimd_defer_norm_shift,
     esimd_gemv_fp8_pern_rs,
     esimd_gemv_fp8_gelu_and_mul_rs,
     esimd_gemv_fp8_qk_norm_rope_rs,

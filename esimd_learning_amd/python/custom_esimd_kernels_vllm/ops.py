@@ -154,15 +154,16 @@ def gemv_tail_counters(n_q, n_k, device) -> torch.Tensor:
 def esimd_gemv_fp8_qk_norm_rope(
     input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
     q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor, n_q: int, n_k: int,
-    eps: float, theta: float = 10000.0, is_neox: bool = True, counters: torch.Tensor = None,
+    eps: float, theta: float, is_neox: bool, counters: torch.Tensor,
     q_out: torch.Tensor = None,
 ) -> None:
     """The QKV GEMV (esimd_gemv_fp8_pern into output [M, N]) followed by
     esimd_qk_norm_rope on its q columns [0, n_q hd) and k columns
     [n_q hd, (n_q + n_k) hd), in one launch for decode batches.  counters:
     int32 device tensor of >= 64 * (n_q + n_k) elements
-    (``gemv_tail_counters``), zero before the first call and left zero by
-    each.  q_out (optional, [M, n_q hd]) also receives the rotated q heads,
+    (``gemv_tail_counters``, allocated once by the caller, not per call, so
+    that the call can be captured in a graph), zero before the first call and
+    left zero by each.  q_out (optional, [M, n_q hd]) also receives the rotated q heads,
     as a copy of output's q columns would."""
     _ops.esimd_gemv_fp8_qk_norm_rope(input, weight, weight_scale, output, q_weight, k_weight, positions, n_q, n_k,
                                      eps, theta, is_neox, counters, q_out)
@@ -176,18 +177,31 @@ def esimd_gemv_fp8_add_rms_norm_defer_groups(N: int) -> int:
     return _ops.esimd_gemv_fp8_add_rms_norm_defer_groups(N)
 
 
+def esimd_defer_norm_shift(norm_weight: torch.Tensor) -> int:
+    """The norm_shift E for esimd_gemv_fp8_add_rms_norm_defer with this norm
+    weight: the smallest E with 2^E >= max|norm_weight| (so that the
+    producer's output cannot overflow whatever the residual holds).  Reads
+    the weight's maximum back to the host: call it once per weight, not per
+    step."""
+    return _ops.esimd_defer_norm_shift(float(norm_weight.float().abs().max()))
+
+
 def esimd_gemv_fp8_add_rms_norm_defer(
     input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, residual: torch.Tensor,
-    norm_weight: torch.Tensor, output: torch.Tensor, row_ss: torch.Tensor,
+    norm_weight: torch.Tensor, output: torch.Tensor, row_ss: torch.Tensor, norm_shift: int = 0,
 ) -> None:
     """The producer half of an add + RMSNorm deferred into the next GEMV
     (up to four rows, e4m3 weights): o = the GEMV's rounded output; residual
-    += o in place; output = residual * norm_weight (rounded; the norm
-    without its 1 / rms); row_ss [M, G] fp32, G =
+    += o in place; output = residual * norm_weight * 2^-norm_shift (rounded;
+    the norm without its 1 / rms); row_ss [M, G] fp32, G =
     ``esimd_gemv_fp8_add_rms_norm_defer_groups(N)``, = the sums of squares of
-    the unrounded o + residual over G equal runs of columns.  Feed output and
-    row_ss to a ``*_rs`` op, which applies rsqrt(sum(row_ss[m]) / N + eps)."""
-    _ops.esimd_gemv_fp8_add_rms_norm_defer(input, weight, weight_scale, residual, norm_weight, output, row_ss)
+    the unrounded (o + residual) * 2^-norm_shift over G equal runs of
+    columns.  Feed output and row_ss to a ``*_rs`` op with eps *
+    4^-norm_shift, which then applies 2^norm_shift / rms.  With norm_shift =
+    ``esimd_defer_norm_shift(norm_weight)`` the output cannot overflow; with
+    0 an fp16 output overflows where |residual * norm_weight| > 65504."""
+    _ops.esimd_gemv_fp8_add_rms_norm_defer(input, weight, weight_scale, residual, norm_weight, output, row_ss,
+                                           norm_shift)
 
 
 def esimd_gemv_fp8_pern_rs(

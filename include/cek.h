@@ -180,8 +180,10 @@ int cek_gemm_fp8_a8w8_ws(const uint8_t* a, const float* sa, const uint8_t* b, co
  * nothing.  Shapes whose plan needs more (cek_gemm_fp8_a8w8_workspace_size
  * above 33554432 bytes) return CEK_ERR_SCRATCH; shapes that run unsplit use
  * no scratch.  The first call on a device looks up the buffer's address on
- * that device.  All calls on one GPU share the buffer: calls that overlap in
- * time there (e.g. on two streams) race.
+ * that device (a host query, no allocation); make that call once at set-up,
+ * outside any graph capture, after which calls may be captured.  All calls
+ * on one GPU share the buffer: calls that overlap in time there (e.g. on two
+ * streams, or two replays of graphs holding such calls) race.
  */
 int cek_gemm_fp8_a8w8_noalloc(const uint8_t* a, const float* sa, const uint8_t* b, const float* sb,
                               void* y, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
@@ -267,19 +269,26 @@ int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, v
  *
  * Producer, cek_gemv_fp8_add_rms_norm_defer: o = the GEMV's rounded output
  * [M, N]; s = o + residual (fp32); residual = round(s) in place;
- * y = round(residual * norm_weight[n]) -- the norm without its 1 / rms --
- * and ss_out [M][G], G = cek_gemv_fp8_add_rms_norm_defer_groups(N): the sums
- * of s^2 over each of G equal runs of N / G columns (G = N / 16, or N / 12
- * where 16-column runs would give fewer than 256 workgroups and N is a
- * multiple of 48: N = 3072 -> 256).  y, residual and ss_out must not overlap
- * each other, x or w.
+ * y = round(residual * norm_weight[n] * 2^-norm_shift) -- the norm without
+ * its 1 / rms -- and ss_out [M][G], G = cek_gemv_fp8_add_rms_norm_defer_groups(N):
+ * the sums of (s * 2^-norm_shift)^2 over each of G equal runs of N / G
+ * columns (G = N / 16, or N / 12 where 16-column runs would give fewer than
+ * 256 workgroups and N is a multiple of 48: N = 3072 -> 256).  Both products
+ * are exact in fp32, so the shift only moves y's one rounding.  With
+ * 2^norm_shift >= max |norm_weight| (cek_defer_norm_shift) |y| <= |residual|,
+ * so y cannot overflow a 16-bit type whatever the residual holds; with
+ * norm_shift = 0 an fp16 y overflows once |residual * norm_weight| > 65504.
+ * |norm_shift| <= 24 (else CEK_ERR_INVALID).  y, residual and ss_out must
+ * not overlap each other, x, w, the weight scale or norm_weight.
  *
  * Consumers (_rs): the named op over x = the producer's y, with each output
  * row m scaled, before rounding (and before gelu_and_mul, QK-norm and RoPE),
  * by inv[m] = rsqrt(sum_j row_ss[m][j] / K + row_eps); n_ss = the producer's
  * G (<= 256, a multiple of 4, row_ss 16-byte aligned), summed in a fixed
- * order.  The result equals the unfused norm -> GEMV to within the rounding
- * of the moved 1 / rms (not bit for bit).
+ * order.  For the norm's eps pass row_eps = eps * 4^-norm_shift: the scaled
+ * sums then give 2^norm_shift / rms, which undoes the producer's shift.
+ * The result equals the unfused norm -> GEMV to within the rounding of the
+ * moved 1 / rms (not bit for bit).
  *
  * All: M <= 4, K a multiple of 1024 (producer and plain consumer: K / 1024
  * in {2, 3, 4, 5, 14, 24}; gate/up and QKV: 3072, 4096, 5120), N % 16 == 0,
@@ -287,9 +296,11 @@ int cek_gemv_fp8_qk_norm_rope(const void* x, const void* w, const void* scale, v
  * fallback: run the unfused ops).
  */
 int64_t cek_gemv_fp8_add_rms_norm_defer_groups(int64_t N);  /* G for N (a multiple of 16), else 0 */
+/* The smallest shift E with 2^E >= max_abs_norm_weight (0 for 0, clamped to +-24). */
+int cek_defer_norm_shift(float max_abs_norm_weight);
 int cek_gemv_fp8_add_rms_norm_defer(const void* x, const void* w, const void* scale, void* residual,
-                                    const void* norm_weight, void* y, float* ss_out, int64_t M, int64_t N, int64_t K,
-                                    int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
+                                    const void* norm_weight, void* y, float* ss_out, int norm_shift, int64_t M,
+                                    int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype, void* stream);
 int cek_gemv_fp8_pern_rs(const void* x, const void* w, const void* scale, void* y, const float* row_ss, int64_t n_ss,
                          float row_eps, int64_t M, int64_t N, int64_t K, int io_dtype, int fp8_fmt, int scale_dtype,
                          void* stream);

@@ -42,6 +42,10 @@ int main(void) {
   expect((int)cek_gemv_fp8_add_rms_norm_defer_groups(3072), 256, "defer groups N = 3072 (12-column runs)");
   expect((int)cek_gemv_fp8_add_rms_norm_defer_groups(4096), 256, "defer groups N = 4096 (16-column runs)");
   expect((int)cek_gemv_fp8_add_rms_norm_defer_groups(100), 0, "defer groups N % 16");
+  expect(cek_defer_norm_shift(1.36f), 1, "defer shift max|w| 1.36");
+  expect(cek_defer_norm_shift(8.0f), 3, "defer shift max|w| 8");
+  expect(cek_gemv_fp8_add_rms_norm_defer(p, p, p, p, p, p, NULL, 25, 4, 3072, 4096, CEK_F16, CEK_E4M3, CEK_F32, NULL),
+         CEK_ERR_INVALID, "defer shift out of range");
   if (fails == 0) printf("ok\n");
   return fails != 0;
 }

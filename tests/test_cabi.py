@@ -67,6 +67,21 @@ def test_defer_norm_groups():
     assert [g(n) for n in (0, 100, -16)] == [0, 0, 0]
 
 
+def test_defer_norm_shift():
+    """The deferred-norm producer's shift for a norm weight's max |w|: the
+    smallest E with 2^E >= max|w| (so residual * w * 2^-E never exceeds the
+    residual), clamped to [-24, 24]; 0 for 0 and NaN.  Host arithmetic only."""
+    lib = cabi.load()
+    f = lib.cek_defer_norm_shift
+    cases = {1.0: 0, 1.36: 1, 2.0: 1, 2.01: 2, 8.0: 3, 8.31: 4, 0.3: -1, 0.5: -1, 0.75: 0, 65504.0: 16,
+             0.0: 0, -3.0: 2, 1e-30: -24, 1e30: 24, float("nan"): 0, float("inf"): 24}
+    for m, e in cases.items():
+        assert f(m) == e, (m, f(m), e)
+    for m in (0.37, 1.0001, 3.9, 4.0, 123.4, 6e-5):
+        e = f(m)
+        assert 2.0 ** e >= m > 2.0 ** (e - 1), (m, e)
+
+
 def test_host_rejects_invalid_arguments():
     """Argument checks return before any HIP call, so they run without a GPU."""
     lib = cabi.load()

@@ -61,13 +61,13 @@ def _butterfly16(sq, groups):
     return a[..., 0]
 
 
-def _producer(ops, x, W, s, r, w, dtype, dev):
+def _producer(ops, x, W, s, r, w, dtype, dev, shift=0):
     M, N = x.shape[0], W.shape[0]
     rd = r.to(dev).clone()
     y = torch.full((M, N), float("nan"), dtype=dtype, device=dev)
     ss = torch.full((M, ops.esimd_gemv_fp8_add_rms_norm_defer_groups(N)), float("nan"), dtype=torch.float32,
                     device=dev)
-    ops.esimd_gemv_fp8_add_rms_norm_defer(x.to(dev), W.to(dev), s.to(dev), rd, w.to(dev), y, ss)
+    ops.esimd_gemv_fp8_add_rms_norm_defer(x.to(dev), W.to(dev), s.to(dev), rd, w.to(dev), y, ss, shift)
     torch.cuda.synchronize()
     return rd.cpu(), y.cpu(), ss.cpu()
 
@@ -97,6 +97,94 @@ def test_producer(ops, dev, M, K, N, dtype):
     assert torch.equal(r1, r_ref)
     assert torch.equal(y1, torch.from_numpy(r_ref.float().numpy() * wf).to(dtype))
     assert torch.equal(ss1, torch.from_numpy(_butterfly16(sv * sv, G)))
+
+
+def test_defer_norm_shift_values(ops):
+    """The shift is the smallest E with 2^E >= max|w| (host function)."""
+    for m, e in ((1.0, 0), (1.36, 1), (2.0, 1), (8.0, 3), (8.31, 4), (0.3, -1), (0.5, -1), (0.0, 0), (65504.0, 16)):
+        assert ops.esimd_defer_norm_shift(torch.tensor([m, -m / 2])) == e, m
+
+
+@pytest.mark.parametrize("N", [3072, 4096])
+def test_producer_shift_large_residual(ops, dev, N):
+    """|residual| up to 3e4 and a norm weight up to ~8: residual * w
+    reaches ~2.4e5, past fp16's 65504.  With the shift from
+    esimd_defer_norm_shift (3 or 4), output = round(residual * w * 2^-shift) and the
+    sums (times 4^-shift) equal the host's fp32 arithmetic bit for bit and are
+    finite; with shift 0 the output overflows to inf (the documented limit
+    of an unshifted hand-off)."""
+    M, K, dtype = 4, 4096, torch.float16
+    _say(f"defer producer shift N={N}")
+    W, s = synthetic.weight_fp8(N, K, seed=N + 21)
+    x = synthetic.activations(M, K, seed=22)
+    r = (synthetic.activations(M, N, seed=23).float() * 1e4).clamp(-3e4, 3e4).half()
+    w = (synthetic.norm_weight(N, seed=24).float() * 6.0).half()
+    shift = ops.esimd_defer_norm_shift(w.to(dev))
+    m = w.float().abs().max().item()
+    assert 2.0 ** shift >= m > 2.0 ** (shift - 1) and shift >= 3
+    o, _, _ = _producer(ops, x, W, s, torch.zeros(M, N, dtype=dtype), w, dtype, dev)  # the GEMV's rounded output
+    of = o.float().numpy()
+    r1, y1, ss1 = _producer(ops, x, W, s, r, w, dtype, dev, shift)
+    sv = (of + r.float().numpy()).astype(np.float32)
+    r_ref = torch.from_numpy(sv).to(dtype)
+    assert torch.equal(r1, r_ref)
+    ys = np.float32(2.0 ** -shift)
+    y_ref = torch.from_numpy((r_ref.float().numpy() * w.float().numpy()).astype(np.float32) * ys).to(dtype)
+    assert torch.isfinite(y1.float()).all()
+    assert torch.equal(y1, y_ref)
+    G = ss1.shape[1]
+    assert torch.equal(ss1, torch.from_numpy(_butterfly16((sv * sv).astype(np.float32) * (ys * ys), G)))
+    _, y0, _ = _producer(ops, x, W, s, r, w, dtype, dev, 0)
+    assert not torch.isfinite(y0.float()).all()
+
+
+@pytest.mark.parametrize("consumer", ["pern", "glu"])
+def test_defer_extreme_rows_vs_oracle(ops, dev, consumer):
+    """Producer (K = 4096 -> N = 3072, config 5's hidden size) then a
+    consumer (the plain GEMV to 4096, or gate/up + gelu_and_mul to d = 1024)
+    against the oracle's unfused chain (GEMV, add+RMSNorm, GEMV / gate-up +
+    gelu_and_mul), row by row, on rows whose residual rms is 1e4 (|r|
+    clipped to 3e4), 1, 1e-4 and 1e-5 (the tiny rows with a zero GEMV input,
+    so that their sums are the residual's alone), with a norm weight up to
+    ~8 (shift 3 or 4).  Below rms ~1e-5 the fp16 residual
+    itself holds fewer than 8 significant bits and the moved rounding leaves
+    the tolerance (a CPU model of the arithmetic: 3.5-4% of max|out| at
+    rms 1e-6, 0.3-0.5% at 1e-5)."""
+    from oracle import act as oact
+    from oracle import norm as onorm
+    M, K, H, d, dtype = 4, 4096, 3072, 1024, torch.float16
+    _say(f"defer extreme rows {consumer}")
+    Wo, so = synthetic.weight_fp8(H, K, seed=31)
+    rows = torch.tensor([1e4, 1.0, 1e-4, 1e-5])[:, None]
+    x = (synthetic.activations(M, K, seed=32).float() * torch.tensor([1.0, 1.0, 0.0, 0.0])[:, None]).half()
+    r = (synthetic.activations(M, H, seed=33).float() * rows).clamp(-3e4, 3e4).half()
+    w = (synthetic.norm_weight(H, seed=34).float() * 6.0).half()
+    N2 = 2 * d if consumer == "glu" else 4096
+    W2, s2 = synthetic.weight_fp8(N2, H, seed=35)
+    shift = ops.esimd_defer_norm_shift(w)
+    assert shift >= 3
+    rd = r.to(dev).clone()
+    y = torch.empty(M, H, dtype=dtype, device=dev)
+    ss = torch.empty(M, ops.esimd_gemv_fp8_add_rms_norm_defer_groups(H), dtype=torch.float32, device=dev)
+    ops.esimd_gemv_fp8_add_rms_norm_defer(x.to(dev), Wo.to(dev), so.to(dev), rd, w.to(dev), y, ss, shift)
+    out = torch.full((M, d if consumer == "glu" else N2), float("nan"), dtype=dtype, device=dev)
+    eps_s = EPS * 4.0 ** -shift
+    if consumer == "glu":
+        ops.esimd_gemv_fp8_gelu_and_mul_rs(y, W2.to(dev), s2.to(dev), out, ss, eps_s)
+    else:
+        ops.esimd_gemv_fp8_pern_rs(y, W2.to(dev), s2.to(dev), out, ss, eps_s)
+    torch.cuda.synchronize()
+    o = ogemv.gemv_fp8_pern(x, Wo, so).to(dtype)
+    r_new, normed = onorm.fused_add_rms_norm(o, r, w, EPS)
+    ref = ogemv.gemv_fp8_pern(normed.to(dtype), W2, s2)
+    if consumer == "glu":
+        ref = torch.from_numpy(oact.gelu_and_mul(ref.to(dtype).float().numpy())).to(dtype)
+    else:
+        ref = ref.to(dtype)
+    assert_close_fp(rd.cpu().float(), r_new.float(), "residual")
+    for m in range(M):
+        err, mx = assert_close_fp(out.cpu()[m].float(), ref[m].float(), f"{consumer} row {m} (rms {rows[m, 0]:g})")
+        print(f"  row {m} rms {rows[m, 0]:g}: max err / max|ref| = {err / mx:.2e}")
 
 
 def _ss_of(v, nss):
@@ -263,3 +351,70 @@ def test_forward_deferred_vs_oracle(ops, dev, dtype):
         assert torch.equal(stack[1].out, out)
         assert torch.equal(rb, ref_r)
         torch.randn(1000, device=dev).sum().item()   # unrelated eager work between replays
+
+
+def test_forward_deferred_large_residual_vs_oracle(ops, dev):
+    """Two config-5 layers (fp16, norms deferred) on a residual stream of
+    |r| up to 3e4 (N(0, 1e4) clipped) with the add+RMSNorm weights scaled
+    to ~8 (so residual * w reaches ~2.5e5, past fp16): the producers' shift
+    keeps the hand-off finite; output and residual against the oracle's two
+    decoder steps."""
+    M, dims = 4, CONFIG5
+    _say("defer forward, large residual")
+    ps = [synthetic.gemma_layer(seed=sd, **dims) for sd in (80, 81)]
+    for p in ps:
+        for k in ("w_in", "w_post"):
+            p[k] = (p[k].float() * 6.0).half()
+    stack = [GemmaDecodeLayer(p, M, dev) for p in ps]
+    assert all(layer.defer_norm and layer.shift_in >= 3 and layer.shift_post >= 3 for layer in stack)
+    h = synthetic.activations(M, dims["hidden"], seed=82)
+    r = (synthetic.activations(M, dims["hidden"], seed=83).float() * 1e4).clamp(-3e4, 3e4).half()
+    pos = synthetic.positions(M, seed=84)
+    rd = r.to(dev)
+    out = forward(stack, h.to(dev), rd, pos.to(dev)).clone()
+    torch.cuda.synchronize()
+    o1, r1, _ = olayer.decoder_step(ps[0], h, r, pos)
+    o2, r2, _ = olayer.decoder_step(ps[1], o1.to(h.dtype), r1, pos)
+    assert_close_fp(rd.cpu().float(), r2.float(), "residual after two layers")
+    err, mx = assert_close_fp(out.cpu().float(), o2.float(), "output of two layers")
+    print(f"  output max err / max|ref| = {err / mx:.2e}")
+
+
+def test_forward_eight_layers_as_benched(ops, dev):
+    """The decode forward the benchmark times (bench_layer): eight chained
+    config-5 layers sharing one weight set (seed 10; the bench gives each
+    layer its own copy of the same values), M = 4, fp16, the default step
+    (both add+RMSNorms deferred across the GEMVs around them, QK-norm+RoPE
+    in the QKV GEMV's tail, gate/up with gelu_and_mul), hidden, residual and
+    positions from seeds 20, 21 and 22; run once eagerly, and its graph
+    replayed.  Output and residual against eight oracle decoder steps, to
+    the op pack's tolerance; the errors are printed as max-abs / max|ref|."""
+    M, L = 4, 8
+    _say("defer forward, eight layers")
+    p = synthetic.gemma_layer(seed=10)
+    pd = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in p.items()}
+    stack = [GemmaDecodeLayer(pd, M, dev) for _ in range(L)]
+    assert all(layer.defer_norm and layer.fuse_tails and layer.fuse_glu for layer in stack)
+    h = synthetic.activations(M, p["hidden"], seed=20)
+    r = synthetic.activations(M, p["hidden"], seed=21)
+    pos = synthetic.positions(M, seed=22)
+    hd, rd, posd = h.to(dev), r.to(dev), pos.to(dev)
+    out = forward(stack, hd.clone(), rd, posd).clone()
+    torch.cuda.synchronize()
+    ho, ro = h, r
+    for _ in range(L):
+        o, ro, _ = olayer.decoder_step(p, ho, ro, pos)
+        ho = o.to(h.dtype)
+    err_r, mr = assert_close_fp(rd.cpu().float(), ro.float(), "residual after eight layers")
+    err_o, mo = assert_close_fp(out.cpu().float(), o.float(), "output after eight layers")
+    print(f"  eight layers: output max err / max|ref| = {err_o / mo:.2e}, residual {err_r / mr:.2e}")
+    # the captured forward (what the bench replays) gives the same values
+    hb, rb = hd.clone(), r.to(dev)
+    g = capture_forward(stack, hb, rb, posd)
+    for _ in range(2):
+        hb.copy_(hd)
+        rb.copy_(r.to(dev))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(stack[-1].out, out)
+        assert torch.equal(rb, rd)

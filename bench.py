@@ -234,6 +234,55 @@ def bench_gemv_table(ops, torch, shapes=((4096, 14336), (4096, 6144), (4096, 409
     return rows
 
 
+def bench_gemv_scaling(ops, torch, K=4096, N0=14336, mults=(1, 2, 4, 8, 16)):
+    """The M = 1 GEMV and the read probe at K = 4096 over N = 14336 x
+    (1, 2, 4, 8, 16) rows (58.7 to 940 MB of weights; random finite e4m3
+    codes, made on the device), each timed over > 2 GB of rotating copies
+    (graph of two passes over the copies, event-timed), and per kernel a
+    least-squares line t = fixed + bytes / rate through its five times: the
+    fixed cost of a launch (ramp-up, first-byte latency, the last
+    workgroups' tail) and the marginal streaming rate.  best_frac_of_spec is
+    what one pass over the headline's 58.7 MB reaches on this part: those
+    bytes over the probe's time at that size, against 8 TB/s."""
+    import numpy as np
+    from esimd_learning_amd import cabi
+    lib = cabi.load()
+    dev = "cuda:0"
+    stream = torch.cuda.Stream()
+    gen = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(1, K, device=dev, generator=gen).half()
+    rows = []
+    for mlt in mults:
+        N = N0 * mlt
+        wb = N * K
+        copies = max(2, math.ceil(ROTATE_BYTES / wb))
+        Ws = [torch.randint(0, 0x7E, (N, K), device=dev, dtype=torch.uint8, generator=gen).view(torch.float8_e4m3fn)
+              for _ in range(copies)]
+        sd = torch.rand(N, device=dev, generator=gen) * 1e-3
+        y = torch.empty(1, N, dtype=torch.float16, device=dev)
+        pfns = [(lambda W=W: cabi.check(lib.cek_hbm_read_probe(W.data_ptr(), wb, None, cabi.stream_ptr(stream))))
+                for W in Ws] * 2
+        gfns = [(lambda W=W: ops.esimd_gemv_fp8_pern(x, W, sd, y, N, K)) for W in Ws] * 2
+        _, p_ms, _ = time_graph(pfns, torch, stream, warm_s=0.2)
+        _, g_ms, _ = time_graph(gfns, torch, stream, warm_s=0.2)
+        rows.append({"N": N, "weight_MB": round(wb / 1e6, 1), "gemv_us": round(g_ms * 1e3 / len(gfns), 3),
+                     "probe_us": round(p_ms * 1e3 / len(pfns), 3)})
+        del Ws
+        torch.cuda.empty_cache()
+    b = np.array([r["weight_MB"] * 1e6 for r in rows])
+    fit = {}
+    for key in ("gemv_us", "probe_us"):
+        t = np.array([r[key] for r in rows])
+        slope, icpt = np.polyfit(b, t, 1)          # us per byte, us
+        resid = t - (slope * b + icpt)
+        fit[key[:-3]] = {"fixed_us": round(float(icpt), 3), "marginal_TBps": round(1e6 / float(slope) / 1e12, 3),
+                         "max_residual_us": round(float(np.abs(resid).max()), 3)}
+    hb = N0 * K
+    return {"K": K, "rows": rows, "fit": fit,
+            "best_frac_of_spec": round(hb / (rows[0]["probe_us"] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+            "gemv_frac_of_probe": round(rows[0]["probe_us"] / rows[0]["gemv_us"], 4)}
+
+
 def bench_norm_quant_gemv(ops, torch, reps=50, N=6144):
     """fused add+RMSNorm+per-token e4m3 quant, then the
     fp8 x fp8 GEMV/GEMM to N = 6144 on its codes and scales.  Per (T, H):
@@ -538,6 +587,95 @@ def bench_layer(torch, steps, M=4, rounds=5, layers=LAYERS):
     return out
 
 
+def bench_parity(ops, torch, eps=1e-6):
+    """Parity of the measured paths against the CPU oracle, computed after
+    every timed region (nothing here is timed):
+      * config 3 (T in {1, 8, 32, 64} x H in {4096, 5120}, the norm+quant
+        leg's inputs): the per-token e4m3 quant of the device's normed rows
+        against the oracle's quant of the same rows -- code and scale
+        mismatches (expected 0) and the rounding ties among them; the fused
+        add+RMSNorm+quant against the oracle's -- residual mismatches
+        (expected 0), rows whose scale differs, and codes that differ (by at
+        most one step: the normed value rounds differently where the sum of
+        squares is taken in another order);
+      * config 5: the decode forward bench_layer times (eight layers of one
+        weight set, the default deferred-norm step), run once eagerly,
+        against eight oracle decoder steps: max-abs error / max|ref| of the
+        output and of the residual."""
+    from esimd_learning_amd import synthetic
+    from esimd_learning_amd.layer import GemmaDecodeLayer, forward
+    from oracle import fp8 as ofp8
+    from oracle import layer as olayer
+    from oracle import norm as onorm
+    import numpy as np
+    dev = "cuda:0"
+    mag = lambda c: np.where(c & 0x80, -(c & 0x7F), c & 0x7F).astype(np.int64)  # noqa: E731  monotone code order
+    tot = {"elements": 0, "quant_code_mismatches": 0, "quant_scale_mismatches": 0, "quant_ties": 0,
+           "fused_residual_mismatches": 0, "fused_rows_scale_differs": 0, "fused_code_diffs": 0,
+           "fused_code_max_step": 0}
+    rows = []
+    for H in (4096, 5120):
+        w = synthetic.norm_weight(H, seed=H)
+        for T in (1, 8, 32, 64):
+            h = synthetic.activations(T, H, seed=T)
+            r = synthetic.activations(T, H, seed=T + 1)
+            hd, rd, wd = h.to(dev), r.to(dev), w.to(dev)
+            # per-token quant of the device's normed rows
+            h2, r2 = hd.clone(), rd.clone()
+            ops.esimd_fused_add_rms_norm_batched(h2, r2, wd, eps)
+            q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+            s = torch.empty(T, dtype=torch.float32, device=dev)
+            ops.esimd_per_token_quant_fp8(h2, q, s)
+            # fused add+RMSNorm+quant
+            r1 = rd.clone()
+            q1 = torch.empty_like(q)
+            s1 = torch.empty_like(s)
+            ops.esimd_fused_add_rms_norm_quant_fp8(hd, r1, wd, eps, q1, s1)
+            torch.cuda.synchronize()
+            xf = h2.cpu().float().numpy()
+            q_ref, s_ref = ofp8.per_token_quant(xf)
+            sn = s.cpu().numpy()
+            v = np.clip((xf / sn[:, None]).astype(np.float32), -448, 448).astype(np.float32)
+            qm = int((q.view(torch.uint8).cpu().numpy() != q_ref).sum())
+            sm = int((sn.view(np.uint32) != s_ref.view(np.uint32)).sum())
+            ties = int(ofp8.e4m3_is_tie(v).sum())
+            r_ref, qf_ref, sf_ref, _ = onorm.fused_add_rms_norm_quant(h, r, w, eps)
+            rm = int((r1.cpu() != r_ref).sum())
+            srows = int((s1.cpu().numpy() != sf_ref.numpy()).sum())
+            d = np.abs(mag(q1.view(torch.uint8).cpu().numpy()) - mag(qf_ref.numpy()))
+            row = {"T": T, "H": H, "quant_code_mismatches": qm, "quant_scale_mismatches": sm, "quant_ties": ties,
+                   "fused_residual_mismatches": rm, "fused_rows_scale_differs": srows,
+                   "fused_code_diffs": int((d != 0).sum()), "fused_code_max_step": int(d.max())}
+            rows.append(row)
+            tot["elements"] += T * H
+            for k in row:
+                if k == "fused_code_max_step":
+                    tot[k] = max(tot[k], row[k])
+                elif k not in ("T", "H"):
+                    tot[k] += row[k]
+    out = {"config3_norm_quant": {"totals": tot, "rows": rows}}
+    # config 5: the benchmarked forward against the oracle
+    M, L = 4, LAYERS
+    p = synthetic.gemma_layer(seed=10)
+    pd = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in p.items()}
+    stack = [GemmaDecodeLayer(pd, M, dev) for _ in range(L)]
+    h = synthetic.activations(M, p["hidden"], seed=20)
+    r = synthetic.activations(M, p["hidden"], seed=21)
+    pos = synthetic.positions(M, seed=22)
+    rd = r.to(dev)
+    y = forward(stack, h.to(dev), rd, pos.to(dev))
+    torch.cuda.synchronize()
+    ho, ro = h, r
+    for _ in range(L):
+        o, ro, _ = olayer.decoder_step(p, ho, ro, pos)
+        ho = o.to(h.dtype)
+    frac = lambda a, b: round(float((a.cpu().float() - b.float()).abs().max() / b.float().abs().max()), 6)  # noqa: E731
+    out["config5_forward"] = {"layers": L, "defer_norm": all(ly.defer_norm for ly in stack),
+                              "output_maxerr_over_maxref": frac(y, o),
+                              "residual_maxerr_over_maxref": frac(rd, ro), "bound": 0.01}
+    return out
+
+
 def _cpu_model():
     """The host CPU's model name (lscpu, else /proc/cpuinfo) and socket/core counts."""
     import subprocess
@@ -654,6 +792,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--no-parity", action="store_true", help="skip the post-timing parity counts against the oracle")
     ap.add_argument("--no-tables", action="store_true", help="skip the config-2 GEMV table and config-3 legs")
     ap.add_argument("--small-ops-only", action="store_true",
                     help="run only the small-kernel leg (norm, quant, gelu_and_mul, QK-norm+RoPE) and print it")
@@ -732,6 +871,10 @@ def main():
         out["roofline"]["frac_of_copy"] = round(g["achieved"] / cbw, 4)
         log(f"device copy: {cbw:.0f} GB/s (read + write); GEMV at {g['achieved'] / cbw:.1%} of it")
     if not a.no_tables:
+        out["gemv_scaling"] = bench_gemv_scaling(ops, torch)
+        gs = out["gemv_scaling"]["fit"]
+        log(f"gemv scaling: gemv fixed {gs['gemv']['fixed_us']} us + {gs['gemv']['marginal_TBps']} TB/s; probe fixed "
+            f"{gs['probe']['fixed_us']} us + {gs['probe']['marginal_TBps']} TB/s")
         out["gemv_shapes"] = bench_gemv_table(ops, torch)
         log("gemv table: " + ", ".join(f"M{r['M']}/{r['K']}x{r['N']}={r['us']}us" for r in out["gemv_shapes"]))
         out["norm_quant_gemv"] = bench_norm_quant_gemv(ops, torch)
@@ -751,6 +894,13 @@ def main():
         dl = out["decoder_layer"]
         log(f"layer: {dl['us_per_step']} us/step, {dl['weight_GBps']} GB/s; " +
             ", ".join(f"{k} {dl[k]}" for k in LAYER_VARIANTS if k != "us_per_step"))
+    if not a.no_parity:
+        log("parity against the oracle ...")
+        out["parity"] = bench_parity(ops, torch)
+        pt = out["parity"]["config3_norm_quant"]["totals"]
+        pf = out["parity"]["config5_forward"]
+        log(f"parity: quant mismatches {pt['quant_code_mismatches']} (ties {pt['quant_ties']}), fused code diffs "
+            f"{pt['fused_code_diffs']} of {pt['elements']}; 8-layer forward err {pf['output_maxerr_over_maxref']}")
     if not a.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch)

@@ -402,6 +402,46 @@ def bench_gemm_all(ops, torch, steps, warmup, all_m=True):
     return head
 
 
+def bench_gemm_k_scaling(ops, torch, M=2048, N=6144, Ks=(1024, 2048, 4096, 8192, 12288), reps=20):
+    """The headline a8w8 shape's time against K (M = 2048, N = 6144: one
+    256 x 192 tile per CU, K / 128 steps each; random finite e4m3 codes,
+    operands re-read from the Infinity Cache; a graph of `reps` launches,
+    event-timed, warmed) and a least-squares line t = fixed + steps x
+    per_step: the fixed cost of a launch (its dispatch, the first loads, the
+    epilogue's output stores) and the time of one K step (48 MFMAs per SIMD).
+    Also the same flops on 256 x 256 tiles with 24 steps each (M = 2048,
+    K = 3072, N = 8192): the step count a stream-K schedule of the
+    headline's 192 tiles of 256 x 256 would give every CU, before any
+    fix-up of the tiles it splits."""
+    import numpy as np
+    dev = "cuda:0"
+    stream = torch.cuda.Stream()
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def timed(M_, K_, N_):
+        a = torch.randint(0, 0x7E, (M_, K_), device=dev, dtype=torch.uint8, generator=gen)
+        b = torch.randint(0, 0x7E, (N_, K_), device=dev, dtype=torch.uint8, generator=gen)
+        sa = torch.rand(M_, device=dev, generator=gen) * 1e-3
+        sb = torch.rand(N_, device=dev, generator=gen) * 1e-3
+        y = torch.empty(M_, N_, dtype=torch.float16, device=dev)
+        fn = lambda: ops.esimd_gemm_fp8_a8w8(a, sa, b, sb, y)  # noqa: E731
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        _, ms, _ = time_graph([fn] * reps, torch, stream, warm_s=0.3)
+        return ms * 1e3 / reps
+
+    rows = [{"K": K, "steps": K // 128, "us": round(timed(M, K, N), 2)} for K in Ks]
+    st = np.array([r["steps"] for r in rows], dtype=np.float64)
+    t = np.array([r["us"] for r in rows])
+    per_step, fixed = np.polyfit(st, t, 1)
+    mfma_us = 48 * 32 / 2.4e3  # one step's MFMA cycles per SIMD at the 2.4 GHz of the 5 PF spec
+    return {"M": M, "N": N, "tile": "256 x 192, one per CU", "rows": rows,
+            "fixed_us": round(float(fixed), 2), "per_step_us": round(float(per_step), 4),
+            "per_step_mfma_us_at_2p4GHz": round(mfma_us, 4),
+            "equal_flops_256x256_24_steps_us": round(timed(2048, 3072, 8192), 2)}
+
+
 def bench_gemm_pert(ops, torch, steps, warmup, M=2048, rotate=False):
     """The reference's prefill op esimd_gemm_fp8_pert (fp16 activations, e4m3
     weights, fp32 per-tensor scale; the w8a16 fp16-MFMA path) at the three
@@ -794,6 +834,8 @@ def main():
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--no-parity", action="store_true", help="skip the post-timing parity counts against the oracle")
     ap.add_argument("--no-tables", action="store_true", help="skip the config-2 GEMV table and config-3 legs")
+    ap.add_argument("--gemm-headline-only", action="store_true",
+                    help="run only the headline a8w8 GEMM leg (M=2048, K=4096, N=6144) and print it (counter runs)")
     ap.add_argument("--small-ops-only", action="store_true",
                     help="run only the small-kernel leg (norm, quant, gelu_and_mul, QK-norm+RoPE) and print it")
     ap.add_argument("--warm-s", type=float, default=None,
@@ -821,6 +863,9 @@ def main():
         torch.cuda.synchronize()
         log(f"copy reference: 10 x {src.numel()} bytes")
         del src, dst
+    if a.gemm_headline_only:
+        print(json.dumps({"gemm": bench_gemm(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))}), flush=True)
+        return
     if a.small_ops_only:
         print(json.dumps({"small_ops": bench_small_ops(ops, torch, reps=max(20, a.steps // 2))}), flush=True)
         return
@@ -883,7 +928,12 @@ def main():
         log("small ops: " + ", ".join(f"{r['op']}/T{r['T']}={r['us']}us" for r in out["small_ops"]))
     if not a.no_gemm:
         out["gemm"] = bench_gemm_all(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
+        out["gemm"]["roofline"]["traffic"] = load_traffic("gemm_a8w8_pipe_kernel_m2048_k4096_n6144")
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")
+        out["gemm_k_scaling"] = bench_gemm_k_scaling(ops, torch)
+        gk = out["gemm_k_scaling"]
+        log(f"gemm k scaling: fixed {gk['fixed_us']} us + {gk['per_step_us']} us per K step; 256x256 x 24 steps "
+            f"{gk['equal_flops_256x256_24_steps_us']} us")
         out["gemm_pert"] = bench_gemm_pert(ops, torch, max(10, a.steps // 40), max(3, a.warmup // 10))
         log("gemm pert (w8a16): " + ", ".join(f"{r['config']}={r['avg_launch_us']}us/{r['tflops']}TF"
                                               for r in out["gemm_pert"]))

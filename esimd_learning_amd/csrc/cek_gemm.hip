@@ -159,15 +159,19 @@ __device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
 // 2048 x 6144).  Writing straight from the MFMA layout instead stores 2 bytes
 // per lane, four rows per instruction, and took 20-40% of a K = 4096 GEMM.
 // In LDS, the 16-byte column chunk k of tile row r sits at k ^ 2 ((r >> 2) & 3),
-// so the four row groups of an accumulator write land in distinct banks.
-// smem must hold BM * BN * 2 bytes; every wave must be done with it (the
-// leading barrier).
+// so the four row groups of an accumulator write land in distinct banks;
+// where a tile row is not a multiple of 8 chunks (BN = 96) the rows are
+// instead BN * 2 + 16 bytes apart (rows 4 apart then start 16 banks apart).
+// smem must hold out_tile_bytes(BM, BN) bytes; every wave must be done with
+// it (the leading barrier).
 // With SL (scales in LDS), rs and cs point at LDS copies of the tile's BM row
 // and BN column scales (loaded by the kernel's prologue, outside smem's first
 // BM * BN * 2 bytes) instead of the global vectors.
 // With wskind >= 0 the column scale is the weight scale ws of that kind
 // (ScaleKind: per channel fp16 / bf16 / fp32, or one fp32 value), in place
 // of cs * s0.
+constexpr int out_tile_bytes(int BM, int BN) { return BM * ((BN / 8) % 8 == 0 ? BN * 2 : BN * 2 + 16); }
+
 template <typename T, int BM, int BN, int WM, int WN, int NT = 256, bool SL = false>
 __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], uint8_t* smem, int wm, int wn,
                                   int lane, int m0, int n0, int M, int N, const float* rs, const float* cs,
@@ -175,7 +179,9 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
                                   int nlo = 0, const void* ws = nullptr, int wskind = -1) {
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
   constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
-  static_assert(CPR % 8 == 0, "the chunk swizzle stays inside aligned groups of 8");
+  constexpr bool XS = CPR % 8 == 0;          // chunk swizzle (inside aligned groups of 8), else padded rows
+  constexpr int RS = XS ? BN * 2 : BN * 2 + 16;  // LDS bytes per tile row
+  auto cpos = [](int r, int k) { return XS ? k ^ (2 * ((r >> 2) & 3)) : k; };
   const int r16 = lane & 15, g = lane >> 4;
   float rsv[FM][4];
 #pragma unroll
@@ -200,8 +206,7 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = wm * TM + i * 16 + 4 * g + v;  // D row = 4 * (lane >> 4) + v
-        const int chunk = (c >> 3) ^ (2 * ((r >> 2) & 3));
-        *reinterpret_cast<uint16_t*>(smem + r * (BN * 2) + chunk * 16 + (c & 7) * 2) =
+        *reinterpret_cast<uint16_t*>(smem + r * RS + cpos(r, c >> 3) * 16 + (c & 7) * 2) =
             T::from_f32(acc[i][j][v] * rsv[i][v] * cv);
       }
   }
@@ -211,7 +216,7 @@ __device__ inline void store_tile(const f4 (&acc)[BM / WM / 16][BN / WN / 16], u
     const int r = q / CPR, k = q % CPR;
     const int m = m0 + r, n = n0 + 8 * k;
     if (m >= M || n >= N || m < mlo) continue;
-    const uint8_t* src = smem + r * (BN * 2) + (k ^ (2 * ((r >> 2) & 3))) * 16;
+    const uint8_t* src = smem + r * RS + cpos(r, k) * 16;
     uint16_t* dst = Y + (size_t)m * N + n;
     if (vec && n >= nlo) {
       __builtin_nontemporal_store(*reinterpret_cast<const u4*>(src), reinterpret_cast<u4*>(dst));
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_lds_kernel(
     }
   }
 
-  static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
+  static_assert(sizeof(smem) >= out_tile_bytes(BM, BN), "output tile must fit the stages");
   store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, sa, sb, 1.f, Y);
 }
 
@@ -332,8 +337,7 @@ struct PipeCfg {
   static constexpr int FM = TM / 16, FN = TN / 16;
   static constexpr int ASLOT = BM * BK, BSLOT = BN * BK;
   static constexpr int NW = WM * WN;
-  static constexpr int ACH = BM / 8 / NW, BCH = BN / 8 / NW;  // 1 KB loads per wave and slot (all waves loading)
-  static_assert(ACH * 8 * NW == BM && BCH * 8 * NW == BN, "writer chunks cover the tile");
+  static_assert(TM * WM == BM && TN * WN == BN && TM % 16 == 0 && TN % 16 == 0, "wave tiles cover the tile");
   static_assert(FM % 2 == 0, "A fragments alternate between two register sets");
 };
 
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   static_assert(LW >= 1 && LW <= NW, "loader waves");
   static_assert(RING >= 2 && RING <= 4, "ring slots");
   constexpr int RINGS = RING * (C::ASLOT + C::BSLOT);
-  constexpr int SMEM = RINGS > BM * BN * 2 ? RINGS : BM * BN * 2;
+  constexpr int SMEM = RINGS > out_tile_bytes(BM, BN) ? RINGS : out_tile_bytes(BM, BN);
   static_assert(BM + BN <= 64 * NW, "one scale per thread");
   // the A ring and the B ring (or the output tile), then the tile's row and
   // column scales
@@ -556,7 +560,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   // every wave's loads (a non-loader's scale load included) are complete
   // here: step KT - 2's barrier (the last) waited for vmcnt(0), and with
   // KT == 1 the prologue's did
-  static_assert(SMEM >= BM * BN * 2, "output tile must fit");
+  static_assert(SMEM >= out_tile_bytes(BM, BN), "output tile must fit");
   if constexpr (SPLIT > 1) {
     // fp32 partial sums in D layout: lane l holds column l & 15, rows
     // 4 (l >> 4) + v of each 16 x 16 block (rows before mlo / columns before
@@ -800,7 +804,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_lds_kernel(
     }
   }
 
-  static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
+  static_assert(sizeof(smem) >= out_tile_bytes(BM, BN), "output tile must fit the stages");
   store_tile<T, BM, BN, WM, WN, 64 * NW>(acc, smem, wm, wn, lane, m0, n0, M, N, nullptr, nullptr, 1.f, Y, 0, 0, scale,
                                          skind);
 }
@@ -950,7 +954,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_w8a16_pipe_kernel(
     P::step(kt, KT, RING == 2 ? 0 : c, RING == 2 ? 1 : nxt(c), smem, loader, wave, wm, wn, r16, pa0, pa1, pb, rX, rW,
             ga, gb, acc, a, b0, b1);
 
-  static_assert(sizeof(smem) >= BM * BN * 2, "output tile must fit the stages");
+  static_assert(sizeof(smem) >= out_tile_bytes(BM, BN), "output tile must fit the stages");
   if constexpr (SPLIT > 1) {
     // fp32 partial sums in D layout: lane l holds column l & 15, rows
     // 4 (l >> 4) + v of each 16 x 16 block (rows and columns past the
@@ -1355,11 +1359,11 @@ namespace cek {
 // of lead does not cover on a small tile (M = 512, K = 4096, N = 6144: 64 x
 // 128 in 2 slots 32.0 us, 128 x 128 8-wave in 3 slots 21.5 us).
 struct A8w8Opt { int bm, bn; double rate; int slots; double t0, step; };
-constexpr int kA8w8Cfgs = 7;
+constexpr int kA8w8Cfgs = 8;
 constexpr A8w8Opt kA8w8Opts[kA8w8Cfgs] = {
     {64, 128, 1750, 512, 0.0, 0.686},   {128, 128, 2250, 512, 1.56, 1.085}, {256, 192, 2480, 256, 0.0, 1.461},
     {256, 256, 2650, 256, 0.0, 1.760},  {128, 128, 0, 256, 2.87, 0.560},    {128, 256, 0, 256, 3.65, 0.914},
-    {256, 128, 0, 256, 2.99, 0.957}};
+    {256, 128, 0, 256, 2.99, 0.957},    {128, 96, 0, 256, 2.40, 0.453}};
 constexpr bool a8w8_splits(int c) { return c == 1 || c == 5 || c == 6; }
 
 struct A8w8Plan { int cfg, split; };
@@ -1590,7 +1594,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
 #define CEK_A8W8_PIPE(TY, BM, BN, WM, WN, OCC, LW, RING)                                                \
   do {                                                                                                \
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
-    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, 1, RING, WM * WN == 8 ? 3 : 1>                 \
+    gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, 1, RING, WM * WN == 8 ? (BM / WM >= 48 ? 3 : 2) : 1> \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, nullptr, M, N, K, tm, tn); \
   } while (0)
 #define CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, SP, RING)                                          \
@@ -1614,6 +1618,8 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
       else if (cfg == 5) CEK_A8W8_SPLITS(TY, 128, 256, 2, 4, 1, 4, 3);                 \
       else if (cfg == 1) CEK_A8W8_SPLITS(TY, 128, 128, 2, 2, 2, 4, 2);                 \
       else CEK_A8W8_SPLITS(TY, 64, 128, 2, 2, 2, 2, 3);                                \
+    } else if (cfg == 7) {                                                             \
+      CEK_A8W8_PIPE(TY, 128, 96, 4, 2, 1, 4, 3);                                       \
     } else if (cfg == 6) {                                                             \
       CEK_A8W8_PIPE(TY, 256, 128, 2, 4, 1, 4, 3);                                      \
     } else if (cfg == 5) {                                                             \

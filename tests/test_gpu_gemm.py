@@ -197,14 +197,16 @@ def test_a8w8_large_tiles(ops, dev, M, K, N):
         assert_close_fp(y.cpu(), ref, f"a8w8 M={M} K={K} N={N} {out_dt}")
 
 
-@pytest.mark.parametrize("M,K,N", [(65, 4096, 200), (100, 2048, 512), (300, 4096, 4096), (300, 14336, 4096),
-                                   (512, 14336, 4096), (640, 14336, 4096), (65, 4096, 203), (100, 2048, 1001),
+@pytest.mark.parametrize("M,K,N", [(65, 4096, 200), (100, 2048, 512), (300, 8192, 4096), (300, 14336, 4096),
+                                   (512, 14336, 4096), (200, 8192, 2048), (150, 4096, 1000), (65, 4096, 203),
+                                   (100, 2048, 1001),
                                    (64, 4096, 6144), (64, 14336, 4096), (64, 4096, 300), (64, 4096, 28672)])
 def test_a8w8_split_k(ops, dev, M, K, N):
     """Shapes with too few output tiles split K (the op allocates the
     workspace the plan asks for): 64 x 128 tiles in 8, 4 and 2 parts (M = 64
     included, which without a workspace takes the weight-streaming kernels),
-    128 x 128 in 4 and 2 parts.  Against the CPU oracle;
+    128 x 256 in 4 parts, 128 x 128 (four waves) in 8 and 4 parts.  Against
+    the CPU oracle;
     the unsplit C-ABI call (no workspace) agrees within the same tolerance;
     two split calls agree bit for bit (the parts are added in order), and a
     workspace 4 bytes off 16-byte alignment (the finalize's element-by-element
@@ -242,11 +244,13 @@ def test_a8w8_split_k(ops, dev, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N,parts", [(225, 4096, 339, 4), (516, 2048, 7302, 0), (710, 2048, 5403, 0),
-                                         (516, 16384, 3293, 2), (516, 8192, 1605, 4), (225, 16384, 339, 8),
-                                         (3232, 16384, 550, 2), (1583, 8192, 550, 4), (419, 16384, 339, 8)])
+                                         (537, 16384, 5000, 2), (516, 8192, 1605, 4), (225, 16384, 339, 8),
+                                         (2720, 16384, 1100, 2), (1583, 8192, 550, 4), (419, 16384, 339, 8),
+                                         (500, 2048, 6000, 0), (300, 4096, 3000, 0)])
 def test_a8w8_round_model_tiles(ops, dev, M, K, N, parts):
     """Shapes (ragged in M and N) on which the round-model plan for M >= 128
-    picks each 8-wave, 3-slot tile (128 x 128, 128 x 256, 256 x 128) unsplit
+    picks each 8-wave, 3-slot tile (128 x 128, 128 x 256, 256 x 128, and
+    128 x 96 with its padded epilogue rows: 500 x 6000, 300 x 3000) unsplit
     or split in 2, 4 or 8 parts (`parts`, 0: unsplit; the op allocates the
     workspace), and without a workspace (the bare C-ABI call) the unsplit
     plan, which at 225 x 339 is the 8-wave 128 x 128 tile.  Both against the

@@ -1130,8 +1130,9 @@ constexpr int kA8w8LdsLayout = 1;
 // within 7% of the fastest of sixteen forms (M = 512, K = 14336: 171 -> 68 us
 // split in 4; M = 512, K = 4096, N = 6144: 52 -> 36 us).
 struct W8Opt { int bm, bn; double t0, step; };
-constexpr W8Opt kW8Opts[5] = {{256, 128, 0.49, 0.972}, {256, 192, 6.84, 1.166}, {256, 256, 0.0, 1.595},
-                              {128, 256, 2.05, 0.904}, {128, 128, 0.0, 0.491}};
+constexpr int kW8Cfgs = 6;
+constexpr W8Opt kW8Opts[kW8Cfgs] = {{256, 128, 0.49, 0.972}, {256, 192, 6.84, 1.166}, {256, 256, 0.0, 1.595},
+                                    {128, 256, 2.05, 0.904}, {128, 128, 0.0, 0.491},  {128, 96, 4.30, 0.447}};
 struct W8Plan { int cfg, split; };
 
 static bool w8_off32(int64_t M, int64_t N, int64_t K) {
@@ -1144,13 +1145,17 @@ static W8Plan plan_w8a16(int64_t M, int64_t N, int64_t K, bool allow_split) {
   W8Plan best{-1, 1};
   if (M < 128 || N < 128 || K % 64 != 0 || !w8_off32(M, N, K)) return best;
   double tbest = -1.0;
-  for (int c = 0; c < 5; ++c) {
+  for (int c = 0; c < kW8Cfgs; ++c) {
     const W8Opt& o = kW8Opts[c];
     if (M < o.bm || N < o.bn) continue;
     for (int sp : {1, 2, 4, 8}) {
       const bool ok = sp == 1 ? c != 4 : (allow_split && (c == 0 || c == 3 || (c == 4 && sp >= 4)));
       if (!ok || (K / 64) % sp || (sp > 1 && K / sp < 1024)) continue;
       const int64_t units = ((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn) * sp;
+      // 128 x 96 only as one nearly full round of at most 8192 K values, where
+      // it was measured (M = 384 / 512, N = 6144, K = 1024 .. 8192; with a
+      // quarter or more of the CUs idle, or two rounds, it lost)
+      if (c == 5 && (units > 256 || units < 192 || K > 8192)) continue;
       const int64_t full = units / 256;
       const double f = (double)(units - full * 256) / 256.0;
       const double rounds = (double)full + (f > 0.0 ? 0.6 + 0.4 * f : 0.0);
@@ -1216,6 +1221,14 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
       gemm_splitk_finalize_w<TY, SP><<<dim3((unsigned)((N + 2047) / 2048), (unsigned)(M < 65535 ? M : 65535)),  \
                                         256, 0, st>>>(ws, scale, skind, yp, (int)M, (int)N);                     \
   } while (0)
+// 128 x 96: waves 4 x 2 (32 x 48 wave tiles), two loader waves (the 16-row
+// B load chunks of 96 rows split evenly over 2), 3 slots
+#define CEK_W8P96(TY, F)                                                                                         \
+  do {                                                                                                          \
+    const int tm = (int)((M + 127) / 128), tn = (int)((N + 95) / 96);                                           \
+    gemm_w8a16_pipe_kernel<TY, F, 128, 96, 1, 4, 2, 2, 1, 3>                                                    \
+        <<<dim3((unsigned)(tm * tn)), 512, 0, st>>>(xp, wp, scale, skind, yp, ws, M, N, K, tm, tn);             \
+  } while (0)
 #define CEK_W8P_SPLITS(TY, F, BM, BN)                        \
   do {                                                       \
     if (plan.split == 2) CEK_W8P(TY, F, BM, BN, 2, 3);       \
@@ -1235,6 +1248,8 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
       CEK_W8P(TY, F, 256, 192, 1, 3);                                      \
     } else if (plan.cfg == 2) {                                            \
       CEK_W8P(TY, F, 256, 256, 1, 2);                                      \
+    } else if (plan.cfg == 5) {                                            \
+      CEK_W8P96(TY, F);                                                    \
     } else {                                                               \
       CEK_W8P(TY, F, 128, 256, 1, 3);                                      \
     }                                                                      \
@@ -1244,6 +1259,7 @@ int launch_w8a16(const void* x, const void* w, const void* scale, int skind, voi
       else if (fp8_fmt == CEK_E4M3) CEK_W8P_ALL(BF16, CEK_E4M3);
       else CEK_W8P_ALL(BF16, CEK_E5M2);
 #undef CEK_W8P_ALL
+#undef CEK_W8P96
 #undef CEK_W8P_SPLITS
 #undef CEK_W8P
       return check_launch();

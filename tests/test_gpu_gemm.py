@@ -76,6 +76,8 @@ def test_gemm_pert_prefill(ops, dev, M, K, N):
     (130, 130, 4096, 0, torch.float16, torch.float8_e4m3fn),     # K = 130: not a multiple of 64
     (130, 4096, 130, 4, torch.float16, torch.float8_e4m3fn),     # 128 x 128, 4 parts
     (130, 8192, 130, 8, torch.bfloat16, torch.float8_e4m3fn),    # 128 x 128, 8 parts
+    (500, 2048, 6000, 0, torch.float16, torch.float8_e4m3fn),    # 128 x 96 (4 x 2 waves, padded epilogue rows)
+    (450, 4096, 5000, 0, torch.bfloat16, torch.float8_e5m2),     # 128 x 96
 ])
 def test_gemm_pert_round_model(ops, dev, M, K, N, parts, io, fmt):
     """Ragged shapes (M and N not multiples of the tile) on which the w8a16

@@ -166,7 +166,7 @@ __device__ inline i8 lds_frag(const uint8_t* row, int p0, int p1) {
 // it (the leading barrier).
 // With SL (scales in LDS), rs and cs point at LDS copies of the tile's BM row
 // and BN column scales (loaded by the kernel's prologue, outside smem's first
-// BM * BN * 2 bytes) instead of the global vectors.
+// out_tile_bytes(BM, BN) bytes) instead of the global vectors.
 // With wskind >= 0 the column scale is the weight scale ws of that kind
 // (ScaleKind: per channel fp16 / bf16 / fp32, or one fp32 value), in place
 // of cs * s0.
@@ -1123,9 +1123,11 @@ constexpr int kA8w8LdsLayout = 1;
 // per round: t0 + step per 64-deep K step of one workgroup), fitted to the
 // nine config-4 shapes with operands streamed from HBM (MI355X):
 //  0  256 x 128, 3 slots;   1  256 x 192, 3 slots;   2  256 x 256, 2 slots;
-//  3  128 x 256, 3 slots;   4  128 x 128, 3 slots (split K only).
-// Unsplit: 0-3; split in 2, 4 or 8 parts (K values per part >= 1024): 0 and
-// 3, and 4 in 4 or 8 parts.  On the nine config-4 shapes (HBM and
+//  3  128 x 256, 3 slots;   4  128 x 128, 3 slots (split K only);
+//  5  128 x 96 (4 x 2 waves, two loader waves), 3 slots, unsplit, only as one
+//     round of 192 .. 256 tiles with K <= 8192 (fitted at M = 512, N = 6144).
+// Unsplit: 0-3 and 5; split in 2, 4 or 8 parts (K values per part >= 1024): 0
+// and 3, and 4 in 4 or 8 parts.  On the nine config-4 shapes (HBM and
 // cache-resident) and ten others (M = 128 .. 3000) the plan's pick measured
 // within 7% of the fastest of sixteen forms (M = 512, K = 14336: 171 -> 68 us
 // split in 4; M = 512, K = 4096, N = 6144: 52 -> 36 us).
@@ -1370,7 +1372,10 @@ namespace cek {
 //  4  128 x 128, 8 waves (2 x 4, four loader waves), 3 slots: loads two
 //     steps ahead, one workgroup per CU;
 //  5  128 x 256, 8 waves, 3 slots;
-//  6  256 x 128, 8 waves, 3 slots.
+//  6  256 x 128, 8 waves, 3 slots;
+//  7  128 x 96, 8 waves (4 x 2, wave tile 32 x 48, four loader waves), 3
+//     slots: 256 tiles at M = 512, N = 6144 (K = 4096 from HBM 21.2 -> 19.2
+//     us against 4; t0 / step fitted against 4's model at K = 1024 .. 8192).
 // The 3-slot tiles are for weights streamed from HBM, whose latency one step
 // of lead does not cover on a small tile (M = 512, K = 4096, N = 6144: 64 x
 // 128 in 2 slots 32.0 us, 128 x 128 8-wave in 3 slots 21.5 us).

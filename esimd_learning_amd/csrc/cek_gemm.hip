@@ -403,6 +403,29 @@ __device__ __forceinline__ void a8w8_issue_chunk(int ch, uint8_t* sB, uint8_t* s
 #endif
 }
 
+// The epilogue's scales (the tile's BM row scales from sa, then its BN column
+// scales from sb) go to LDS at sc first, by 4-byte direct-to-LDS loads (one
+// instruction per wave for 64 of them), so that the prologue's wait covers
+// their latency; register loads mixed with the direct-to-LDS ones would make
+// the compiler drain every load before using them.  Waves 0 .. BM / 64 - 1
+// load row scales, the rest column scales.  Each wave issues at most one
+// load, before any of its operand loads.
+template <int BM, int BN, int NW>
+__device__ __forceinline__ void stage_tile_scales(float* sc, const float* sa, const float* sb, int M, int N, int m0,
+                                                  int n0, int wave, int lane) {
+  static_assert(BM % 64 == 0, "a wave's scales come from one of sa, sb");
+  static_assert(BM + BN <= 64 * NW, "one scale per thread");
+  if (64 * wave < BM + BN) {
+    const int t = min(64 * wave + lane, BM + BN - 1);
+    const bool rows = 64 * wave < BM;
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(rows ? sa : sb, (uint32_t)(rows ? M : N) * 4u),
+                                             (lds_ptr_t)(sc + 64 * wave), 4,
+                                             (uint32_t)(rows ? m0 + t : n0 + t - BM) * 4u, 0, 0, 0);
+#endif
+  }
+}
+
 // One K step kt from ring slot c (the next step's slot cn).  Its barrier
 // (before the last MFMA group) waits for step kt + 1's loads, leaves up to
 // RING - 2 later steps' in flight, and is followed by chunk 0 of step
@@ -469,7 +492,6 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   static_assert(RING >= 2 && RING <= 4, "ring slots");
   constexpr int RINGS = RING * (C::ASLOT + C::BSLOT);
   constexpr int SMEM = RINGS > out_tile_bytes(BM, BN) ? RINGS : out_tile_bytes(BM, BN);
-  static_assert(BM + BN <= 64 * NW, "one scale per thread");
   // the A ring and the B ring (or the output tile), then the tile's row and
   // column scales
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + (BM + BN) * 4];
@@ -491,21 +513,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   const int m0 = min(mlo, M - BM), n0 = min(nlo, N - BN);
   const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)((size_t)M * K));
   const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B, (uint32_t)((size_t)N * K));
-  // The epilogue's scales go to LDS first, by 4-byte direct-to-LDS loads
-  // (one instruction per wave for 64 of them), so that the prologue's wait
-  // covers their latency; register loads mixed with the direct-to-LDS ones
-  // would make the compiler drain every load before using them.  Waves
-  // 0 .. BM / 64 - 1 load row scales, the rest column scales.
-  static_assert(BM % 64 == 0, "a wave's scales come from one of sa, sb");
-  if (64 * wave < BM + BN) {
-    const int t = min(64 * wave + lane, BM + BN - 1);
-    const bool rows = 64 * wave < BM;
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(rows ? sa : sb, (uint32_t)(rows ? M : N) * 4u),
-                                             (lds_ptr_t)(sc + 64 * wave), 4,
-                                             (uint32_t)(rows ? m0 + t : n0 + t - BM) * 4u, 0, 0, 0);
-#endif
-  }
+  stage_tile_scales<BM, BN, NW>(sc, sa, sb, M, N, m0, n0, wave, lane);
 
   // loader chunk j = wave + LW i: lane l fills row 8 j + (l >> 3), position
   // l & 7, i.e. logical chunk (l & 7) ^ s(row) (s(row) = row & 7 = (l >> 3)
@@ -581,6 +589,172 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_a8w8_pipe_kernel(
   } else {
     store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y, mlo, nlo);
   }
+}
+
+// ---------------------------------------------------------------------------
+// gemm_a8w8_pipe_kernel with a deeper B ring: A in 2 slots, B in 3, so the
+// B (weight) loads run two K steps ahead instead of one and an HBM miss has
+// two steps to land (M = 2048, K = 4096, N = 6144 with weights from HBM:
+// 45.0 -> 41.2 us; cache-resident 39.6 -> 40.1 us; 256 x 192 needs
+// 2 x 32 + 3 x 24 KB of LDS, a joint third slot 168 KB).  Unsplit only.
+//
+// Load group G(k), issued from the barrier of step k on (chunk 0 there,
+// chunks 1 .. NCH - 1 in the next step's first MFMA groups), is A(k + 2) into
+// A slot k % 2 and B(k + 3) into B slot k % 3 -- the slots step k has just
+// given up -- A loads first.  The barrier of step k needs A(k + 1) (in
+// G(k - 1)) and B(k + 1) (in G(k - 2)); the only loads issued after A(k + 1)
+// are G(k - 1)'s B loads, so the wait leaves those BL in flight
+// (vmcnt(BL) while B(k + 2) exists, vmcnt(0) after).  The prologue loads
+// A(0) B(0), A(1) B(1) and B(2).
+// ---------------------------------------------------------------------------
+
+// Chunk ch (of NCH) of a load group: A step ka's AL loads into sA (if ha),
+// then B step kb's BL loads into sB (if hb); rows and offsets as in
+// a8w8_issue_chunk.
+template <int AL, int BL, int LW, int NCH>
+__device__ __forceinline__ void a8w8_issue_chunk_ab(int ch, uint8_t* sA, uint8_t* sB, int ka, int kb, bool ha, bool hb,
+                                                    int w, __amdgpu_buffer_rsrc_t rA, __amdgpu_buffer_rsrc_t rB, int K,
+                                                    uint32_t ga, uint32_t gb) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int T = AL + BL, CS = (T + NCH - 1) / NCH;
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    if (i < ch * CS || i >= ch * CS + CS) continue;
+    if (i < AL) {
+      if (ha)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr_t)(sA + (w + LW * i) * 1024), 16, ga + (uint32_t)ka,
+                                                 (int)((uint32_t)(i * LW * 8) * (uint32_t)K), 0, 0);
+    } else {
+      if (hb)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr_t)(sB + (w + LW * (i - AL)) * 1024), 16,
+                                                 gb + (uint32_t)kb, (int)((uint32_t)((i - AL) * LW * 8) * (uint32_t)K),
+                                                 0, 0);
+    }
+  }
+#endif
+}
+
+// One K step kt: A slot CA = kt % 2, B slot cb = kt % 3.
+template <int BM, int BN, int WM, int WN, int LW, int NCH, int CA>
+__device__ __forceinline__ void a8w8_b3_step(int kt, int KT, int cb, uint8_t* sAr, uint8_t* sBr, bool loader,
+                                             int wave, int wm, int wn, int r16, int p0, int p1,
+                                             __amdgpu_buffer_rsrc_t rA, __amdgpu_buffer_rsrc_t rB, int K, uint32_t ga,
+                                             uint32_t gb,
+                                             f4 (&acc)[PipeCfg<BM, BN, WM, WN>::FM][PipeCfg<BM, BN, WM, WN>::FN],
+                                             i8 (&a)[2], const i8 (&bc)[PipeCfg<BM, BN, WM, WN>::FN],
+                                             i8 (&bn)[PipeCfg<BM, BN, WM, WN>::FN]) {
+  using C = PipeCfg<BM, BN, WM, WN>;
+  using L = LoadSplit<BM, BN, LW>;
+  constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN;
+  static_assert(NCH >= 1 && NCH <= FM, "chunks 1 .. NCH - 1 go out in the groups before the barrier");
+  const uint8_t* sA = sAr + CA * C::ASLOT + (wm * TM + r16) * BK;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    if (i + 1 < FM) {
+      a[(i + 1) & 1] = lds_frag(sA + (i + 1) * 16 * BK, p0, p1);
+      if (i < NCH - 1 && loader && kt >= 1) {  // chunk i + 1 of G(kt - 1)
+        const int cbp = cb == 0 ? 2 : cb - 1;  // B slot (kt - 1) % 3 = (kt + 2) % 3
+        a8w8_issue_chunk_ab<L::AL, L::BL, LW, NCH>(i + 1, sAr + (1 - CA) * C::ASLOT, sBr + cbp * C::BSLOT,
+                                                   (kt + 1) * BK, (kt + 2) * BK, kt + 1 < KT, kt + 2 < KT, wave, rA,
+                                                   rB, K, ga, gb);
+      }
+    } else if (kt + 1 < KT) {
+      if (kt + 2 < KT) barrier_vmcnt<L::BL>();
+      else barrier_vmcnt<0>();
+      if (loader)  // chunk 0 of G(kt)
+        a8w8_issue_chunk_ab<L::AL, L::BL, LW, NCH>(0, sAr + CA * C::ASLOT, sBr + cb * C::BSLOT, (kt + 2) * BK,
+                                                   (kt + 3) * BK, kt + 2 < KT, kt + 3 < KT, wave, rA, rB, K, ga, gb);
+      const int cbn = cb == 2 ? 0 : cb + 1;
+      const uint8_t* nA = sAr + (1 - CA) * C::ASLOT + (wm * TM + r16) * BK;
+      const uint8_t* nB = sBr + cbn * C::BSLOT + (wn * TN + r16) * BK;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bn[j] = lds_frag(nB + j * 16 * BK, p0, p1);
+      a[0] = lds_frag(nA, p0, p1);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = mfma_fp8_16x16x128(a[i & 1], bc[j], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Tile order: groups of 4 tile rows (the XCD's 32 tiles of a 2048 x 6144
+// output are then 4 x 8 tiles, 10 MB of A and B, against 11 MB for 8 x 4:
+// 1-3% faster with weights from HBM).
+template <typename T, int BM, int BN, int WM, int WN, int LW, int NCH>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_a8w8_pipe_b3_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sa,
+    const uint8_t* __restrict__ B, const float* __restrict__ sb,
+    uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m, int tiles_n) {
+  using C = PipeCfg<BM, BN, WM, WN>;
+  using L = LoadSplit<BM, BN, LW>;
+  constexpr int BK = C::BK, TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NW = C::NW;
+  constexpr int AL = L::AL, BL = L::BL;
+  static_assert(LW >= 1 && LW <= NW, "loader waves");
+  static_assert(AL + 2 * BL <= 63, "vmcnt immediate");
+  constexpr int RINGS = 2 * C::ASLOT + 3 * C::BSLOT;
+  constexpr int SMEM = RINGS > out_tile_bytes(BM, BN) ? RINGS : out_tile_bytes(BM, BN);
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + (BM + BN) * 4];
+  static_assert(sizeof(smem) <= 160 * 1024, "LDS");
+  uint8_t* sAr = smem;
+  uint8_t* sBr = smem + 2 * C::ASLOT;
+  float* sc = reinterpret_cast<float*>(smem + SMEM);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const bool loader = wave < LW;
+  int tm, tn;
+  tile_of<BM, BN, 4>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int mlo = tm * BM, nlo = tn * BN;  // edge tiles moved back inside, as in gemm_a8w8_pipe_kernel
+  const int m0 = min(mlo, M - BM), n0 = min(nlo, N - BN);
+  const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)((size_t)M * K));
+  const __amdgpu_buffer_rsrc_t rB = buf_rsrc(B, (uint32_t)((size_t)N * K));
+  stage_tile_scales<BM, BN, NW>(sc, sa, sb, M, N, m0, n0, wave, lane);
+  const uint32_t cofs = (uint32_t)(((lane & 7) ^ swz<1>(lane >> 3)) * 16);
+  const uint32_t ga = (uint32_t)(m0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs;
+  const uint32_t gb = (uint32_t)(n0 + wave * 8 + (lane >> 3)) * (uint32_t)K + cofs;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int p0 = g ^ swz<1>(r16), p1 = (g + 4) ^ swz<1>(r16);
+
+  f4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  if (loader) {
+    a8w8_issue_chunk_ab<AL, BL, LW, 1>(0, sAr, sBr, 0, 0, true, true, wave, rA, rB, K, ga, gb);
+    a8w8_issue_chunk_ab<AL, BL, LW, 1>(0, sAr + C::ASLOT, sBr + C::BSLOT, BK, BK, KT > 1, KT > 1, wave, rA, rB, K, ga,
+                                       gb);
+    a8w8_issue_chunk_ab<AL, BL, LW, 1>(0, sAr, sBr + 2 * C::BSLOT, 0, 2 * BK, false, KT > 2, wave, rA, rB, K, ga, gb);
+  }
+  // step 0 in (a non-loader has at most its older scale load out)
+  if (KT > 2) barrier_vmcnt<AL + 2 * BL>();
+  else if (KT > 1) barrier_vmcnt<AL + BL>();
+  else barrier_vmcnt<0>();
+  i8 a[2], b0[FN], b1[FN];
+  {
+    const uint8_t* sA = sAr + (wm * TM + r16) * BK;
+    const uint8_t* sB = sBr + (wn * TN + r16) * BK;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) b0[j] = lds_frag(sB + j * 16 * BK, p0, p1);
+    a[0] = lds_frag(sA, p0, p1);
+  }
+  int kt = 0, cb = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    a8w8_b3_step<BM, BN, WM, WN, LW, NCH, 0>(kt, KT, cb, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, rA, rB, K, ga,
+                                             gb, acc, a, b0, b1);
+    cb = cb == 2 ? 0 : cb + 1;
+    a8w8_b3_step<BM, BN, WM, WN, LW, NCH, 1>(kt + 1, KT, cb, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, rA, rB, K,
+                                             ga, gb, acc, a, b1, b0);
+    cb = cb == 2 ? 0 : cb + 1;
+  }
+  if (kt < KT)
+    a8w8_b3_step<BM, BN, WM, WN, LW, NCH, 0>(kt, KT, cb, sAr, sBr, loader, wave, wm, wn, r16, p0, p1, rA, rB, K, ga,
+                                             gb, acc, a, b0, b1);
+  // every load is complete: the last barrier (step KT - 2's, or the
+  // prologue's with KT == 1) waited for vmcnt(0)
+  store_tile<T, BM, BN, WM, WN, 64 * NW, true>(acc, smem, wm, wn, lane, m0, n0, M, N, sc, sc + BM, 1.f, Y, mlo, nlo);
 }
 
 // Y[m, n] = Out(sa[m] * sb[n] * (P[0][m, n] + P[1][m, n] + ...)), the parts
@@ -1595,10 +1769,11 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
   if (K % 128 == 0) {
     // Tile (and split-K) choice: plan_a8w8.  Every configuration runs
     // gemm_a8w8_pipe_kernel (register-pipelined fragment reads,
-    // single-offset addressing) when the matrices are below 4 GB and hold at
-    // least one tile in each dimension; otherwise configurations 0-3 run
-    // gemm_a8w8_lds_kernel with the same tile (its loads clamp rows), and
-    // the plan only picks 4-6 where the pipelined kernel applies.  Split K
+    // single-offset addressing; configuration 2, 256 x 192, its 3-slot B
+    // ring form gemm_a8w8_pipe_b3_kernel) when the matrices are below 4 GB
+    // and hold at least one tile in each dimension; otherwise configurations
+    // 0-3 run gemm_a8w8_lds_kernel with the same tile (its loads clamp rows),
+    // and the plan only picks 4-7 where the pipelined kernel applies.  Split K
     // needs a workspace of a8w8_workspace_bytes; without one the unsplit
     // plan runs.
     const bool off32 = a8w8_off32(M, N, K);
@@ -1617,6 +1792,12 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
     gemm_a8w8_pipe_kernel<TY, BM, BN, WM, WN, OCC, LW, 1, RING, WM * WN == 8 ? (BM / WM >= 48 ? 3 : 2) : 1> \
         <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, nullptr, M, N, K, tm, tn); \
+  } while (0)
+#define CEK_A8W8_PIPE_B3(TY, BM, BN, WM, WN, LW, NCH)                                                  \
+  do {                                                                                                \
+    const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);                           \
+    gemm_a8w8_pipe_b3_kernel<TY, BM, BN, WM, WN, LW, NCH>                                             \
+        <<<dim3((unsigned)(tm * tn)), 64 * WM * WN, 0, st>>>(a, sa, b, sb, yp, M, N, K, tm, tn);      \
   } while (0)
 #define CEK_A8W8_SPLIT(TY, BM, BN, WM, WN, OCC, LW, SP, RING)                                          \
   do {                                                                                                \
@@ -1651,7 +1832,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
       if (pipe) CEK_A8W8_PIPE(TY, 256, 256, 2, 4, 1, 4, 2);                            \
       else CEK_A8W8(TY, 256, 256, 4, 2, 1);                                            \
     } else if (cfg == 2) {                                                             \
-      if (pipe) CEK_A8W8_PIPE(TY, 256, 192, 2, 4, 1, 4, 2);                            \
+      if (pipe) CEK_A8W8_PIPE_B3(TY, 256, 192, 2, 4, 4, 3);                           \
       else CEK_A8W8(TY, 256, 192, 2, 4, 1);                                            \
     } else if (cfg == 1) {                                                             \
       if (pipe) CEK_A8W8_PIPE(TY, 128, 128, 2, 2, 2, 4, 2);                            \
@@ -1665,6 +1846,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     else CEK_A8W8_ALL(BF16);
 #undef CEK_A8W8
 #undef CEK_A8W8_PIPE
+#undef CEK_A8W8_PIPE_B3
 #undef CEK_A8W8_SPLIT
 #undef CEK_A8W8_SPLITS
 #undef CEK_A8W8_ALL

@@ -177,7 +177,7 @@ def test_a8w8_decode_rows(ops, dev, M, K, N):
 
 @pytest.mark.parametrize("M,K,N", [(4096, 1024, 8192), (4000, 512, 8150), (2000, 1024, 6100), (2048, 512, 6144),
                                    (2048, 640, 6144), (2048, 128, 6144), (2048, 256, 6144), (2040, 384, 6100),
-                                   (520, 1024, 28800),
+                                   (2000, 768, 6100), (2048, 896, 6144), (520, 1024, 28800),
                                    (4100, 512, 6150), (100, 256, 3000), (200, 512, 100), (70, 384, 130)])
 def test_a8w8_large_tiles(ops, dev, M, K, N):
     """The tile configurations (256 x 256, 256 x 192, 128 x 128, 64 x 128),
@@ -187,7 +187,10 @@ def test_a8w8_large_tiles(ops, dev, M, K, N):
     clamping LDS kernel.  K = 640 and 128 give an odd number of K steps and a
     single one; K = 128, 256 and 384 (one to three steps) also cover the
     8-wave tiles' load chunks at the ends of the K loop (the prologue loads
-    steps 0 and 1 whole, later steps go out in chunks)."""
+    steps 0 and 1 whole, later steps go out in chunks).  256 x 192 (M near
+    2048, N near 6144) runs the 3-slot B ring: K = 128 .. 896 (1 to 7 steps)
+    cover its prologue (A 0-1, B 0-2), the slot cycle of period 3 against the
+    A ring's 2, and its tail waits."""
     _say(f"a8w8 large tiles M={M} K={K} N={N}")
     q, sa, W8, sb = _a8w8_inputs(M, K, N, seed=M + N)
     qd, Wd = q.to(dev), W8.to(dev)

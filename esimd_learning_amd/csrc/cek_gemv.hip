@@ -1143,6 +1143,143 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 }
 
 // ---------------------------------------------------------------------------
+// 9 <= M <= 16 with wide N: the activations resident in LDS.
+//
+// gemv_lds_kernel reads, for every 16-row tile, the 16 activation rows of
+// each K stage from L2 straight into MFMA operand layout: lane l takes row
+// l & 15, so every such load touches 16 cache lines, and at M = 16 the
+// texture-address unit stalls on them (its waves wait on outstanding loads
+// most of their cycles).  Here a workgroup loads the whole activation matrix
+// (16 rows x K values, rows >= M repeating row M - 1: 64-128 KB) into LDS
+// once, by direct-to-LDS loads, and streams its weight rows from global
+// memory straight into operand registers (no weight staging, no barrier per
+// stage).  A workgroup runs TPB tiles of 16 weight rows at a time, each tile
+// split over two waves: the wave of half h takes K values [h K / 2,
+// (h + 1) K / 2) of the tile's rows, as 64-byte chunks (lane group g = lane
+// >> 4 takes bytes 16 g .. 16 g + 15 of a chunk, two 8-value MFMA operands),
+// PD chunks in flight; the second half's sum is then added to the first's
+// through LDS, scaled and rounded as in gemv_lds_kernel.  The sum order
+// differs from gemv_lds_kernel's, so the outputs may differ from it in the
+// last bit: the dispatcher picks the kernel per weight matrix (by its own
+// row count), so a multi-matrix launch still gives each matrix what it gets
+// alone.  Slots of TPB tiles run grid-stride over the tiles of all segments.
+//
+// LDS: activation chunk lc (16 bytes) of row r sits at (lc & ~15) | ((lc ^ r)
+// & 15): the 16 rows that one 16-lane group of a ds_read_b128 reads at the
+// same K land in 16 different 16-byte bank groups.  The direct-to-LDS loads
+// fill LDS in order, so lane i of load j fetches the logical chunk that
+// belongs at physical chunk 64 j + i (the map is its own inverse).
+//
+// Measured on MI355X against gemv_lds_kernel (weights from HBM, M = 16 unless
+// given): K = 4096, N = 14336 17.37 -> 15.25 us, N = 28672 29.99 -> 26.49,
+// M = 12, N = 14336 16.44 -> 15.01, M = 9, N = 28672 27.15 -> 26.31;
+// K = 3072, N = 12288 12.65 -> 12.29.  Not faster at 512 tiles or fewer
+// (N = 6144 9.99 against 10.34, N = 8192 equal) nor above 2048 (N = 49152:
+// 44.2 against 44.7).  Splitting each tile's K by residues mod 4 over the
+// waves instead (which sums in gemv_lds_kernel's order, bit for bit) was
+// 0-8% slower than this form where it gained, and 8% slower than
+// gemv_lds_kernel at M = 9, N = 28672.
+template <typename T, typename TO, int FMT, int K, int TPB, int PD>
+__global__ __launch_bounds__(128 * TPB) void gemv_xres_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
+                                                             int M, int tiles) {
+  constexpr int NCW = K / 128;  // 64-byte chunks per wave and tile (half of the K values)
+  constexpr int XBYTES = 16 * K * 2, CPR = K / 8;
+  static_assert(NCW % PD == 0, "whole prefetch groups");
+  static_assert(XBYTES % 1024 == 0, "1 KB direct-to-LDS loads");
+  __shared__ __attribute__((aligned(1024))) uint8_t sx[XBYTES];
+  __shared__ f4 red[TPB * 64];  // the second halves' sums
+  static_assert(sizeof(sx) + sizeof(red) <= 160 * 1024, "LDS");
+  // wave-uniform indices (so that the segment table is read by scalar loads,
+  // which do not count against the weight loads' vmcnt)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int tw = wave >> 1, kh = wave & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int nslot = (tiles + TPB - 1) / TPB;
+  // this wave's tile of slot s (clamped: a wave past the last tile repeats
+  // it and stores nothing) and the first weight byte it reads: its row
+  // (clamped into its matrix; rows past it are never stored), K half, lane group
+  auto wsrc = [&](int s) {
+    const SegRef r = find_seg(sg, min(s * TPB + tw, tiles - 1));
+    return r.w + (size_t)min(16 * r.group + r16, r.n - 1) * K + (K / 2) * kh + 16 * g;
+  };
+  // half 0: the weight scale of this lane's output column of slot s's tile
+  auto scale_bits = [&](int s) {
+    const SegRef r = find_seg(sg, min(s * TPB + tw, tiles - 1));
+    return kh == 0 ? load_scale_bits(r.s, skind, min(16 * r.group + r16, r.n - 1)) : 0u;
+  };
+  int s = blockIdx.x;
+  uint32_t scb = s < nslot ? scale_bits(s) : 0u;
+  {
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, M * K * 2, 0x00020000);
+    for (int j = wave; j < XBYTES / 1024; j += 2 * TPB) {
+      const int pc = 64 * j + lane, r = pc / CPR, p = pc % CPR;
+      const int lc = (p & ~15) | ((p ^ r) & 15);
+#if defined(__HIP_DEVICE_COMPILE__)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(sx + 1024 * j), 16,
+                                               (uint32_t)((min(r, M - 1) * K + 8 * lc) * 2), 0, 0, 0);
+#endif
+    }
+  }
+  u4 wb[PD];
+  const uint8_t* wr = wsrc(s);
+  if (s < nslot) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) wb[i] = load_u4(wr + 64 * i);
+    wait_vmcnt<PD>();  // this wave's activation loads (older) are in LDS
+  } else {
+    wait_vmcnt<0>();
+  }
+  bare_barrier();
+  const uint8_t* xr = sx + r16 * (K * 2);
+  const int c0 = NCW * kh;  // this wave's first chunk
+  for (; s < nslot; s += gridDim.x) {
+    const int sn = s + gridDim.x;
+    const uint8_t* wn = wsrc(sn);
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int j0 = 0; j0 < NCW; j0 += PD) {
+      // the next PD chunks of this tile, or the first of the next slot's
+      // (after the last slot: the PD chunks just read again, still in the
+      // caches and never used -- the loads stay unconditional, so every wait
+      // count is static)
+      const uint8_t* src = j0 + PD < NCW ? wr + 64 * (j0 + PD) : (sn < nslot ? wn : wr + 64 * (NCW - PD));
+#pragma unroll
+      for (int i = 0; i < PD; ++i) {
+        const u4 w = wb[i];
+        wb[i] = load_u4(src + 64 * i);
+        u4 lo, hi;
+        decode16<T, FMT>(w, lo, hi);
+        const int lc = 8 * (c0 + j0 + i) + 2 * g;  // chunk c: 16-byte activation pieces 8 c + 2 g, + 1
+        const u4 x0 = *reinterpret_cast<const u4*>(xr + 16 * ((lc & ~15) | ((lc ^ r16) & 15)));
+        const u4 x1 = *reinterpret_cast<const u4*>(xr + 16 * (((lc + 1) & ~15) | (((lc + 1) ^ r16) & 15)));
+        acc = mfma16x16x32<T>(x0, lo, acc);
+        acc = mfma16x16x32<T>(x1, hi, acc);
+      }
+    }
+    if (kh == 1) red[tw * 64 + lane] = acc;
+    lds_barrier();
+    const int tile = s * TPB + tw;
+    if (kh == 0 && tile < tiles) {
+      const SegRef r = find_seg(sg, tile);
+      const f4 c = acc + red[tw * 64 + lane];
+      const int n = 16 * r.group + r16;
+      const float sc = scale_value(scb, skind);
+      if (n < r.n) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = 4 * g + v;
+          if (m < M) r.y[(size_t)m * r.n + n] = TO::from_f32(f32_round(c[v] * sc));
+        }
+      }
+    }
+    if (sn < nslot) scb = scale_bits(sn);
+    lds_barrier();  // half 0 has read red before the next slot writes it
+    wr = wn;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic: any M, K, alignment.  One wave per output row of a segment.
 // ---------------------------------------------------------------------------
 template <typename T, int FMT>
@@ -1277,6 +1414,37 @@ static bool launch_lds(const void* x, GemvSegs& sg, int skind, int M, int K, int
     case 24: return launch_lds_steps<T, TO, FMT, XF8, 24>(x, sg, skind, M, N, st);
     default: return false;
   }
+}
+
+// gemv_xres_kernel takes a weight matrix of 512 < tiles <= 2048 16-row tiles
+// (8208 <= N <= 32768) when 9 <= M <= 16, the activations are fp16 / bf16 and
+// K is 2, 3 or 4 KiB values (the range where it measured faster).
+static bool xres_matrix(int M, int K, int n) {
+  const int tiles = (n + 15) / 16;
+  return M >= 9 && M <= 16 && (K == 2048 || K == 3072 || K == 4096) && tiles > 512 && tiles <= 2048;
+}
+
+// gemv_xres_kernel over every segment of sg (all of them xres_matrix): TPB =
+// 4 tiles per slot up to 1024 tiles, else 8, one slot per workgroup (one
+// workgroup per CU) as far as 256 workgroups go.
+template <typename T, typename TO, int FMT>
+static void launch_xres(const void* x, GemvSegs& sg, int skind, int M, int K, hipStream_t st) {
+  const int tiles = seg_grid(sg, 16);  // gstart: first tile of each segment
+  const int tpb = tiles <= 1024 ? 4 : 8;
+  const int nslot = (tiles + tpb - 1) / tpb;
+  const dim3 grid((unsigned)(nslot < 256 ? nslot : 256));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+#define CEK_XRES(KK, TT) gemv_xres_kernel<T, TO, FMT, KK, TT, 8><<<grid, 128 * (TT), 0, st>>>(xp, sg, skind, M, tiles)
+#define CEK_XRES_K(KK)            \
+  do {                            \
+    if (tpb == 4) CEK_XRES(KK, 4); \
+    else CEK_XRES(KK, 8);         \
+  } while (0)
+  if (K == 2048) CEK_XRES_K(2048);
+  else if (K == 3072) CEK_XRES_K(3072);
+  else CEK_XRES_K(4096);
+#undef CEK_XRES_K
+#undef CEK_XRES
 }
 
 // Gate/up GEMV with gelu_and_mul fused (gemv_lds_kernel's GLU form): one
@@ -1433,6 +1601,31 @@ static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bo
   // each matrix alone would (the LDS forms it may pick between agree bit for
   // bit).
   const int m_lds = K >= 14336 ? 1 : 3;
+  if constexpr (!XF8) {
+    // matrices that gemv_xres_kernel serves go to one launch of it, the rest
+    // on through the kernels below (its sum order differs from theirs, so the
+    // choice is per matrix: a multi-matrix launch gives each matrix what it
+    // gets alone)
+    if (vec16) {
+      GemvSegs sx{}, so{};
+      sx.xs = so.xs = sg.xs;
+      for (int i = 0; i < sg.count; ++i) {
+        GemvSegs& d = xres_matrix(M, K, sg.n[i]) ? sx : so;
+        d.w[d.count] = sg.w[i];
+        d.s[d.count] = sg.s[i];
+        d.y[d.count] = sg.y[i];
+        d.n[d.count] = sg.n[i];
+        ++d.count;
+      }
+      if (sx.count > 0) {
+        launch_xres<T, TO, FMT>(x, sx, skind, M, K, st);
+        if (so.count == 0) return check_launch();
+        sg = so;
+        N = 0;
+        for (int i = 0; i < sg.count; ++i) N += sg.n[i];
+      }
+    }
+  }
   if (vec16 && M >= m_lds && launch_lds<T, TO, FMT, XF8>(x, sg, skind, M, K, N, st)) return check_launch();
   if (M > 16) return CEK_ERR_UNSUPPORTED;
   if (vec16 && M <= 4) {

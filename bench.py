@@ -928,7 +928,7 @@ def main():
         log("small ops: " + ", ".join(f"{r['op']}/T{r['T']}={r['us']}us" for r in out["small_ops"]))
     if not a.no_gemm:
         out["gemm"] = bench_gemm_all(ops, torch, max(10, a.steps // 20), max(3, a.warmup // 10))
-        out["gemm"]["roofline"]["traffic"] = load_traffic("gemm_a8w8_pipe_kernel_m2048_k4096_n6144")
+        out["gemm"]["roofline"]["traffic"] = load_traffic("gemm_a8w8_pipe_b3_kernel_m2048_k4096_n6144")
         log(f"gemm: {out['gemm']['avg_launch_us']:.1f} us, {out['gemm']['tflops']:.0f} TFLOP/s")
         out["gemm_k_scaling"] = bench_gemm_k_scaling(ops, torch)
         gk = out["gemm_k_scaling"]

@@ -48,6 +48,32 @@ def test_c_host_program(tmp_path):
     assert r.stdout.strip().endswith("ok")
 
 
+def test_c_host_program_sanitized(tmp_path):
+    """The same host program built with AddressSanitizer and
+    UndefinedBehaviorSanitizer (host code only; libcek.so itself is the
+    normal build, seen through the sanitizer's interceptors): no invalid
+    access, undefined behaviour or leak on the argument-check paths."""
+    import os
+    import shutil
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = Path(__file__).parent / "c" / "abi_host.c"
+    exe = tmp_path / "abi_host_asan"
+    libdir = Path(cabi.LIBCEK).parent
+    b = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-g", "-fno-omit-frame-pointer",
+                        "-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-I", str(cabi.HEADER.parent),
+                        str(src), "-o", str(exe), "-L", str(libdir), "-lcek", f"-Wl,-rpath,{libdir}"],
+                       capture_output=True, text=True)
+    if b.returncode != 0 and "asan" in (b.stderr + b.stdout).lower():
+        pytest.skip("no sanitizer runtime: " + b.stderr[-200:])
+    assert b.returncode == 0, b.stdout + b.stderr
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:halt_on_error=1", UBSAN_OPTIONS="halt_on_error=1")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().endswith("ok")
+
+
 def test_library_loads_and_reports():
     lib = cabi.load()
     assert lib.cek_version() == 100

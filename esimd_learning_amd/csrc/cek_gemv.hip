@@ -1280,6 +1280,136 @@ __global__ __launch_bounds__(128 * TPB) void gemv_xres_kernel(const uint16_t* __
 }
 
 // ---------------------------------------------------------------------------
+// The same for e4m3 activations (the a8w8 GEMV, per-row activation scales
+// sg.xs, fp32 per-channel weight scales), 17 <= M <= 32: the activation codes
+// of MB = 2 blocks of 16 rows (rows >= M repeating row M - 1; 32 K bytes: up
+// to 128 KB) resident in LDS, the weights straight into the operands of
+// v_mfma_f32_16x16x128_f8f6f4.  A lane's operand for the 128-byte K chunk c
+// is bytes 128 c + 16 g .. + 15 and 128 c + 64 + 16 g .. + 15 of its row (two
+// 16-byte loads, each of 16 rows x 64 contiguous bytes), the activation
+// operand the same bytes of its activation row.  Each tile's K is split in
+// KS contiguous parts over KS waves, added in order through LDS; outputs
+// Out(sum * (sb[n] * sa[m])) as in gemv_lds_kernel.  Measured on MI355X
+// against gemv_lds_kernel (weights from HBM, K = 4096, M = 32 unless given):
+// N = 6144 (config 3 at T = 32) 12.53 -> 10.32 us, N = 14336 23.71 -> 16.1,
+// N = 28672 33.97 -> 27.28, M = 24, N = 6144 11.09 -> 10.21, M = 17,
+// N = 14336 18.3 -> 15.83; at 256 tiles (N = 4096) no faster (8.68 against
+// 8.69-9.74).  Of 1 x 4, 2 x 2, 2 x 4 and 4 x 2 (tiles per slot x K parts),
+// 2 x 4 was the fastest or within 1% of it wherever the kernel gained.
+template <typename TO, int K, int TPB, int KS, int PD>
+__global__ __launch_bounds__(64 * TPB * KS) void gemv_xres8_kernel(const uint8_t* __restrict__ x, GemvSegs sg, int M,
+                                                                  int tiles) {
+  constexpr int MB = 2;
+  constexpr int NCW = K / 128 / KS;  // 128-byte K chunks per wave and tile
+  constexpr int XBYTES = 16 * MB * K, CPR = K / 16;
+  static_assert(NCW % PD == 0, "whole prefetch groups");
+  static_assert(XBYTES % 1024 == 0, "1 KB direct-to-LDS loads");
+  __shared__ __attribute__((aligned(1024))) uint8_t sx[XBYTES];
+  __shared__ f4 red[TPB * (KS - 1) * MB * 64];
+  static_assert(sizeof(sx) + sizeof(red) <= 160 * 1024, "LDS");
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int tw = wave / KS, kh = wave % KS;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int nslot = (tiles + TPB - 1) / TPB;
+  auto wsrc = [&](int s) {
+    const SegRef r = find_seg(sg, min(s * TPB + tw, tiles - 1));
+    return r.w + (size_t)min(16 * r.group + r16, r.n - 1) * K + (K / KS) * kh + 16 * g;
+  };
+  auto scale_bits = [&](int s) {
+    const SegRef r = find_seg(sg, min(s * TPB + tw, tiles - 1));
+    return kh == 0 ? load_scale_bits(r.s, SK_F32, min(16 * r.group + r16, r.n - 1)) : 0u;
+  };
+  float scm[MB][4];  // the activation rows' scales (D row 16 b + 4 g + v)
+#pragma unroll
+  for (int b = 0; b < MB; ++b)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) scm[b][v] = sg.xs[min(16 * b + 4 * g + v, M - 1)];
+  int s = blockIdx.x;
+  uint32_t scb = s < nslot ? scale_bits(s) : 0u;
+  {
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(x), 0, M * K, 0x00020000);
+    for (int j = wave; j < XBYTES / 1024; j += TPB * KS) {
+      const int pc = 64 * j + lane, r = pc / CPR, p = pc % CPR;
+      const int lc = (p & ~15) | ((p ^ r) & 15);
+#if defined(__HIP_DEVICE_COMPILE__)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(sx + 1024 * j), 16,
+                                               (uint32_t)(min(r, M - 1) * K + 16 * lc), 0, 0, 0);
+#endif
+    }
+  }
+  u4 wb[PD][2];
+  const uint8_t* wr = wsrc(s);
+  if (s < nslot) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      wb[i][0] = load_u4(wr + 128 * i);
+      wb[i][1] = load_u4(wr + 128 * i + 64);
+    }
+    wait_vmcnt<2 * PD>();  // this wave's activation loads (older) are in LDS
+  } else {
+    wait_vmcnt<0>();
+  }
+  bare_barrier();
+  const int c0 = NCW * kh;  // this wave's first chunk
+  for (; s < nslot; s += gridDim.x) {
+    const int sn = s + gridDim.x;
+    const uint8_t* wn = wsrc(sn);
+    f4 acc[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int j0 = 0; j0 < NCW; j0 += PD) {
+      // the next PD chunks, the next slot's first, or (after the last slot)
+      // the ones just read again: unconditional loads, static wait counts
+      const uint8_t* src = j0 + PD < NCW ? wr + 128 * (j0 + PD) : (sn < nslot ? wn : wr + 128 * (NCW - PD));
+#pragma unroll
+      for (int i = 0; i < PD; ++i) {
+        const i8 wop = cat_i8(wb[i][0], wb[i][1]);
+        wb[i][0] = load_u4(src + 128 * i);
+        wb[i][1] = load_u4(src + 128 * i + 64);
+        const int lc0 = 8 * (c0 + j0 + i) + g, lc1 = lc0 + 4;  // 16-byte pieces of chunk c
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          const int rr = 16 * b + r16;
+          const uint8_t* xr = sx + rr * K;
+          const u4 x0 = *reinterpret_cast<const u4*>(xr + 16 * ((lc0 & ~15) | ((lc0 ^ rr) & 15)));
+          const u4 x1 = *reinterpret_cast<const u4*>(xr + 16 * ((lc1 & ~15) | ((lc1 ^ rr) & 15)));
+          acc[b] = mfma_fp8_16x16x128(cat_i8(x0, x1), wop, acc[b]);
+        }
+      }
+    }
+    if (kh > 0) {
+#pragma unroll
+      for (int b = 0; b < MB; ++b) red[((tw * (KS - 1) + kh - 1) * MB + b) * 64 + lane] = acc[b];
+    }
+    lds_barrier();
+    const int tile = s * TPB + tw;
+    if (kh == 0 && tile < tiles) {
+      const SegRef r = find_seg(sg, tile);
+      const int n = 16 * r.group + r16;
+      const float sc = scale_value(scb, SK_F32);
+      if (n < r.n) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          f4 c = acc[b];
+#pragma unroll
+          for (int q = 1; q < KS; ++q) c += red[((tw * (KS - 1) + q - 1) * MB + b) * 64 + lane];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int m = 16 * b + 4 * g + v;
+            if (m < M) r.y[(size_t)m * r.n + n] = TO::from_f32(f32_round(c[v] * (sc * scm[b][v])));
+          }
+        }
+      }
+    }
+    if (sn < nslot) scb = scale_bits(sn);
+    lds_barrier();  // part 0 has read red before the next slot writes it
+    wr = wn;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic: any M, K, alignment.  One wave per output row of a segment.
 // ---------------------------------------------------------------------------
 template <typename T, int FMT>
@@ -1708,6 +1838,25 @@ int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const 
   sg.y[0] = static_cast<uint16_t*>(y);
   sg.n[0] = (int)N;
   sg.xs = xs;
+  // 17 <= M <= 32 with K of 2, 3 or 4 KiB values and at least 384 16-row
+  // tiles: gemv_xres8_kernel, 2 tiles x 4 K parts per workgroup, one slot per
+  // workgroup as far as 256 workgroups go
+  if (M >= 17 && M <= 32 && (K == 2048 || K == 3072 || K == 4096) && (N + 15) / 16 >= 384) {
+    const int tiles = seg_grid(sg, 16);
+    const int nslot = (tiles + 1) / 2;
+    const dim3 grid((unsigned)(nslot < 256 ? nslot : 256));
+    const int m = (int)M;
+#define CEK_X8(KK, PP)                                                                                         \
+  do {                                                                                                         \
+    if (out_dtype == CEK_F16) gemv_xres8_kernel<F16, KK, 2, 4, PP><<<grid, 512, 0, st>>>(x, sg, m, tiles);     \
+    else gemv_xres8_kernel<BF16, KK, 2, 4, PP><<<grid, 512, 0, st>>>(x, sg, m, tiles);                         \
+  } while (0)
+    if (K == 2048) CEK_X8(2048, 4);
+    else if (K == 3072) CEK_X8(3072, 6);
+    else CEK_X8(4096, 4);
+#undef CEK_X8
+    return check_launch();
+  }
   if (M > 16) {  // only the LDS path takes these
     const bool ok = out_dtype == CEK_F16 ? launch_lds<F16, F16, CEK_E4M3, true>(x, sg, SK_F32, (int)M, (int)K, (int)N, st)
                                          : launch_lds<F16, BF16, CEK_E4M3, true>(x, sg, SK_F32, (int)M, (int)K, (int)N, st);

@@ -98,3 +98,29 @@ def test_xres_multi_matrix_equals_single(ops, dev, M, Ns, K):
         torch.cuda.synchronize()
         assert torch.equal(ys[i], y1), f"matrix {i} (N={n})"
         assert_close_fp(ys[i].cpu(), ogemv.gemv_fp8_pern(x, Ws[i], Ss[i]), f"matrix {i}")
+
+
+# The e4m3-activation form (gemv_xres8_kernel): the a8w8 GEMM op sends M <= 64
+# (without a split-K workspace) to the GEMV kernels; 17 <= M <= 32 with at
+# least 384 row tiles and K of 2, 3 or 4 KiB values takes this one.  N = 28672
+# gives 896 slots of 2 tiles: 3-4 slots per workgroup.
+@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("K,N", [(4096, 6144), (3072, 12288), (2048, 8200), (4096, 28672)])
+def test_xres8_a8w8_vs_oracle(ops, dev, M, K, N):
+    from oracle import gemm as ogemm
+    from oracle import norm as onorm
+    _say(f"a8w8 gemv xres8 M={M} K={K} N={N}")
+    x = synthetic.activations(M, K, seed=M + K)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=N + 5)
+    W8 = W8.view(torch.uint8)
+    qd, sad, Wd, sbd = q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev)
+    ref = ogemm.gemm_a8w8(q, sa, W8, sb)
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.full((M, N), float("nan"), dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y)
+        y2 = torch.full((M, N), float("nan"), dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(qd, sad, Wd, sbd, y2)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2), "not deterministic"
+        assert_close_fp(y.cpu(), ref, f"a8w8 xres8 M={M} K={K} N={N} {out_dt}")

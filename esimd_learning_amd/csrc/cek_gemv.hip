@@ -1296,17 +1296,22 @@ __global__ __launch_bounds__(128 * TPB) void gemv_xres_kernel(const uint16_t* __
 // N = 14336 18.3 -> 15.83; at 256 tiles (N = 4096) no faster (8.68 against
 // 8.69-9.74).  Of 1 x 4, 2 x 2, 2 x 4 and 4 x 2 (tiles per slot x K parts),
 // 2 x 4 was the fastest or within 1% of it wherever the kernel gained.
-template <typename TO, int K, int TPB, int KS, int PD>
+// ONE (the launch runs one slot per workgroup): the later K parts' sums go
+// through the activation area, once every wave is done reading it, so that
+// 32 rows of K = 5120 (160 KB, all of LDS) fit.
+template <typename TO, int K, int TPB, int KS, int PD, bool ONE = false>
 __global__ __launch_bounds__(64 * TPB * KS) void gemv_xres8_kernel(const uint8_t* __restrict__ x, GemvSegs sg, int M,
                                                                   int tiles) {
   constexpr int MB = 2;
   constexpr int NCW = K / 128 / KS;  // 128-byte K chunks per wave and tile
   constexpr int XBYTES = 16 * MB * K, CPR = K / 16;
+  constexpr int REDB = TPB * (KS - 1) * MB * 64 * 16;  // bytes of the later parts' sums
   static_assert(NCW % PD == 0, "whole prefetch groups");
   static_assert(XBYTES % 1024 == 0, "1 KB direct-to-LDS loads");
-  __shared__ __attribute__((aligned(1024))) uint8_t sx[XBYTES];
-  __shared__ f4 red[TPB * (KS - 1) * MB * 64];
-  static_assert(sizeof(sx) + sizeof(red) <= 160 * 1024, "LDS");
+  static_assert(!ONE || REDB <= XBYTES, "the sums fit the activation area");
+  __shared__ __attribute__((aligned(1024))) uint8_t sx[XBYTES + (ONE ? 0 : REDB)];
+  static_assert(sizeof(sx) <= 160 * 1024, "LDS");
+  f4* red = reinterpret_cast<f4*>(ONE ? sx : sx + XBYTES);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int tw = wave / KS, kh = wave % KS;
   const int r16 = lane & 15, g = lane >> 4;
@@ -1379,6 +1384,7 @@ __global__ __launch_bounds__(64 * TPB * KS) void gemv_xres8_kernel(const uint8_t
         }
       }
     }
+    if constexpr (ONE) lds_barrier();  // every wave is done reading the activations
     if (kh > 0) {
 #pragma unroll
       for (int b = 0; b < MB; ++b) red[((tw * (KS - 1) + kh - 1) * MB + b) * 64 + lane] = acc[b];
@@ -1840,8 +1846,23 @@ int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const 
   sg.xs = xs;
   // 17 <= M <= 32 with K of 2, 3 or 4 KiB values and at least 384 16-row
   // tiles: gemv_xres8_kernel, 2 tiles x 4 K parts per workgroup, one slot per
-  // workgroup as far as 256 workgroups go
-  if (M >= 17 && M <= 32 && (K == 2048 || K == 3072 || K == 4096) && (N + 15) / 16 >= 384) {
+  // workgroup as far as 256 workgroups go; K = 5120 (160 KB of activations)
+  // only where one round of slots covers the tiles (384 to 512 tiles).  Where
+  // a workgroup has one slot (up to 512 tiles) only from 24 rows on: its
+  // activation load is not amortised, and below that the other kernel's
+  // repeated rows cost little (K = 5120, N = 8000: M = 17 12.04 -> 13.23 us,
+  // M = 24, N = 6144 13.37 -> 12.28, M = 32 15.12 -> 12.38).
+  const int tiles16 = (int)((N + 15) / 16);
+  const int m_min = tiles16 <= 512 ? 24 : 17;
+  if (M >= m_min && M <= 32 && K == 5120 && tiles16 >= 384 && tiles16 <= 512) {
+    const int tiles = seg_grid(sg, 16);
+    const int nslot = (tiles + 1) / 2;
+    const int m = (int)M;
+    if (out_dtype == CEK_F16) gemv_xres8_kernel<F16, 5120, 2, 4, 5, true><<<nslot, 512, 0, st>>>(x, sg, m, tiles);
+    else gemv_xres8_kernel<BF16, 5120, 2, 4, 5, true><<<nslot, 512, 0, st>>>(x, sg, m, tiles);
+    return check_launch();
+  }
+  if (M >= m_min && M <= 32 && (K == 2048 || K == 3072 || K == 4096) && tiles16 >= 384) {
     const int tiles = seg_grid(sg, 16);
     const int nslot = (tiles + 1) / 2;
     const dim3 grid((unsigned)(nslot < 256 ? nslot : 256));

@@ -1174,8 +1174,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 // given): K = 4096, N = 14336 17.37 -> 15.25 us, N = 28672 29.99 -> 26.49,
 // M = 12, N = 14336 16.44 -> 15.01, M = 9, N = 28672 27.15 -> 26.31;
 // K = 3072, N = 12288 12.65 -> 12.29.  Not faster at 512 tiles or fewer
-// (N = 6144 9.99 against 10.34, N = 8192 equal) nor above 2048 (N = 49152:
-// 44.2 against 44.7).  Splitting each tile's K by residues mod 4 over the
+// (N = 6144: 10.34 us against 9.99 for gemv_lds_kernel; N = 8192 equal) nor
+// above 2048 (N = 49152: 44.7 against 44.2).  Splitting each tile's K by residues mod 4 over the
 // waves instead (which sums in gemv_lds_kernel's order, bit for bit) was
 // 0-8% slower than this form where it gained, and 8% slower than
 // gemv_lds_kernel at M = 9, N = 28672.
@@ -1291,10 +1291,10 @@ __global__ __launch_bounds__(128 * TPB) void gemv_xres_kernel(const uint16_t* __
 // KS contiguous parts over KS waves, added in order through LDS; outputs
 // Out(sum * (sb[n] * sa[m])) as in gemv_lds_kernel.  Measured on MI355X
 // against gemv_lds_kernel (weights from HBM, K = 4096, M = 32 unless given):
-// N = 6144 (config 3 at T = 32) 12.53 -> 10.32 us, N = 14336 23.71 -> 16.1,
-// N = 28672 33.97 -> 27.28, M = 24, N = 6144 11.09 -> 10.21, M = 17,
-// N = 14336 18.3 -> 15.83; at 256 tiles (N = 4096) no faster (8.68 against
-// 8.69-9.74).  Of 1 x 4, 2 x 2, 2 x 4 and 4 x 2 (tiles per slot x K parts),
+// N = 6144 (32 tokens into a 4096-wide QKV) 12.53 -> 10.32 us, N = 14336
+// 23.71 -> 16.1, N = 28672 33.97 -> 27.28, M = 24, N = 6144 11.09 -> 10.21,
+// M = 17, N = 14336 18.3 -> 15.83; at 256 tiles (N = 4096) no faster
+// (8.69-9.74 us against 8.68 for gemv_lds_kernel).  Of 1 x 4, 2 x 2, 2 x 4 and 4 x 2 (tiles per slot x K parts),
 // 2 x 4 was the fastest or within 1% of it wherever the kernel gained.
 // ONE (the launch runs one slot per workgroup): the later K parts' sums go
 // through the activation area, once every wave is done reading it, so that

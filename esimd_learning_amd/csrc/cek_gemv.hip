@@ -133,27 +133,37 @@ __device__ inline SegRef find_seg(const GemvSegs& sg, int b) {
 // waves.  Small workgroups dispatched in order keep the rows being read in a
 // sliding window of HBM, which streams better than long-lived persistent
 // waves each walking its own region.
+// RP > 1 (rows shorter than 4 KB: K = 4096 / RP, RP in {2, 4}): a load
+// instruction covers RP consecutive rows of 256 / RP units each, thread t
+// taking unit t % (256 / RP) of row t / (256 / RP) of each pass, so no thread
+// idles; the workgroup owns R passes (R x RP rows).  A row's units, wave sums
+// and the order they are added in are those of RP = 1 without the idle
+// threads' zeros, so the outputs do not depend on RP or R.
 // ---------------------------------------------------------------------------
 // With XF8 the activations are e4m3 codes (x points at bytes) decoded exactly
 // into T pairs, and the epilogue multiplies by the row's activation scale.
-template <typename T, typename TO, int FMT, bool XF8, int MT, int R, int U>
+template <typename T, typename TO, int FMT, bool XF8, int MT, int R, int U, int RP = 1>
 __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restrict__ x, GemvSegs sg, int skind,
                                                        int M, int K) {
+  static_assert(RP == 1 || RP == 2 || RP == 4, "a row covers whole waves");
   typedef typename T::pair P;
   __shared__ float red[4][MT * R];
   const SegRef sr = find_seg(sg, blockIdx.x);
   const int N = sr.n;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int row0 = sr.group * R;
-  const int K16 = K >> 4;
+  const int row0 = sr.group * R * RP;
+  const int K16 = K >> 4;  // 256 / RP when RP > 1
+  constexpr int TPR = 256 / RP;  // threads per row of a pass
+  const int sub = t / TPR;       // this thread's row within each pass
+  const int tu = t % TPR;        // and its first 16-byte unit
   // Output scales are loaded up front: their latency then overlaps the
   // weight loads' instead of following the reduction with the workgroup's
   // slot held and no weight bytes in flight.
   uint32_t sc_bits = 0;
   float sc_m = 1.f;
-  if (t < MT * R) {
-    const int m = t / R, n = row0 + t % R;
+  if (t < MT * R * RP) {
+    const int m = t / (R * RP), n = row0 + t % (R * RP);
     if (m < M && n < N) {
       sc_bits = load_scale_bits(sr.s, skind, n);
       if (XF8) sc_m = sg.xs[m];
@@ -163,7 +173,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
   const uint8_t* wrow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = row0 + r < N ? row0 + r : N - 1;  // clamped rows are never stored
+    const int row = row0 + r * RP + sub < N ? row0 + r * RP + sub : N - 1;  // clamped rows are never stored
     wrow[r] = sr.w + (size_t)row * K;
   }
   float acc[MT][R];
@@ -172,7 +182,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
 
-  for (int base = t; base < K16; base += 256 * U) {
+  for (int base = tu; base < K16; base += 256 * U) {
     u4 wv[U][R];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -237,10 +247,16 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const uint16_t* __restric
       if (lane == 0) red[wave][m * R + r] = s;
     }
   __syncthreads();
-  if (t < MT * R) {
-    const int m = t / R, r = t % R, n = row0 + r;
+  if (t < MT * R * RP) {
+    // output (m, row row0 + q): pass r = q / RP, row sub = q % RP of it, whose
+    // sums sit in waves 4 / RP * sub .. 4 / RP * (sub + 1) - 1
+    const int m = t / (R * RP), q = t % (R * RP), n = row0 + q;
     if (m < M && n < N) {
-      float s = red[0][t] + red[1][t] + red[2][t] + red[3][t];
+      const int i = m * R + q / RP;
+      float s;
+      if (RP == 1) s = red[0][i] + red[1][i] + red[2][i] + red[3][i];
+      else if (RP == 2) s = red[2 * (q % 2)][i] + red[2 * (q % 2) + 1][i];
+      else s = red[q % 4][i];
       if (XF8) s *= sc_m;
       sr.y[(size_t)m * N + n] = TO::from_f32(s * scale_value(sc_bits, skind));
     }
@@ -1771,10 +1787,28 @@ static int launch_gemv_t(const void* x, GemvSegs sg, int skind, int M, int K, bo
     // rows.  One 16-byte unit per thread and row per round.
     const int K16 = K / 16;
     const bool r2 = M == 1 && K16 <= 256;
-#define CEK_DOT(MT, R) gemv_dot_kernel<T, TO, FMT, XF8, MT, R, 1><<<dim3(seg_grid(sg, R)), 256, 0, st>>>(xp, sg, skind, M, K)
-    if (M == 1) { if (r2) CEK_DOT(1, 2); else CEK_DOT(1, 4); }
-    else if (M == 2) CEK_DOT(2, 4);
-    else CEK_DOT(4, 4);
+    // K = 2048 and 1024 (rows of 128 and 64 units): 2 and 4 rows per load
+    // instruction (RP), two passes per workgroup, instead of 256-thread
+    // workgroups half or three quarters idle (M = 1, K = 1024, N = 16384:
+    // 7.67 -> 4.71 us; K = 2048: 8.31 -> 7.04 us; M = 2, K = 2048: 8.73 ->
+    // 7.83 us; one pass or three or four measured slower; outputs unchanged).
+#define CEK_DOT(MT, R, RP) \
+  gemv_dot_kernel<T, TO, FMT, XF8, MT, R, 1, RP><<<dim3(seg_grid(sg, (R) * (RP))), 256, 0, st>>>(xp, sg, skind, M, K)
+    if (K16 == 128 || K16 == 64) {
+      if (K16 == 128) {
+        if (M == 1) CEK_DOT(1, 2, 2);
+        else if (M == 2) CEK_DOT(2, 2, 2);
+        else CEK_DOT(4, 2, 2);
+      } else {
+        if (M == 1) CEK_DOT(1, 2, 4);
+        else if (M == 2) CEK_DOT(2, 2, 4);
+        else CEK_DOT(4, 2, 4);
+      }
+    } else if (M == 1) {
+      if (r2) CEK_DOT(1, 2, 1);
+      else CEK_DOT(1, 4, 1);
+    } else if (M == 2) CEK_DOT(2, 4, 1);
+    else CEK_DOT(4, 4, 1);
 #undef CEK_DOT
   } else if (vec16 && K % 64 == 0 && M <= 16) {
     // 16-row tiles per wave (NT) and 64-byte K steps in flight per wave

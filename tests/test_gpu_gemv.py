@@ -137,6 +137,34 @@ def test_gemv_generic_path(ops, dev, M, K):
     assert_close_fp(y, ogemv.gemv_fp8_pern(x, W8, s), f"generic M={M} K={K}")
 
 
+# K = 2048 and 1024 with one or two rows: the v_dot2 kernel puts 2 and 4 rows
+# into each load instruction (two passes per workgroup, 4 and 8 rows).  N not
+# a multiple of the rows per workgroup ends a workgroup inside a pass or
+# before its second pass; N = 1 and 3 leave most of the only workgroup's rows
+# clamped.  Both fp8 formats, both activation types, and the e4m3-activation
+# form (the a8w8 op's GEMV route for one or two rows).
+@pytest.mark.parametrize("K,N", [(2048, 1001), (2048, 8192), (1024, 999), (1024, 16384), (1024, 3), (2048, 1)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_gemv_rows_per_pass(ops, dev, M, K, N):
+    _say(f"gemv rows-per-pass M={M} K={K} N={N}")
+    for io, fmt in [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)]:
+        W8, s = synthetic.weight_fp8(N, K, seed=K + N + M, fmt=fmt)
+        x = synthetic.activations(M, K, seed=M + 40, dtype=io)
+        y = _run_pern(ops, x, W8, s, dev)
+        assert y.dtype == io
+        assert_close_fp(y, ogemv.gemv_fp8_pern(x, W8, s), f"rows-per-pass M={M} K={K} N={N} io={io}")
+    from oracle import gemm as ogemm
+    from oracle import norm as onorm
+    x = synthetic.activations(M, K, seed=M + 41)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=N + 9)
+    W8 = W8.view(torch.uint8)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.to(dev), sb.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemm.gemm_a8w8(q, sa, W8, sb), f"a8w8 rows-per-pass M={M} K={K} N={N}")
+
+
 def test_gemv_misaligned_input(ops, dev):
     # an input view starting 2 bytes into its buffer -> generic path
     N, K = 64, 256

@@ -34,11 +34,14 @@
 //    same tile and reduce through LDS.
 //  * gemv_generic_kernel: any K / alignment; byte loads.  Correctness path
 //    for shapes the vector kernels do not take.
+#include <climits>
 #include <type_traits>
 
 #include "cek_rowops.h"
 
 namespace cek {
+
+constexpr int kCUs = 256;  // MI355X compute units, for the launch-balance rules
 
 
 int launch_w8a16(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N, int64_t K,
@@ -1492,12 +1495,29 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
       CEK_LDS_T(NT, D, MX, 1, ROT);                       \
     }                                                     \
   } while (0)
-  // K = 4096 or 5120 (4-5 stages per 16-row tile): consecutive tiles per
-  // workgroup, as many as keep >= 224 workgroups (measured on MI355X: 4
-  // tiles at N = 14336 and 28672, M = 4: 15.7 -> 13.2 and 25.9 -> 22.7 us;
-  // 2 at N = 6144; one below 384 tiles).  At K = 3072 one tile was fastest.
+  // K = 4096 or 5120 (4-5 stages per 16-row tile): TPW consecutive tiles
+  // per workgroup.  A workgroup streams at a rate its stages in flight set,
+  // so a launch takes as long as its busiest CU's tiles: of 4, 2 and 1 tiles
+  // per workgroup the count whose busiest CU gets the fewest tiles
+  // (tpw * ceil(workgroups / CUs)), the larger count on a tie (its
+  // workgroups fill their pipelines fewer times).  Measured on MI355X at
+  // M = 4 (weights from HBM, us for 4 / 2 / 1 tiles): N = 14336 12.78 /
+  // 13.36 / 13.19; N = 20480 21.05 / 17.94 / 16.99; N = 24576 21.21 / 19.46
+  // / 19.71; N = 28672 22.40 / 23.14 / 21.88; N = 32768 23.01 / 24.12 /
+  // 25.66; N = 6144: 2 tiles 7.84, 1 tile 8.21.  The forms agree bit for bit.
+  // At K = 3072 one tile was fastest.
   const int tiles = (N + 15) / 16;
-  const int tpw = MULTI ? (tiles >= 896 ? 4 : (tiles >= 384 ? 2 : 1)) : 1;
+  int tpw = 1;
+  if constexpr (MULTI) {
+    int busiest = INT_MAX;
+    for (int c = 4; c >= 1; c >>= 1) {
+      const int load = c * (((tiles + c - 1) / c + kCUs - 1) / kCUs);
+      if (load < busiest) {
+        busiest = load;
+        tpw = c;
+      }
+    }
+  }
   if constexpr (!XF8) {
     // fp16/bf16, M <= 8: activations staged through LDS (contiguous loads
     // of just the M rows); for long K only up to 12288 rows (5-20% faster

@@ -407,7 +407,7 @@ __device__ inline void lds_load_scales(uint32_t (&sc_n)[NT], float (&sc_m)[MB][4
 // COH: the outputs are stored at device scope (global_store ... sc1: written
 // through to the level every XCD sees), for a tail epilogue that another
 // workgroup runs on them.
-template <int NT, int MB, bool COH = false>
+template <int NT, int MB, bool COH = false, int ROWS = 16>
 __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wave, int lane, int n0, int N,
                                         int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
                                         const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
@@ -425,7 +425,7 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int n = n0 + t * 16 + n16;  // D column = lane & 15
-    if (n >= N) continue;
+    if (n >= N || n16 >= ROWS) continue;  // (ROWS < 16: columns past the tile repeat its last row)
     const float sc = scale_value(sc_n[t], skind);
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
@@ -540,14 +540,14 @@ __device__ inline void lds_reduce_tile(const f4 (&acc)[NT][MB], uint8_t* redp, i
 
 // lds_reduce_store for one tile of a multi-tile workgroup (n0 = the tile's
 // first row).
-template <int NT, int MB>
+template <int NT, int MB, int ROWS = 16>
 __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* redp, int wave, int lane, int n0, int N,
                                              int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
                                              const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
   const int n16 = lane & 15, g = lane >> 4;
   lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, xscaled, [&](int t, int b, int v, float o) {
     const int n = n0 + t * 16 + n16, m = b * 16 + g * 4 + v;  // D column = lane & 15, row = 4 (lane >> 4) + v
-    if (n < N && m < M) sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+    if (n < N && n16 < ROWS && m < M) sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
   });
 }
 
@@ -698,7 +698,8 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
 // runtime chunk offsets cost VALU address arithmetic, which made the
 // multi-tile and M > 4 forms 1-5% slower with it.
 template <typename T, typename TO, int FMT, bool XF8, int NT, int MB, int D, int STEPS, int MX = 0, int TPW = 1,
-          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0, bool ROT = false, int EPI = EPI_NONE>
+          bool GLU = false, bool NORM = false, int TAIL = TAIL_NONE, int TP = 0, bool ROT = false, int EPI = EPI_NONE,
+          bool R12 = false>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs sg, int skind, int M, NormArgs na) {
   constexpr bool PROD = EPI == EPI_ADDNORM || EPI == EPI_ADDNORM12;  // deferred-norm producer
   static_assert(!PROD || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !XF8 &&
@@ -714,8 +715,10 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   static_assert(TAIL == TAIL_NONE || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && !XF8 &&
                                       std::is_same<T, TO>::value),
                 "tails: one 16-row tile per workgroup, fp16 / bf16 activations");
+  static_assert(!R12 || (NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !ROT && EPI == EPI_NONE),
+                "12-row plain tiles: one tile wide, no K rotation (so each output's sum order is the 16-row form's)");
   constexpr int K = STEPS * 1024;
-  constexpr int ROWS = EPI == EPI_ADDNORM12 ? 12 : 16 * NT, S = D + 1, STAGE = ROWS * 1024;
+  constexpr int ROWS = EPI == EPI_ADDNORM12 || R12 ? 12 : 16 * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
   constexpr int XB = XF8 ? 1 : 2;  // activation bytes per value
   constexpr int LW = ROWS / 4;     // weight rows per wave and stage
@@ -1137,8 +1140,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
             });
           }
         } else {
-          lds_reduce_store_tile<NT, MB>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
-                                        XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
+          lds_reduce_store_tile<NT, MB, ROWS>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
+                                              XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
         }
         if (i + 1 < NS) {
 #pragma unroll
@@ -1156,8 +1159,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   if constexpr (PROD)
     lds_reduce_addnorm<T, ROWS>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
   else if constexpr (TPW == 1)
-    lds_reduce_store<NT, MB, TAIL != TAIL_NONE>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
-                                                XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
+    lds_reduce_store<NT, MB, TAIL != TAIL_NONE, ROWS>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
+                                                      XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
   if constexpr (TAIL != TAIL_NONE) gemv_tail<T, TAIL, TP>(na.tail, sr.y, nw, N, M, smem, rcs, rsn);
 }
 
@@ -1485,15 +1488,26 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
       <<<dim3(seg_grid(sg, 16 * (NT) * (TPW))), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
   constexpr bool SHORT = S >= 3 && S <= 5;
   constexpr bool MULTI = S == 4 || S == 5;  // multi-tile workgroups (K = 4096, 5120)
-#define CEK_LDS_TPW(NT, D, MX, ROT)                       \
-  do {                                                    \
-    if constexpr (MULTI) {                                \
-      if (tpw == 4) CEK_LDS_T(NT, D, MX, 4, ROT);         \
-      else if (tpw == 2) CEK_LDS_T(NT, D, MX, 2, ROT);    \
-      else CEK_LDS_T(NT, D, MX, 1, ROT);                  \
-    } else {                                              \
-      CEK_LDS_T(NT, D, MX, 1, ROT);                       \
-    }                                                     \
+#define CEK_LDS_T12(D, MX, TPW)                                                                          \
+  gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, TPW, false, false, TAIL_NONE, 0, false, EPI_NONE, true> \
+      <<<dim3(seg_grid(sg, 12 * (TPW))), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
+#define CEK_LDS_TPW(NT, D, MX, ROT)                                  \
+  do {                                                               \
+    if (!(ROT) && (NT) == 1 && r12) {                                \
+      if constexpr (MULTI) {                                         \
+        if (tpw12 == 4) CEK_LDS_T12(D, MX, 4);                       \
+        else if (tpw12 == 2) CEK_LDS_T12(D, MX, 2);                  \
+        else CEK_LDS_T12(D, MX, 1);                                  \
+      } else {                                                       \
+        CEK_LDS_T12(D, MX, 1);                                       \
+      }                                                              \
+    } else if constexpr (MULTI) {                                    \
+      if (tpw == 4) CEK_LDS_T(NT, D, MX, 4, ROT);                    \
+      else if (tpw == 2) CEK_LDS_T(NT, D, MX, 2, ROT);               \
+      else CEK_LDS_T(NT, D, MX, 1, ROT);                             \
+    } else {                                                         \
+      CEK_LDS_T(NT, D, MX, 1, ROT);                                  \
+    }                                                                \
   } while (0)
   // K = 4096 or 5120 (4-5 stages per 16-row tile): TPW consecutive tiles
   // per workgroup.  A workgroup streams at a rate its stages in flight set,
@@ -1506,18 +1520,36 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   // / 19.71; N = 28672 22.40 / 23.14 / 21.88; N = 32768 23.01 / 24.12 /
   // 25.66; N = 6144: 2 tiles 7.84, 1 tile 8.21.  The forms agree bit for bit.
   // At K = 3072 one tile was fastest.
-  const int tiles = (N + 15) / 16;
-  int tpw = 1;
-  if constexpr (MULTI) {
-    int busiest = INT_MAX;
-    for (int c = 4; c >= 1; c >>= 1) {
-      const int load = c * (((tiles + c - 1) / c + kCUs - 1) / kCUs);
-      if (load < busiest) {
-        busiest = load;
-        tpw = c;
+  // rows of the busiest CU with tiles of rt rows, c tiles per workgroup
+  auto busiest_rows = [&](int rt, int c) {
+    const int t = (N + rt - 1) / rt;
+    return rt * c * (((t + c - 1) / c + kCUs - 1) / kCUs);
+  };
+  auto pick_tpw = [&](int rt, int& rows) {
+    int best = 1;
+    rows = INT_MAX;
+    for (int c = MULTI ? 4 : 1; c >= 1; c >>= 1) {
+      const int r = busiest_rows(rt, c);
+      if (r < rows) {
+        rows = r;
+        best = c;
       }
     }
-  }
+    return best;
+  };
+  int rows16, rows12;
+  const int tpw = pick_tpw(16, rows16);
+  // 12-row tiles (the forms without the K rotation, one tile wide; MFMA
+  // operand lanes 12-15 repeat row 11 and are not stored): each output's
+  // sum is the 16-row form's bit for bit, so they are free to pick where
+  // they cut the busiest CU's rows by a fifth or more -- N = 6144 (24 rows
+  // against 32; measured on MI355X, weights from HBM: fp16 M = 8, K = 4096
+  // 8.17 -> 7.75 us, M = 5 7.82 -> 7.35, K = 5120 9.59 -> 9.06; e4m3
+  // activations M = 8, K = 4096 7.76 -> 7.10, K = 5120 8.84 -> 8.16, M = 4
+  // 7.04 -> 6.66) or N = 3072.  The 32-row tiles of 9-16 rows at N >= 6144
+  // stay (with 12-row tiles: M = 16, N = 6144 9.82 -> 11.23 us).
+  const int tpw12 = pick_tpw(12, rows12);
+  const bool r12 = 5 * rows12 <= 4 * rows16;
   if constexpr (!XF8) {
     // fp16/bf16, M <= 8: activations staged through LDS (contiguous loads
     // of just the M rows); for long K only up to 12288 rows (5-20% faster
@@ -1571,6 +1603,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   return false;
 #undef CEK_LDS
 #undef CEK_LDS_T
+#undef CEK_LDS_T12
 #undef CEK_LDS_TPW
 }
 

@@ -10,7 +10,8 @@ through the public ops:
 * esimd_gemm_fp8_a8w8 with 3 <= M <= 64 (e4m3 activations and weights);
 * the fused multi-matrix GEMV (segment table), whose segments share a launch;
 * K = 4096 or 5120 with many rows, where a workgroup streams two or four
-  consecutive 16-row tiles (N >= 384 or >= 896 tiles, ragged last workgroup).
+  consecutive 16-row tiles (ragged last workgroup);
+* 12-row tiles, where they balance the CUs better than 16-row ones.
 
 N values include ones that are not multiples of the 16- and 32-row tiles.
 Reference: the CPU oracle; tolerance |out - ref| <= 1e-2 max|ref| + 2e-2 |ref|.
@@ -162,3 +163,57 @@ def test_fused_segments_multi_tile(ops, dev):
     torch.cuda.synchronize()
     for w, s, y in zip(Ws, Ss, ys):
         assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, w, s), f"fused multi-tile N={w.shape[0]}")
+
+
+# 12-row tiles: the forms without the K rotation (5-8 fp16 / bf16 rows, e4m3
+# activations up to 8 rows, 9-16 rows below N = 6144) take them where they cut
+# the busiest CU's rows by a fifth (N = 6000-6150: 24 rows against 32; N =
+# 3000-3072: 12 against 16), ragged N ending inside a 12-row tile and inside a
+# two-tile workgroup.
+@pytest.mark.parametrize("M,K,N", [(5, 4096, 6144), (8, 4096, 6100), (7, 3072, 6000), (6, 5120, 6143), (12, 4096, 3000),
+                                   (16, 3072, 3072)])
+def test_gemv_12row_tiles(ops, dev, M, K, N):
+    _say(f"lds gemv 12-row tiles M={M} K={K} N={N}")
+    for io, fmt in [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)]:
+        W8, s = synthetic.weight_fp8(N, K, seed=N + K + 1, fmt=fmt)
+        x = synthetic.activations(M, K, seed=M + 13, dtype=io)
+        y = torch.full((M, N), float("nan"), dtype=io, device=dev)
+        ops.esimd_gemv_fp8_pern(x.to(dev), W8.to(dev), s.to(dev), y, N, K)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, W8, s), f"12-row M={M} K={K} N={N} {io}")
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 4096, 6144), (8, 5120, 6101), (8, 4096, 6144)])
+def test_a8w8_12row_tiles(ops, dev, M, K, N):
+    _say(f"lds a8w8 12-row tiles M={M} K={K} N={N}")
+    x = synthetic.activations(M, K, seed=M + 17)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=K + 21)
+    ref = ogemm.gemm_a8w8(q, sa, W8.view(torch.uint8), sb)
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.full((M, N), float("nan"), dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.view(torch.uint8).to(dev), sb.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ref, f"a8w8 12-row M={M} K={K} N={N} {out_dt}")
+
+
+# A matrix alone takes 12-row tiles; in a fused launch whose total row count
+# picks 16-row tiles (M = 8: 20480 rows, one tile per workgroup) or 32-row
+# tiles (M = 12: 6144 rows) it must still get the same outputs bit for bit
+# (the tile heights add each output's K chunks in the same order).
+@pytest.mark.parametrize("M,K,Ns", [(8, 4096, (6144, 14336)), (12, 3072, (3072, 3072))])
+def test_12row_fused_equals_single(ops, dev, M, K, Ns):
+    _say(f"lds 12-row fused == single M={M} K={K} Ns={Ns}")
+    x = synthetic.activations(M, K, seed=23)
+    Ws, Ss = zip(*[synthetic.weight_fp8(n, K, seed=n + 3) for n in Ns])
+    xd = x.to(dev)
+    Wd = [w.to(dev) for w in Ws]
+    Sd = [s.to(dev) for s in Ss]
+    ys = [torch.full((M, n), float("nan"), dtype=torch.float16, device=dev) for n in Ns]
+    ops.esimd_gemv_fp8_pern_fused(xd, Wd, Sd, ys)
+    for i, n in enumerate(Ns):
+        y1 = torch.full((M, n), float("nan"), dtype=torch.float16, device=dev)
+        ops.esimd_gemv_fp8_pern(xd, Wd[i], Sd[i], y1, n, K)
+        torch.cuda.synchronize()
+        assert torch.equal(ys[i], y1), f"matrix {i} (N={n})"
+        assert_close_fp(y1.cpu(), ogemv.gemv_fp8_pern(x, Ws[i], Ss[i]), f"matrix {i}")

@@ -1629,21 +1629,31 @@ static bool xres_matrix(int M, int K, int n) {
   return M >= 9 && M <= 16 && (K == 2048 || K == 3072 || K == 4096) && tiles > 512 && tiles <= 2048;
 }
 
-// gemv_xres_kernel over every segment of sg (all of them xres_matrix): TPB =
-// 4 tiles per slot up to 1024 tiles, else 8, one slot per workgroup (one
-// workgroup per CU) as far as 256 workgroups go.
+// gemv_xres_kernel over every segment of sg (all of them xres_matrix): one
+// slot per workgroup (one workgroup per CU) as far as the CUs go, TPB =
+// ceil(tiles / CUs) tiles per slot (3 to 8), so that the slots spread evenly
+// over the CUs (each tile's sum does not depend on TPB).  Measured on MI355X
+// at M = 16 against 4 tiles per slot up to 1024 tiles and 8 above (weights
+// from HBM): K = 4096, N = 9000 13.74 -> 12.36 us, N = 16400 23.24 -> 18.55,
+// N = 20480 23.86 -> 20.51, N = 24576 25.09 -> 22.50, N = 28672 26.72 ->
+// 25.78; K = 3072, N = 12288 12.17 -> 11.83; N = 14336 equal.
 template <typename T, typename TO, int FMT>
 static void launch_xres(const void* x, GemvSegs& sg, int skind, int M, int K, hipStream_t st) {
   const int tiles = seg_grid(sg, 16);  // gstart: first tile of each segment
-  const int tpb = tiles <= 1024 ? 4 : 8;
+  int tpb = (tiles + kCUs - 1) / kCUs;
+  tpb = tpb < 3 ? 3 : (tpb > 8 ? 8 : tpb);
   const int nslot = (tiles + tpb - 1) / tpb;
-  const dim3 grid((unsigned)(nslot < 256 ? nslot : 256));
+  const dim3 grid((unsigned)(nslot < kCUs ? nslot : kCUs));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
 #define CEK_XRES(KK, TT) gemv_xres_kernel<T, TO, FMT, KK, TT, 8><<<grid, 128 * (TT), 0, st>>>(xp, sg, skind, M, tiles)
 #define CEK_XRES_K(KK)            \
   do {                            \
-    if (tpb == 4) CEK_XRES(KK, 4); \
-    else CEK_XRES(KK, 8);         \
+    if (tpb == 3) CEK_XRES(KK, 3);      \
+    else if (tpb == 4) CEK_XRES(KK, 4); \
+    else if (tpb == 5) CEK_XRES(KK, 5); \
+    else if (tpb == 6) CEK_XRES(KK, 6); \
+    else if (tpb == 7) CEK_XRES(KK, 7); \
+    else CEK_XRES(KK, 8);               \
   } while (0)
   if (K == 2048) CEK_XRES_K(2048);
   else if (K == 3072) CEK_XRES_K(3072);

@@ -2,7 +2,7 @@
 512 < N / 16 <= 2048 row tiles per weight matrix run gemv_xres_kernel
 (activations resident in LDS, weights streamed into MFMA operands, each
 tile's K in two halves).  Checked against the CPU oracle (tolerance as in
-the other GEMV tests) over 4 and 8 tiles per workgroup slot, ragged N, both
+the other GEMV tests) over 3 to 8 tiles per workgroup slot, ragged N, both
 fp8 formats, both activation types and every scale kind; and, since its sum
 order differs from the other GEMV kernels', the multi-matrix op must still
 give each matrix, bit for bit, what the single op gives it -- with matrices
@@ -35,8 +35,9 @@ def _pern(ops, xd, Wd, sd, io):
     return y
 
 
-# (K, N): 563 tiles (4 per slot), 768, 1025 (8 per slot), 2048 (256 slots), ragged N
-SHAPES = [(4096, 9000), (3072, 12288), (4096, 16400), (2048, 32768), (4096, 14336)]
+# (K, N): tiles per slot ceil(tiles / 256): 563 tiles (3 per slot, ragged N),
+# 768 (3), 896 (4), 1025 (5, ragged), 1536 (6), 1792 (7), 2048 (8)
+SHAPES = [(4096, 9000), (3072, 12288), (4096, 14336), (4096, 16400), (4096, 24576), (2048, 28672), (2048, 32768)]
 
 
 @pytest.mark.parametrize("M", [9, 12, 16])

@@ -1321,9 +1321,14 @@ __global__ __launch_bounds__(128 * TPB) void gemv_xres_kernel(const uint16_t* __
 // ONE (the launch runs one slot per workgroup): the later K parts' sums go
 // through the activation area, once every wave is done reading it, so that
 // 32 rows of K = 5120 (160 KB, all of LDS) fit.
-template <typename TO, int K, int TPB, int KS, int PD, bool ONE = false>
+// RT = 12: tiles of 12 weight rows (the segment table counts 12-row groups);
+// operand lanes 12-15 load row 11 again (the same cache lines as lane 11's,
+// in the same instruction) and are not stored.  A tile's K parts and their
+// order do not depend on RT, so neither do the outputs.
+template <typename TO, int K, int TPB, int KS, int PD, bool ONE = false, int RT = 16>
 __global__ __launch_bounds__(64 * TPB * KS) void gemv_xres8_kernel(const uint8_t* __restrict__ x, GemvSegs sg, int M,
                                                                   int tiles) {
+  static_assert(RT == 16 || RT == 12, "tile rows");
   constexpr int MB = 2;
   constexpr int NCW = K / 128 / KS;  // 128-byte K chunks per wave and tile
   constexpr int XBYTES = 16 * MB * K, CPR = K / 16;
@@ -1340,11 +1345,11 @@ __global__ __launch_bounds__(64 * TPB * KS) void gemv_xres8_kernel(const uint8_t
   const int nslot = (tiles + TPB - 1) / TPB;
   auto wsrc = [&](int s) {
     const SegRef r = find_seg(sg, min(s * TPB + tw, tiles - 1));
-    return r.w + (size_t)min(16 * r.group + r16, r.n - 1) * K + (K / KS) * kh + 16 * g;
+    return r.w + (size_t)min(RT * r.group + min(r16, RT - 1), r.n - 1) * K + (K / KS) * kh + 16 * g;
   };
   auto scale_bits = [&](int s) {
     const SegRef r = find_seg(sg, min(s * TPB + tw, tiles - 1));
-    return kh == 0 ? load_scale_bits(r.s, SK_F32, min(16 * r.group + r16, r.n - 1)) : 0u;
+    return kh == 0 ? load_scale_bits(r.s, SK_F32, min(RT * r.group + min(r16, RT - 1), r.n - 1)) : 0u;
   };
   float scm[MB][4];  // the activation rows' scales (D row 16 b + 4 g + v)
 #pragma unroll
@@ -1415,9 +1420,9 @@ __global__ __launch_bounds__(64 * TPB * KS) void gemv_xres8_kernel(const uint8_t
     const int tile = s * TPB + tw;
     if (kh == 0 && tile < tiles) {
       const SegRef r = find_seg(sg, tile);
-      const int n = 16 * r.group + r16;
+      const int n = RT * r.group + r16;
       const float sc = scale_value(scb, SK_F32);
-      if (n < r.n) {
+      if (n < r.n && r16 < RT) {
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
           f4 c = acc[b];
@@ -1951,28 +1956,53 @@ int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const 
   // M = 24, N = 6144 13.37 -> 12.28, M = 32 15.12 -> 12.38).
   const int tiles16 = (int)((N + 15) / 16);
   const int m_min = tiles16 <= 512 ? 24 : 17;
+  // 12-row tiles (RT = 12) where they cut the busiest CU's rows by a fifth
+  // or more (N ~ 6144: 256 slots of 2 x 12 rows against 192 of 2 x 16; the
+  // outputs do not change).  Measured on MI355X, weights from HBM: M = 32,
+  // N = 6144, K = 4096 10.29 -> 9.89 us, K = 5120 12.36 -> 11.87 us; M = 24
+  // 10.17 -> 9.78 and 12.20 -> 11.69 us.
+  auto busiest_rows = [&](int rt) {
+    const int ns = ((int)((N + rt - 1) / rt) + 1) / 2;
+    return 2 * rt * ((ns + kCUs - 1) / kCUs);
+  };
+  const bool x12 = 5 * busiest_rows(12) <= 4 * busiest_rows(16);
   if (M >= m_min && M <= 32 && K == 5120 && tiles16 >= 384 && tiles16 <= 512) {
-    const int tiles = seg_grid(sg, 16);
+    // (RT = 12 only where one round of slots still covers its tiles)
+    const bool r12 = x12 && (((int)((N + 11) / 12) + 1) / 2 <= kCUs);
+    const int tiles = seg_grid(sg, r12 ? 12 : 16);
     const int nslot = (tiles + 1) / 2;
     const int m = (int)M;
-    if (out_dtype == CEK_F16) gemv_xres8_kernel<F16, 5120, 2, 4, 5, true><<<nslot, 512, 0, st>>>(x, sg, m, tiles);
-    else gemv_xres8_kernel<BF16, 5120, 2, 4, 5, true><<<nslot, 512, 0, st>>>(x, sg, m, tiles);
+#define CEK_X8ONE(TY, RTT) gemv_xres8_kernel<TY, 5120, 2, 4, 5, true, RTT><<<nslot, 512, 0, st>>>(x, sg, m, tiles)
+    if (out_dtype == CEK_F16) {
+      if (r12) CEK_X8ONE(F16, 12);
+      else CEK_X8ONE(F16, 16);
+    } else {
+      if (r12) CEK_X8ONE(BF16, 12);
+      else CEK_X8ONE(BF16, 16);
+    }
+#undef CEK_X8ONE
     return check_launch();
   }
   if (M >= m_min && M <= 32 && (K == 2048 || K == 3072 || K == 4096) && tiles16 >= 384) {
-    const int tiles = seg_grid(sg, 16);
+    const int tiles = seg_grid(sg, x12 ? 12 : 16);
     const int nslot = (tiles + 1) / 2;
-    const dim3 grid((unsigned)(nslot < 256 ? nslot : 256));
+    const dim3 grid((unsigned)(nslot < kCUs ? nslot : kCUs));
     const int m = (int)M;
-#define CEK_X8(KK, PP)                                                                                         \
-  do {                                                                                                         \
-    if (out_dtype == CEK_F16) gemv_xres8_kernel<F16, KK, 2, 4, PP><<<grid, 512, 0, st>>>(x, sg, m, tiles);     \
-    else gemv_xres8_kernel<BF16, KK, 2, 4, PP><<<grid, 512, 0, st>>>(x, sg, m, tiles);                         \
+#define CEK_X8R(KK, PP, RTT)                                                                                         \
+  do {                                                                                                               \
+    if (out_dtype == CEK_F16) gemv_xres8_kernel<F16, KK, 2, 4, PP, false, RTT><<<grid, 512, 0, st>>>(x, sg, m, tiles); \
+    else gemv_xres8_kernel<BF16, KK, 2, 4, PP, false, RTT><<<grid, 512, 0, st>>>(x, sg, m, tiles);                     \
+  } while (0)
+#define CEK_X8(KK, PP)               \
+  do {                               \
+    if (x12) CEK_X8R(KK, PP, 12);    \
+    else CEK_X8R(KK, PP, 16);        \
   } while (0)
     if (K == 2048) CEK_X8(2048, 4);
     else if (K == 3072) CEK_X8(3072, 6);
     else CEK_X8(4096, 4);
 #undef CEK_X8
+#undef CEK_X8R
     return check_launch();
   }
   if (M > 16) {  // only the LDS path takes these

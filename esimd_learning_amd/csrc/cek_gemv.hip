@@ -1507,6 +1507,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
         CEK_LDS_T12(D, MX, 1);                                       \
       }                                                              \
     } else if constexpr (MULTI) {                                    \
+      const int tpw = (ROT) ? tpw_rot : tpw_plain;                   \
       if (tpw == 4) CEK_LDS_T(NT, D, MX, 4, ROT);                    \
       else if (tpw == 2) CEK_LDS_T(NT, D, MX, 2, ROT);               \
       else CEK_LDS_T(NT, D, MX, 1, ROT);                             \
@@ -1516,15 +1517,17 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   } while (0)
   // K = 4096 or 5120 (4-5 stages per 16-row tile): TPW consecutive tiles
   // per workgroup.  A workgroup streams at a rate its stages in flight set,
-  // so a launch takes as long as its busiest CU's tiles: of 4, 2 and 1 tiles
-  // per workgroup the count whose busiest CU gets the fewest tiles
-  // (tpw * ceil(workgroups / CUs)), the larger count on a tie (its
-  // workgroups fill their pipelines fewer times).  Measured on MI355X at
-  // M = 4 (weights from HBM, us for 4 / 2 / 1 tiles): N = 14336 12.78 /
-  // 13.36 / 13.19; N = 20480 21.05 / 17.94 / 16.99; N = 24576 21.21 / 19.46
-  // / 19.71; N = 28672 22.40 / 23.14 / 21.88; N = 32768 23.01 / 24.12 /
-  // 25.66; N = 6144: 2 tiles 7.84, 1 tile 8.21.  The forms agree bit for bit.
-  // At K = 3072 one tile was fastest.
+  // so a launch takes as long as its busiest CU's share: of 4, 2 and 1 tiles
+  // per workgroup the count with the least ceil(workgroups / CUs) * (tpw *
+  // STEPS + F), F the stages' worth a workgroup loses filling its pipeline
+  // (0.5 for the M <= 4 forms, prefetch depth 3; 1.5 for the others), the
+  // larger count on a tie.  Measured on MI355X (weights from HBM, us for 4 /
+  // 2 / 1 tiles), M = 4: N = 14336 12.78 / 13.36 / 13.19; N = 20480 21.05 /
+  // 17.94 / 16.99; N = 24576 21.21 / 19.46 / 19.71; N = 28672 22.40 / 23.14 /
+  // 21.88; N = 32768 23.01 / 24.12 / 25.66; N = 6144: 2 tiles 7.84, 1 tile
+  // 8.21; M = 8: N = 20480 22.84 / - / 20.17, N = 24576 23.53 / 20.99 / -,
+  // M = 6, N = 28672 23.36 / - / 25.43.  The forms agree bit for bit.  At
+  // K = 3072 one tile was fastest.
   // rows of the busiest CU with tiles of rt rows, c tiles per workgroup
   auto busiest_rows = [&](int rt, int c) {
     const int t = (N + rt - 1) / rt;
@@ -1542,8 +1545,23 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
     }
     return best;
   };
+  // tiles per workgroup with a pipeline fill of f2 / 2 stages per workgroup
+  auto pick_tpw_fill = [&](int f2) {
+    int best = 1;
+    long cost = LONG_MAX;
+    for (int c = MULTI ? 4 : 1; c >= 1; c >>= 1) {
+      const long wgs = ((N + 15) / 16 + c - 1) / c;
+      const long k = ((wgs + kCUs - 1) / kCUs) * (2L * c * S + f2);
+      if (k < cost) {
+        cost = k;
+        best = c;
+      }
+    }
+    return best;
+  };
   int rows16, rows12;
-  const int tpw = pick_tpw(16, rows16);
+  pick_tpw(16, rows16);
+  const int tpw_rot = pick_tpw_fill(1), tpw_plain = pick_tpw_fill(3);
   // 12-row tiles (the forms without the K rotation, one tile wide; MFMA
   // operand lanes 12-15 repeat row 11 and are not stored): each output's
   // sum is the 16-row form's bit for bit, so they are free to pick where

@@ -1520,33 +1520,15 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   // so a launch takes as long as its busiest CU's share: of 4, 2 and 1 tiles
   // per workgroup the count with the least ceil(workgroups / CUs) * (tpw *
   // STEPS + F), F the stages' worth a workgroup loses filling its pipeline
-  // (0.5 for the M <= 4 forms, prefetch depth 3; 1.5 for the others), the
-  // larger count on a tie.  Measured on MI355X (weights from HBM, us for 4 /
-  // 2 / 1 tiles), M = 4: N = 14336 12.78 / 13.36 / 13.19; N = 20480 21.05 /
-  // 17.94 / 16.99; N = 24576 21.21 / 19.46 / 19.71; N = 28672 22.40 / 23.14 /
-  // 21.88; N = 32768 23.01 / 24.12 / 25.66; N = 6144: 2 tiles 7.84, 1 tile
-  // 8.21; M = 8: N = 20480 22.84 / - / 20.17, N = 24576 23.53 / 20.99 / -,
-  // M = 6, N = 28672 23.36 / - / 25.43.  The forms agree bit for bit.  At
-  // K = 3072 one tile was fastest.
-  // rows of the busiest CU with tiles of rt rows, c tiles per workgroup
-  auto busiest_rows = [&](int rt, int c) {
-    const int t = (N + rt - 1) / rt;
-    return rt * c * (((t + c - 1) / c + kCUs - 1) / kCUs);
-  };
-  auto pick_tpw = [&](int rt, int& rows) {
-    int best = 1;
-    rows = INT_MAX;
-    for (int c = MULTI ? 4 : 1; c >= 1; c >>= 1) {
-      const int r = busiest_rows(rt, c);
-      if (r < rows) {
-        rows = r;
-        best = c;
-      }
-    }
-    return best;
-  };
-  // tiles per workgroup with a pipeline fill of f2 / 2 stages per workgroup
-  auto pick_tpw_fill = [&](int f2) {
+  // (0.5 for the rotated forms -- fp16 / bf16, M <= 4, prefetch depth 3 --
+  // and 1.5 for the others), the larger count on a tie.  Measured on MI355X
+  // (weights from HBM, us for 4 / 2 / 1 tiles), M = 4: N = 14336 12.78 /
+  // 13.36 / 13.19; N = 20480 21.05 / 17.94 / 16.99; N = 24576 21.21 / 19.46
+  // / 19.71; N = 28672 22.40 / 23.14 / 21.88; N = 32768 23.01 / 24.12 /
+  // 25.66; N = 6144: 2 tiles 7.84, 1 tile 8.21; M = 8: N = 20480 22.84 / - /
+  // 20.17, N = 24576 23.53 / 20.99 / -, M = 6, N = 28672 23.36 / - / 25.43.
+  // The forms agree bit for bit.  At K = 3072 one tile was fastest.
+  auto pick_tpw_fill = [&](int f2) {  // f2 = 2 F
     int best = 1;
     long cost = LONG_MAX;
     for (int c = MULTI ? 4 : 1; c >= 1; c >>= 1) {
@@ -1559,8 +1541,6 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
     }
     return best;
   };
-  int rows16, rows12;
-  pick_tpw(16, rows16);
   const int tpw_rot = pick_tpw_fill(1), tpw_plain = pick_tpw_fill(3);
   // 12-row tiles (the forms without the K rotation, one tile wide; MFMA
   // operand lanes 12-15 repeat row 11 and are not stored): each output's
@@ -1571,7 +1551,24 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   // activations M = 8, K = 4096 7.76 -> 7.10, K = 5120 8.84 -> 8.16, M = 4
   // 7.04 -> 6.66) or N = 3072.  The 32-row tiles of 9-16 rows at N >= 6144
   // stay (with 12-row tiles: M = 16, N = 6144 9.82 -> 11.23 us).
-  const int tpw12 = pick_tpw(12, rows12);
+  // least_rows(rt, rows): the tiles per workgroup that give the busiest CU
+  // the fewest rows with tiles of rt rows, and that count of rows
+  auto least_rows = [&](int rt, int& rows) {
+    const int t = (N + rt - 1) / rt;
+    int best = 1;
+    rows = INT_MAX;
+    for (int c = MULTI ? 4 : 1; c >= 1; c >>= 1) {
+      const int r = rt * c * (((t + c - 1) / c + kCUs - 1) / kCUs);
+      if (r < rows) {
+        rows = r;
+        best = c;
+      }
+    }
+    return best;
+  };
+  int rows16, rows12;
+  least_rows(16, rows16);
+  const int tpw12 = least_rows(12, rows12);
   const bool r12 = 5 * rows12 <= 4 * rows16;
   if constexpr (!XF8) {
     // fp16/bf16, M <= 8: activations staged through LDS (contiguous loads

@@ -217,3 +217,17 @@ def test_12row_fused_equals_single(ops, dev, M, K, Ns):
         torch.cuda.synchronize()
         assert torch.equal(ys[i], y1), f"matrix {i} (N={n})"
         assert_close_fp(y1.cpu(), ogemv.gemv_fp8_pern(x, Ws[i], Ss[i]), f"matrix {i}")
+
+
+@pytest.mark.parametrize("M,K,N", [(8, 4096, 6144), (12, 3072, 3070)])
+def test_gemv_pert_12row_tiles(ops, dev, M, K, N):
+    """The per-tensor-scale op on 12-row tiles (fp16 and bf16)."""
+    _say(f"lds gemv pert 12-row tiles M={M} K={K} N={N}")
+    W8, _ = synthetic.weight_fp8(N, K, seed=N + 31)
+    sv = torch.tensor(0.031)
+    for io in (torch.float16, torch.bfloat16):
+        x = synthetic.activations(M, K, seed=M + 37, dtype=io)
+        y = torch.full((M, N), float("nan"), dtype=io, device=dev)
+        ops.esimd_gemv_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ogemv.gemv_fp8_pert(x, W8, sv), f"pert 12-row M={M} K={K} N={N} {io}")

@@ -43,7 +43,6 @@ namespace cek {
 
 constexpr int kCUs = 256;  // MI355X compute units, for the launch-balance rules
 
-
 int launch_w8a16(const void* x, const void* w, const void* scale, int skind, void* y, int64_t M, int64_t N, int64_t K,
                  int io_dtype, int fp8_fmt, float* ws, int64_t ws_bytes, hipStream_t st);  // cek_gemm.hip
 
@@ -665,6 +664,12 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
 // cross-wave reduction and store while the next tile's stages are already in
 // flight.  For short K (few stages per tile) this spreads the pipeline fill
 // and the epilogue of a workgroup over several tiles.
+//
+// R12: tiles of 12 rows instead of 16 (each wave streams 3 rows per stage;
+// MFMA operand lanes 12-15 read row 11 again and are not stored), so that a
+// launch can spread its rows more evenly over the CUs.  Only without ROT:
+// every tile then reads its K chunks in the same order, so each output's sum
+// is the 16-row form's bit for bit.
 //
 // GLU (gate/up matrix with gelu_and_mul fused into the epilogue; TPW = 2,
 // one segment of N = 2 d rows): the workgroup's two tiles are gate rows

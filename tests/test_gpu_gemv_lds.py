@@ -123,10 +123,13 @@ def test_fused_segments_lds(ops, dev):
 
 
 @pytest.mark.parametrize("M,K,N", [(4, 4096, 14336), (3, 4096, 14350), (8, 4096, 28700), (6, 5120, 14400),
-                                   (4, 3072, 12300), (2, 4096, 14336)])
+                                   (4, 3072, 12300), (2, 4096, 14336),
+                                   (4, 4096, 20470), (3, 5120, 24570), (8, 4096, 24570), (8, 4096, 20470)])
 def test_gemv_multi_tile(ops, dev, M, K, N):
     """Workgroups that own 2 or 4 consecutive tiles (the last one partly
-    past N), fp16 and bf16 activations."""
+    past N), fp16 and bf16 activations; at 1280 and 1536 tiles the
+    launch-balance rule picks 1 or 2 tiles per workgroup for the rotated
+    (M <= 4) and the other forms."""
     _say(f"lds gemv multi-tile M={M} K={K} N={N}")
     W8, s = synthetic.weight_fp8(N, K, seed=N + K)
     x = synthetic.activations(M, K, seed=M + 11)

@@ -32,8 +32,18 @@
 //    (l & 15) of a 16-row tile at k-offset 16 * (l >> 4) of each 64-byte
 //    step.  The four waves of a workgroup interleave over the K steps of the
 //    same tile and reduce through LDS.
+//  * gemv_xres_kernel (9 <= M <= 16, 512 < N / 16 <= 2048, K <= 4096) and
+//    gemv_xres8_kernel (e4m3 activations, 17 <= M <= 32): the activations
+//    stay in LDS for the whole launch and the weights stream straight into
+//    MFMA operand registers (see the comments at the kernels).
 //  * gemv_generic_kernel: any K / alignment; byte loads.  Correctness path
 //    for shapes the vector kernels do not take.
+//
+// Launch balance: a weight-streaming workgroup runs at the rate its loads in
+// flight allow, so a launch lasts as long as its busiest CU's share.  The
+// launchers pick rows per workgroup (tiles per workgroup or slot, 12- or
+// 16-row tiles) to even that share out over the 256 CUs, among forms whose
+// outputs agree bit for bit.
 #include <climits>
 #include <type_traits>
 

@@ -1996,7 +1996,13 @@ int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const 
     return 2 * rt * ((ns + kCUs - 1) / kCUs);
   };
   const bool x12 = 5 * busiest_rows(12) <= 4 * busiest_rows(16);
-  if (M >= m_min && M <= 32 && K == 5120 && tiles16 >= 384 && tiles16 <= 512) {
+  // With 12-row tiles the kernel also takes N from 384 12-row tiles (4608)
+  // up: M = 32, K = 4096, N = 4608 / 5120 / 6100 12.13 / 12.25 / 12.53 ->
+  // 8.92 / 9.20 / 9.91 us against the LDS kernel; K = 5120 14.81 / 14.87 /
+  // 15.05 -> 10.56 / 10.85 / 11.80 us; M = 24, N = 5120 10.77 -> 9.21 us.
+  const int tiles12 = (int)((N + 11) / 12);
+  const bool wide = tiles16 >= 384 || (x12 && tiles12 >= 384);
+  if (M >= m_min && M <= 32 && K == 5120 && wide && (tiles16 <= 512 || (x12 && tiles12 <= 512))) {
     // (RT = 12 only where one round of slots still covers its tiles)
     const bool r12 = x12 && (((int)((N + 11) / 12) + 1) / 2 <= kCUs);
     const int tiles = seg_grid(sg, r12 ? 12 : 16);
@@ -2013,7 +2019,7 @@ int launch_gemv_a8w8(const uint8_t* x, const float* xs, const uint8_t* w, const 
 #undef CEK_X8ONE
     return check_launch();
   }
-  if (M >= m_min && M <= 32 && (K == 2048 || K == 3072 || K == 4096) && tiles16 >= 384) {
+  if (M >= m_min && M <= 32 && (K == 2048 || K == 3072 || K == 4096) && wide) {
     const int tiles = seg_grid(sg, x12 ? 12 : 16);
     const int nslot = (tiles + 1) / 2;
     const dim3 grid((unsigned)(nslot < kCUs ? nslot : kCUs));

@@ -108,10 +108,11 @@ def test_xres_multi_matrix_equals_single(ops, dev, M, Ns, K):
 # workgroup.  K = 5120 (the 32 activation rows fill all of LDS; the K parts'
 # sums reuse it) up to 512 tiles; N = 14336 at K = 5120 and M = 17 at up to
 # 512 tiles stay on the other kernel.  N ~ 6144 runs 12-row tiles (256 slots),
-# N = 6140 and 6130 with a ragged last one.
+# N = 6140 and 6130 with a ragged last one; 12-row tiles also take N from 384
+# of them (4608) up, from 24 rows (N = 4608, 5000, 5120).
 @pytest.mark.parametrize("M", [17, 24, 32])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 6140), (3072, 12288), (2048, 8200), (4096, 28672), (5120, 6144),
-                                 (5120, 6130), (5120, 8190), (5120, 14336)])
+                                 (5120, 6130), (5120, 8190), (5120, 14336), (4096, 4608), (4096, 5000), (5120, 5120)])
 def test_xres8_a8w8_vs_oracle(ops, dev, M, K, N):
     from oracle import gemm as ogemm
     from oracle import norm as onorm

@@ -1609,10 +1609,13 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   }
   if (M <= 16) {
     if constexpr (SHORT) {
-      // Two 16-row tiles per workgroup halve the activation re-reads once
-      // there are enough rows to keep >= 192 workgroups.
+      // Two 16-row tiles per workgroup halve the activation re-reads; they
+      // pay once there are more 16-row tiles than CUs (measured on MI355X,
+      // M = 16, K = 4096, weights from HBM: N = 4608 11.02 -> 9.26 us, N =
+      // 5120 11.03 -> 9.31, K = 3072, N = 5120 8.94 -> 7.54; M = 12, N = 5120
+      // 9.76 -> 8.88; at N = 4096, one tile per CU, 7.67 -> 9.16 slower).
       // (fp16 / bf16 M <= 4 took the staged form above)
-      if (N >= 6144 && (XF8 ? M > 8 : M >= 8)) CEK_LDS(2, 1, 2);
+      if ((N + 15) / 16 > kCUs && (XF8 ? M > 8 : M >= 8)) CEK_LDS(2, 1, 2);
       else CEK_LDS_TPW(1, 3, 0, false);
     } else if constexpr (XF8 && S >= 3) {
       CEK_LDS(1, 1, 3);

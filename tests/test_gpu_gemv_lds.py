@@ -36,8 +36,10 @@ def _say(msg):
     sys.stdout.flush()
 
 
-# (K, N): every instantiated K, with N on both sides of the 6144-row switch
-SHAPES = [(2048, 1000), (3072, 6200), (4096, 6144), (4096, 2050), (5120, 6150), (14336, 1030), (24576, 520)]
+# (K, N): every instantiated K, with N on both sides of the switch to 32-row
+# tiles for 9-16 rows (more 16-row tiles than CUs: N = 4610 and up)
+SHAPES = [(2048, 1000), (3072, 6200), (4096, 6144), (4096, 2050), (5120, 6150), (14336, 1030), (24576, 520),
+          (4096, 4610)]
 
 
 @pytest.mark.parametrize("K,N", SHAPES)

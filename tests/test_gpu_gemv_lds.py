@@ -84,7 +84,7 @@ def test_gemm_pert_skinny(ops, dev, M, K, N):
 
 @pytest.mark.parametrize("M,K,N", [(3, 3072, 1000), (7, 24576, 300), (12, 4096, 6160), (16, 5120, 6144),
                                    (20, 4096, 3000), (32, 14336, 1024), (33, 4096, 2000), (64, 2048, 8192),
-                                   (48, 4096, 9000)])
+                                   (48, 4096, 9000), (12, 4096, 4610), (16, 5120, 5000)])
 def test_a8w8_skinny(ops, dev, M, K, N):
     """a8w8 M <= 64: LDS kernel with 1, 2 and 4 activation blocks (and the
     tiled GEMM for M > 32, N > 8192).  The torch op gives the split-K plan

@@ -1780,6 +1780,16 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
     const int64_t need = a8w8_workspace_bytes(M, N, K);
     const A8w8Plan plan = plan_a8w8(M, N, K, off32, need > 0 && ws && ws_bytes >= need);
     const int cfg = plan.cfg;
+    // The split 64 x 128 plan with fewer parts than CUs runs 64 x 96 tiles
+    // instead where those still make one part per CU at most: the outputs are
+    // the same (a part's K order and the parts' order do not depend on the
+    // tile), and the CUs are evenly loaded (measured on MI355X, weights from
+    // HBM: M = 64, N = 6144, K = 4096 13.11 -> 12.64 us, K = 5120 13.20 ->
+    // 12.59 us, 192 -> 256 workgroups; where 64 x 128 already fills the CUs,
+    // 64 x 96 was slower, e.g. K = 14336, N = 4096 17.83 -> 21.46 us).
+    constexpr int64_t kCUs = 256;  // MI355X compute units
+    auto parts = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * plan.split; };
+    const bool n96 = cfg == 0 && plan.split > 1 && parts(64, 128) < kCUs && parts(64, 96) <= kCUs;
     const bool pipe = off32 && M >= kA8w8Opts[cfg].bm && N >= kA8w8Opts[cfg].bn;
 #define CEK_A8W8(TY, BM, BN, WM, WN, OCC)                                                               \
   do {                                                                                                \
@@ -1819,6 +1829,7 @@ static int launch_a8w8(const uint8_t* a, const float* sa, const uint8_t* b, cons
       if (cfg == 6) CEK_A8W8_SPLITS(TY, 256, 128, 2, 4, 1, 4, 3);                      \
       else if (cfg == 5) CEK_A8W8_SPLITS(TY, 128, 256, 2, 4, 1, 4, 3);                 \
       else if (cfg == 1) CEK_A8W8_SPLITS(TY, 128, 128, 2, 2, 2, 4, 2);                 \
+      else if (n96) CEK_A8W8_SPLITS(TY, 64, 96, 2, 2, 2, 2, 3);                        \
       else CEK_A8W8_SPLITS(TY, 64, 128, 2, 2, 2, 2, 3);                                \
     } else if (cfg == 7) {                                                             \
       CEK_A8W8_PIPE(TY, 128, 96, 4, 2, 1, 4, 3);                                       \

@@ -209,13 +209,13 @@ def test_a8w8_large_tiles(ops, dev, M, K, N):
 def test_a8w8_split_k(ops, dev, M, K, N):
     """Shapes with too few output tiles split K (the op allocates the
     workspace the plan asks for): 64 x 128 tiles in 8, 4 and 2 parts (M = 64
-    included, which without a workspace takes the weight-streaming kernels),
-    128 x 256 in 4 parts, 128 x 128 (four waves) in 8 and 4 parts.  Against
-    the CPU oracle;
+    included, which without a workspace takes the weight-streaming kernels;
+    at N = 6144 on 64 x 96 tiles, 256 parts), 128 x 256 in 4 parts, 128 x 128
+    (four waves) in 8 and 4 parts.  Against the CPU oracle;
     the unsplit C-ABI call (no workspace) agrees within the same tolerance;
     two split calls agree bit for bit (the parts are added in order), and a
     workspace 4 bytes off 16-byte alignment (the finalize's element-by-element
-    form, also taken for N % 8 != 0) gives the same outputs."""
+    form, also taken for N % 4 != 0) gives the same outputs."""
     from esimd_learning_amd import cabi
     _say(f"a8w8 split K M={M} K={K} N={N}")
     lib = cabi.load()

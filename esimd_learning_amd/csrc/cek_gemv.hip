@@ -398,15 +398,17 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
 //    units per lane feed one v_mfma_f32_16x16x128_f8f6f4 (no decode).
 // ---------------------------------------------------------------------------
 // Wave 0's output scales of the LDS-staged kernels: sc_n[t] (raw bits) for
-// column n0 + 16 t + (lane & 15), sc_m[b][v] for row 16 b + 4 (lane >> 4) + v (xs:
-// per-row activation scales, or null).  Loaded at the start of the kernel so
-// that their latency overlaps the weight loads'.
-template <int NT, int MB>
+// column n0 + SH t + (lane & 15) (SH = 16 or 12 rows per MFMA tile; lanes past
+// SH repeat the tile's last row), sc_m[b][v] for row 16 b + 4 (lane >> 4) + v
+// (xs: per-row activation scales, or null).  Loaded at the start of the
+// kernel so that their latency overlaps the weight loads'.
+template <int NT, int MB, int SH = 16>
 __device__ inline void lds_load_scales(uint32_t (&sc_n)[NT], float (&sc_m)[MB][4], int wave, int lane, int n0, int N,
                                        int M, const SegRef& sr, int skind, const float* xs) {
   const int n16 = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) sc_n[t] = wave == 0 ? load_scale_bits(sr.s, skind, min(n0 + t * 16 + n16, N - 1)) : 0u;
+  for (int t = 0; t < NT; ++t)
+    sc_n[t] = wave == 0 ? load_scale_bits(sr.s, skind, min(n0 + t * SH + min(n16, SH - 1), N - 1)) : 0u;
 #pragma unroll
   for (int b = 0; b < MB; ++b)
 #pragma unroll
@@ -415,8 +417,9 @@ __device__ inline void lds_load_scales(uint32_t (&sc_n)[NT], float (&sc_m)[MB][4
 
 // COH: the outputs are stored at device scope (global_store ... sc1: written
 // through to the level every XCD sees), for a tail epilogue that another
-// workgroup runs on them.
-template <int NT, int MB, bool COH = false, int ROWS = 16>
+// workgroup runs on them.  SH: rows per MFMA tile (16, or 12 with operand
+// columns 12-15 repeating row 11, which are not stored).
+template <int NT, int MB, bool COH = false, int SH = 16>
 __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wave, int lane, int n0, int N,
                                         int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
                                         const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
@@ -433,8 +436,8 @@ __device__ inline void lds_reduce_store(f4 (&acc)[NT][MB], uint8_t* smem, int wa
   const int n16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int n = n0 + t * 16 + n16;  // D column = lane & 15
-    if (n >= N || n16 >= ROWS) continue;  // (ROWS < 16: columns past the tile repeat its last row)
+    const int n = n0 + t * SH + n16;  // D column = lane & 15
+    if (n >= N || n16 >= SH) continue;
     const float sc = scale_value(sc_n[t], skind);
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
@@ -549,14 +552,14 @@ __device__ inline void lds_reduce_tile(const f4 (&acc)[NT][MB], uint8_t* redp, i
 
 // lds_reduce_store for one tile of a multi-tile workgroup (n0 = the tile's
 // first row).
-template <int NT, int MB, int ROWS = 16>
+template <int NT, int MB, int SH = 16>
 __device__ inline void lds_reduce_store_tile(const f4 (&acc)[NT][MB], uint8_t* redp, int wave, int lane, int n0, int N,
                                              int M, const SegRef& sr, int skind, const uint32_t (&sc_n)[NT],
                                              const float (&sc_m)[MB][4], bool xscaled, bool bf16_out) {
   const int n16 = lane & 15, g = lane >> 4;
   lds_reduce_tile<NT, MB>(acc, redp, wave, lane, skind, sc_n, sc_m, xscaled, [&](int t, int b, int v, float o) {
-    const int n = n0 + t * 16 + n16, m = b * 16 + g * 4 + v;  // D column = lane & 15, row = 4 (lane >> 4) + v
-    if (n < N && n16 < ROWS && m < M) sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
+    const int n = n0 + t * SH + n16, m = b * 16 + g * 4 + v;  // D column = lane & 15, row = 4 (lane >> 4) + v
+    if (n < N && n16 < SH && m < M) sr.y[(size_t)m * N + n] = bf16_out ? BF16::from_f32(o) : F16::from_f32(o);
   });
 }
 
@@ -675,11 +678,12 @@ __device__ void gemv_tail(const TailArgs& ta, uint16_t* y, int n0, int N, int M,
 // flight.  For short K (few stages per tile) this spreads the pipeline fill
 // and the epilogue of a workgroup over several tiles.
 //
-// R12: tiles of 12 rows instead of 16 (each wave streams 3 rows per stage;
-// MFMA operand lanes 12-15 read row 11 again and are not stored), so that a
-// launch can spread its rows more evenly over the CUs.  Only without ROT:
-// every tile then reads its K chunks in the same order, so each output's sum
-// is the 16-row form's bit for bit.
+// R12: tiles of 12 rows instead of 16 (each wave streams 3 rows per stage
+// and tile; MFMA operand lanes 12-15 read row 11 again and are not stored),
+// so that a launch can spread its rows more evenly over the CUs; NT = 2 then
+// gives 24-row workgroups.  Only without ROT: every tile then reads its K
+// chunks in the same order, so each output's sum is the 16-row form's bit
+// for bit.
 //
 // GLU (gate/up matrix with gelu_and_mul fused into the epilogue; TPW = 2,
 // one segment of N = 2 d rows): the workgroup's two tiles are gate rows
@@ -730,10 +734,12 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   static_assert(TAIL == TAIL_NONE || (TPW == 1 && NT == 1 && MB == 1 && !GLU && !NORM && !XF8 &&
                                       std::is_same<T, TO>::value),
                 "tails: one 16-row tile per workgroup, fp16 / bf16 activations");
-  static_assert(!R12 || (NT == 1 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !ROT && EPI == EPI_NONE),
-                "12-row plain tiles: one tile wide, no K rotation (so each output's sum order is the 16-row form's)");
+  static_assert(!R12 || (NT <= 2 && MB == 1 && !GLU && !NORM && TAIL == TAIL_NONE && !ROT && EPI == EPI_NONE),
+                "12-row plain tiles: one or two tiles wide, no K rotation (so each output's sum order is the 16-row "
+                "form's)");
   constexpr int K = STEPS * 1024;
-  constexpr int ROWS = EPI == EPI_ADDNORM12 || R12 ? 12 : 16 * NT, S = D + 1, STAGE = ROWS * 1024;
+  constexpr int SH = EPI == EPI_ADDNORM12 || R12 ? 12 : 16;  // rows of one MFMA tile
+  constexpr int ROWS = SH * NT, S = D + 1, STAGE = ROWS * 1024;
   constexpr int QN = XF8 ? 2 : 4;  // operand groups per wave and stage
   constexpr int XB = XF8 ? 1 : 2;  // activation bytes per value
   constexpr int LW = ROWS / 4;     // weight rows per wave and stage
@@ -756,7 +762,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   const int N = sr.n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n16 = lane & 15, g = lane >> 4;
-  const int wn16 = ROWS < 16 ? min(n16, ROWS - 1) : n16;  // this lane's weight row of the stage (MFMA operand)
+  const int wn16 = SH < 16 ? min(n16, SH - 1) : n16;  // this lane's weight row of an MFMA tile (operand)
   const int half = GLU ? N >> 1 : 0;                 // GLU: d, the up rows' offset
   const int nw = sr.group * ROWS * (GLU ? 1 : TPW);  // first row of the workgroup
   // first row of tile t
@@ -773,7 +779,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   };
   uint32_t sc_n[NT];
   float sc_m[MB][4];
-  lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 && !NORM ? sg.xs : nullptr);
+  lds_load_scales<NT, MB, SH>(sc_n, sc_m, wave, lane, nw, N, M, sr, skind, XF8 && !NORM ? sg.xs : nullptr);
   // this wave loads rows wave + 4 j of every stage of tile t: row
   // tile_row(t) + wave + 4 j, clamped into the tile's matrix (clamped rows are
   // never stored)
@@ -1113,10 +1119,11 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const uint8_t* rw = sw + (16 * t + wn16) * 1024;  // row 16 t + wn16: slots are v ^ wn16
+        const int rr = SH * t + wn16;  // the lane's row of MFMA tile t in the stage
+        const uint8_t* rw = sw + rr * 1024;  // its unit v sits at slot v ^ (rr & 15)
         if constexpr (XF8) {
-          const i8 bf = cat_i8(*reinterpret_cast<const u4*>(rw + 16 * (v ^ wn16)),
-                               *reinterpret_cast<const u4*>(rw + 16 * ((v + 1) ^ wn16)));
+          const i8 bf = cat_i8(*reinterpret_cast<const u4*>(rw + 16 * (v ^ (rr & 15))),
+                               *reinterpret_cast<const u4*>(rw + 16 * ((v + 1) ^ (rr & 15))));
 #pragma unroll
           for (int b = 0; b < MB; ++b) {
             if constexpr (MX > 0) acc[t][b] = mfma_fp8_16x16x128(cat_i8(xa0, xa1), bf, acc[t][b]);
@@ -1124,7 +1131,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           }
         } else {
           u4 lo, hi;
-          decode16<T, FMT>(*reinterpret_cast<const u4*>(rw + 16 * (v ^ wn16)), lo, hi);
+          decode16<T, FMT>(*reinterpret_cast<const u4*>(rw + 16 * (v ^ (rr & 15))), lo, hi);
 #pragma unroll
           for (int b = 0; b < MB; ++b) {
             if constexpr (MX > 0) {
@@ -1155,7 +1162,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
             });
           }
         } else {
-          lds_reduce_store_tile<NT, MB, ROWS>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
+          lds_reduce_store_tile<NT, MB, SH>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
                                               XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
         }
         if (i + 1 < NS) {
@@ -1163,7 +1170,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
-          lds_load_scales<NT, MB>(sc_n, sc_m, wave, lane, tile_row(i / STEPS + 1), N, M, sr, skind,
+          lds_load_scales<NT, MB, SH>(sc_n, sc_m, wave, lane, tile_row(i / STEPS + 1), N, M, sr, skind,
                                   XF8 && !NORM ? sg.xs : nullptr);
           if constexpr (NORM && XF8) pick_row_scales();
           pick_rs();
@@ -1174,8 +1181,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
   if constexpr (PROD)
     lds_reduce_addnorm<T, ROWS>(acc[0][0], smem, wave, lane, nw, N, M, sr, skind, sc_n[0], na, pres, pnw);
   else if constexpr (TPW == 1)
-    lds_reduce_store<NT, MB, TAIL != TAIL_NONE, ROWS>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
-                                                      XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
+    lds_reduce_store<NT, MB, TAIL != TAIL_NONE, SH>(acc, smem, wave, lane, nw, N, M, sr, skind, sc_n, sc_m,
+                                                    XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
   if constexpr (TAIL != TAIL_NONE) gemv_tail<T, TAIL, TP>(na.tail, sr.y, nw, N, M, smem, rcs, rsn);
 }
 
@@ -1511,6 +1518,9 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
 #define CEK_LDS_T12(D, MX, TPW)                                                                          \
   gemv_lds_kernel<T, TO, FMT, XF8, 1, 1, D, S, MX, TPW, false, false, TAIL_NONE, 0, false, EPI_NONE, true> \
       <<<dim3(seg_grid(sg, 12 * (TPW))), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
+#define CEK_LDS_24(D)                                                                                   \
+  gemv_lds_kernel<T, TO, FMT, XF8, 2, 1, D, S, 0, 1, false, false, TAIL_NONE, 0, false, EPI_NONE, true> \
+      <<<dim3(seg_grid(sg, 24)), 256, 0, st>>>(x, sg, skind, M, NormArgs{})
 #define CEK_LDS_TPW(NT, D, MX, ROT)                                  \
   do {                                                               \
     if (!(ROT) && (NT) == 1 && r12) {                                \
@@ -1566,8 +1576,9 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   // against 32; measured on MI355X, weights from HBM: fp16 M = 8, K = 4096
   // 8.17 -> 7.75 us, M = 5 7.82 -> 7.35, K = 5120 9.59 -> 9.06; e4m3
   // activations M = 8, K = 4096 7.76 -> 7.10, K = 5120 8.84 -> 8.16, M = 4
-  // 7.04 -> 6.66) or N = 3072.  The 32-row tiles of 9-16 rows at N >= 6144
-  // stay (with 12-row tiles: M = 16, N = 6144 9.82 -> 11.23 us).
+  // 7.04 -> 6.66) or N = 3072.  9-16 rows above 256 16-row tiles take
+  // two-tile workgroups instead (one 12-row tile per workgroup: M = 16,
+  // N = 6144 9.82 -> 11.23 us).
   // least_rows(rt, rows): the tiles per workgroup that give the busiest CU
   // the fewest rows with tiles of rt rows, and that count of rows
   auto least_rows = [&](int rt, int& rows) {
@@ -1587,6 +1598,10 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   least_rows(16, rows16);
   const int tpw12 = least_rows(12, rows12);
   const bool r12 = 5 * rows12 <= 4 * rows16;
+  // two-tile workgroups: 2 x 12 rows where they cut the busiest CU's rows
+  // against 2 x 16 by a fifth or more (N = 4608-6144: 24 rows against 32)
+  auto busiest = [&](int wrows) { return wrows * (((N + wrows - 1) / wrows + kCUs - 1) / kCUs); };
+  const bool n24 = 5 * busiest(24) <= 4 * busiest(32);
   if constexpr (!XF8) {
     // fp16/bf16, M <= 8: activations staged through LDS (contiguous loads
     // of just the M rows); for long K only up to 12288 rows (5-20% faster
@@ -1616,9 +1631,21 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
       // M = 16, K = 4096, weights from HBM: N = 4608 11.02 -> 9.26 us, N =
       // 5120 11.03 -> 9.31, K = 3072, N = 5120 8.94 -> 7.54; M = 12, N = 5120
       // 9.76 -> 8.88; at N = 4096, one tile per CU, 7.67 -> 9.16 slower).
+      // Two 12-row tiles (24 rows) where that evens out the CUs (N = 4112 to
+      // 6144: every CU one workgroup of 24 rows instead of 3 in 4 CUs one of
+      // 32), same outputs: M = 16, K = 4096, N = 6144 9.48 -> 8.90 us, N =
+      // 4608 9.29 -> 8.54; M = 9, N = 4608 8.44 -> 7.54; M = 12, N = 6144
+      // 9.35 -> 8.52, K = 5120, N = 5120 9.88 -> 9.64; K = 3072, M = 16, N =
+      // 6144 7.88 -> 7.65; e4m3 activations M = 12, N = 6144 8.08 -> 7.37,
+      // M = 16, K = 5120 9.02 -> 8.84.  At 5-8 rows against the 12-row forms
+      // they were within +-3% at N = 6144 and are not used there.
       // (fp16 / bf16 M <= 4 took the staged form above)
-      if ((N + 15) / 16 > kCUs && (XF8 ? M > 8 : M >= 8)) CEK_LDS(2, 1, 2);
-      else CEK_LDS_TPW(1, 3, 0, false);
+      if ((N + 15) / 16 > kCUs && (XF8 ? M > 8 : M >= 8)) {
+        if (n24) CEK_LDS_24(2);
+        else CEK_LDS(2, 1, 2);
+      } else {
+        CEK_LDS_TPW(1, 3, 0, false);
+      }
     } else if constexpr (XF8 && S >= 3) {
       CEK_LDS(1, 1, 3);
     } else if constexpr (!XF8) {
@@ -1644,6 +1671,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
 #undef CEK_LDS
 #undef CEK_LDS_T
 #undef CEK_LDS_T12
+#undef CEK_LDS_24
 #undef CEK_LDS_TPW
 }
 

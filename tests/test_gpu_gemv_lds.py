@@ -202,11 +202,51 @@ def test_a8w8_12row_tiles(ops, dev, M, K, N):
         assert_close_fp(y.cpu(), ref, f"a8w8 12-row M={M} K={K} N={N} {out_dt}")
 
 
+# Two 12-row tiles per workgroup (24 rows): 9-16 rows (e4m3 activations: 9-16)
+# where there are more 16-row tiles than CUs and 24-row workgroups cut the
+# busiest CU's rows against 32-row ones by a fifth (N = 4112-6144); ragged N
+# ending inside either tile of the last workgroup.
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 6144), (9, 4096, 4112), (12, 5120, 5000), (16, 3072, 4610),
+                                   (13, 4096, 6133)])
+def test_gemv_24row_tiles(ops, dev, M, K, N):
+    _say(f"lds gemv 24-row tiles M={M} K={K} N={N}")
+    for io, fmt in [(torch.float16, torch.float8_e4m3fn), (torch.bfloat16, torch.float8_e5m2)]:
+        W8, s = synthetic.weight_fp8(N, K, seed=N + K + 5, fmt=fmt)
+        x = synthetic.activations(M, K, seed=M + 19, dtype=io)
+        y = torch.full((M, N), float("nan"), dtype=io, device=dev)
+        ops.esimd_gemv_fp8_pern(x.to(dev), W8.to(dev), s.to(dev), y, N, K)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ogemv.gemv_fp8_pern(x, W8, s), f"24-row M={M} K={K} N={N} {io}")
+    W8, _ = synthetic.weight_fp8(N, K, seed=N + 41)
+    sv = torch.tensor(0.029)
+    x = synthetic.activations(M, K, seed=M + 43)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    ops.esimd_gemv_fp8_pert(x.to(dev), W8.to(dev), sv.to(dev), y)
+    torch.cuda.synchronize()
+    assert_close_fp(y.cpu(), ogemv.gemv_fp8_pert(x, W8, sv), f"pert 24-row M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(12, 4096, 6144), (16, 5120, 4700), (9, 3072, 6100)])
+def test_a8w8_24row_tiles(ops, dev, M, K, N):
+    _say(f"lds a8w8 24-row tiles M={M} K={K} N={N}")
+    x = synthetic.activations(M, K, seed=M + 47)
+    q, sa = onorm.per_token_quant(x)
+    W8, sb = synthetic.weight_fp8(N, K, seed=K + 53)
+    ref = ogemm.gemm_a8w8(q, sa, W8.view(torch.uint8), sb)
+    for out_dt in (torch.float16, torch.bfloat16):
+        y = torch.full((M, N), float("nan"), dtype=out_dt, device=dev)
+        ops.esimd_gemm_fp8_a8w8(q.to(dev), sa.to(dev), W8.view(torch.uint8).to(dev), sb.to(dev), y)
+        torch.cuda.synchronize()
+        assert_close_fp(y.cpu(), ref, f"a8w8 24-row M={M} K={K} N={N} {out_dt}")
+
+
 # A matrix alone takes 12-row tiles; in a fused launch whose total row count
-# picks 16-row tiles (M = 8: 20480 rows, one tile per workgroup) or 32-row
-# tiles (M = 12: 6144 rows) it must still get the same outputs bit for bit
-# (the tile heights add each output's K chunks in the same order).
-@pytest.mark.parametrize("M,K,Ns", [(8, 4096, (6144, 14336)), (12, 3072, (3072, 3072))])
+# picks 16-row tiles (M = 8: 20480 rows, one tile per workgroup), 24-row
+# workgroups (M = 12: 6144 rows; M = 16: 6001 rows over two ragged matrices)
+# or 32-row ones (M = 12: 7168 rows) it must still get the same outputs bit
+# for bit (the tile heights add each output's K chunks in the same order).
+@pytest.mark.parametrize("M,K,Ns", [(8, 4096, (6144, 14336)), (12, 3072, (3072, 3072)), (16, 4096, (3000, 3001)),
+                                    (12, 4096, (3072, 4096))])
 def test_12row_fused_equals_single(ops, dev, M, K, Ns):
     _say(f"lds 12-row fused == single M={M} K={K} Ns={Ns}")
     x = synthetic.activations(M, K, seed=23)

@@ -11,7 +11,8 @@ through the public ops:
 * the fused multi-matrix GEMV (segment table), whose segments share a launch;
 * K = 4096 or 5120 with many rows, where a workgroup streams two or four
   consecutive 16-row tiles (ragged last workgroup);
-* 12-row tiles, where they balance the CUs better than 16-row ones.
+* 12-row tiles, one or two per workgroup, where they balance the CUs better
+  than 16-row ones.
 
 N values include ones that are not multiples of the 16- and 32-row tiles.
 Reference: the CPU oracle; tolerance |out - ref| <= 1e-2 max|ref| + 2e-2 |ref|.
@@ -36,10 +37,11 @@ def _say(msg):
     sys.stdout.flush()
 
 
-# (K, N): every instantiated K, with N on both sides of the switch to 32-row
-# tiles for 9-16 rows (more 16-row tiles than CUs: N = 4610 and up)
+# (K, N): every instantiated K, with N on both sides of the switch to
+# two-tile workgroups for 9-16 rows (more 16-row tiles than CUs: N = 4112 and
+# up): 24 rows (two 12-row tiles) up to N = 6144, 32 rows above
 SHAPES = [(2048, 1000), (3072, 6200), (4096, 6144), (4096, 2050), (5120, 6150), (14336, 1030), (24576, 520),
-          (4096, 4610)]
+          (4096, 4610), (4096, 7000)]
 
 
 @pytest.mark.parametrize("K,N", SHAPES)

@@ -1802,10 +1802,11 @@ static void launch_norm_steps(GemvSegs& sg, const NormArgs& na, int skind, int M
 
 template <typename T, typename TO, bool XF8>
 static void launch_norm_t(GemvSegs& sg, const NormArgs& na, int skind, int M, int N, int K, bool glu, hipStream_t st) {
-  // one activation row (M = 1) or up to four
+  // one activation row (M = 1) or up to four (the quantising form: one)
   auto by_rows = [&](auto s) {
     constexpr int S_ = decltype(s)::value;
-    if (M == 1) launch_norm_steps<T, TO, XF8, S_, 1>(sg, na, skind, M, N, glu, st);
+    if constexpr (XF8) launch_norm_steps<T, TO, XF8, S_, 1>(sg, na, skind, M, N, glu, st);
+    else if (M == 1) launch_norm_steps<T, TO, XF8, S_, 1>(sg, na, skind, M, N, glu, st);
     else launch_norm_steps<T, TO, XF8, S_, 4>(sg, na, skind, M, N, glu, st);
   };
   if (K == 3072) by_rows(std::integral_constant<int, 3>{});
@@ -1822,11 +1823,11 @@ static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_by
   return pa < pb + b_bytes && pb < pa + a_bytes;
 }
 
-// The fused launch covers M <= 4 rows, K in {3072, 4096, 5120}, e4m3
-// weights, 16-byte aligned operands and side outputs that do not overlap the
-// inputs; CEK_ERR_UNSUPPORTED otherwise (the caller runs the norm, then the
-// GEMV).  q_out != null selects the quantising form (a8w8 GEMV: fp32
-// per-channel weight scales).
+// The fused launch covers M <= 4 rows (the quantising form: M = 1), K in
+// {3072, 4096, 5120}, e4m3 weights, 16-byte aligned operands and side
+// outputs that do not overlap the inputs; CEK_ERR_UNSUPPORTED otherwise (the
+// caller runs the norm, then the GEMV).  q_out != null selects the
+// quantising form (a8w8 GEMV: fp32 per-channel weight scales).
 int launch_norm_gemv(const NormArgs& na, const void* w, const void* scale, int skind, void* y, int64_t M,
                      int64_t N, int64_t K, bool glu, int io_dtype, int fp8_fmt, hipStream_t st) {
   const bool quant = na.q_out != nullptr;
@@ -1841,6 +1842,14 @@ int launch_norm_gemv(const NormArgs& na, const void* w, const void* scale, int s
   if (N * K > ((int64_t)1 << 40)) return CEK_ERR_INVALID;
   const int64_t rb = M * K * 2;  // bytes of one [M, K] activation matrix
   if (N == 0 || M > 4 || (K != 3072 && K != 4096 && K != 5120) || fp8_fmt != CEK_E4M3) return CEK_ERR_UNSUPPORTED;
+  // The quantising form fuses one row only: from two rows on, the prologue
+  // that every workgroup runs (the norm and the quantisation of all M rows)
+  // made the launch slower than the norm+quant launch and the product
+  // (measured on MI355X, weights from HBM, us fused / two launches: M = 2-4,
+  // K = 4096, N = 6144 12.6-13.0 / 10.1-10.2; K = 5120 26.0-26.7 /
+  // 11.8-12.0; K = 3072, N = 12288 27.4-27.7 / 11.3-12.0; at M = 1 7.9 /
+  // 9.4, 9.1 / 11.5 and 9.8 / 11.7).
+  if (quant && M > 1) return CEK_ERR_UNSUPPORTED;
   if (!aligned(na.h, 16) || !aligned(na.r, 16) || !aligned(na.w, 16) || !aligned(na.r_out, 16) || !aligned(w, 16) ||
       (na.h_out && !aligned(na.h_out, 16)) || (quant && !aligned(na.q_out, 16)))
     return CEK_ERR_UNSUPPORTED;

@@ -207,11 +207,15 @@ int cek_gelu_and_mul(void* out, const void* x, int64_t T, int64_t d,
  *                  of cek_fused_add_rms_norm_quant_fp8); y = a8w8 GEMV of
  *                  the codes (W e4m3, scale fp32 [N])
  * with gelu_and_mul != 0: W holds 2d = N rows (gate, then up) and y [M, d]
- * is gelu_tanh(gate) * up, as cek_gemv_fp8_gelu_and_mul.  Every value
- * equals the unfused ops', bit for bit.  residual_out and hidden_out must
- * not overlap hidden or residual.  Covers M <= 4, K in {3072, 4096, 5120},
- * e4m3 weights and 16-byte aligned operands; CEK_ERR_UNSUPPORTED otherwise,
- * for the caller to run the norm and the GEMV as two launches.
+ * is gelu_tanh(gate) * up, as cek_gemv_fp8_gelu_and_mul.  residual_out,
+ * hidden_out, q_out and q_scale equal the unfused ops' bit for bit, and so
+ * does y from three rows on and with gelu_and_mul (at one or two rows the
+ * unfused GEMV sums in another order: y within the GEMV's tolerance).
+ * residual_out and hidden_out must not overlap hidden or residual.  Covers
+ * M <= 4 (with q_out: M = 1, where one launch is faster than two), K in
+ * {3072, 4096, 5120}, e4m3 weights and 16-byte aligned operands;
+ * CEK_ERR_UNSUPPORTED otherwise, for the caller to run the norm and the
+ * GEMV as two launches.
  */
 int cek_add_rms_norm_gemv_fp8(const void* hidden, const void* residual, const void* norm_weight, float eps,
                               void* residual_out, void* hidden_out, uint8_t* q_out, float* q_scale,

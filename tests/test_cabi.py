@@ -166,6 +166,10 @@ def test_host_rejects_invalid_arguments():
     assert ng(p, p, p, 1e-6, q, None, None, None, p, p, p, 4, 64, 2048, 0, 0, 0, 2, None) == U   # K
     assert ng(p, p, p, 1e-6, q, None, None, None, p, p, p, 4, 64, 4096, 0, 0, 1, 2, None) == U   # e5m2
     assert ng(p, p, p, 1e-6, p, None, None, None, p, p, p, 4, 64, 4096, 0, 0, 0, 2, None) == U   # r_out aliases
+    # the quantising form fuses one row only (two launches are faster from two
+    # rows on); outputs at distinct fake addresses, so only the row count decides
+    h_, r_, w_, ro, qo, qs = (C.c_void_p(a) for a in (1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20))
+    assert ng(h_, r_, w_, 1e-6, ro, None, qo, qs, p, p, p, 2, 64, 4096, 0, 0, 0, 2, None) == U
     assert ng(None, None, None, 1e-6, None, None, None, None, None, None, None, 0, 64, 4096, 0, 0, 0, 2,
               None) == cabi.CEK_OK
     # split-K workspace: size query, and a negative or missing workspace

@@ -244,11 +244,12 @@ def test_a8w8_24row_tiles(ops, dev, M, K, N):
 
 # A matrix alone takes 12-row tiles; in a fused launch whose total row count
 # picks 16-row tiles (M = 8: 20480 rows, one tile per workgroup), 24-row
-# workgroups (M = 12: 6144 rows; M = 16: 6001 rows over two ragged matrices)
+# workgroups (M = 12: 6144 rows; M = 16: 6001 rows over two ragged matrices,
+# 6008 with an 8-row one inside a single workgroup)
 # or 32-row ones (M = 12: 7168 rows) it must still get the same outputs bit
 # for bit (the tile heights add each output's K chunks in the same order).
 @pytest.mark.parametrize("M,K,Ns", [(8, 4096, (6144, 14336)), (12, 3072, (3072, 3072)), (16, 4096, (3000, 3001)),
-                                    (12, 4096, (3072, 4096))])
+                                    (12, 4096, (3072, 4096)), (16, 4096, (6000, 8))])
 def test_12row_fused_equals_single(ops, dev, M, K, Ns):
     _say(f"lds 12-row fused == single M={M} K={K} Ns={Ns}")
     x = synthetic.activations(M, K, seed=23)

@@ -1163,7 +1163,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
           }
         } else {
           lds_reduce_store_tile<NT, MB, SH>(acc, redp, wave, lane, tile_row(i / STEPS), N, M, sr, skind, sc_n, sc_m,
-                                              XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
+                                            XF8 || EPI == EPI_ROWSCALE, std::is_same<TO, BF16>::value);
         }
         if (i + 1 < NS) {
 #pragma unroll
@@ -1171,7 +1171,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(const void* xv, GemvSegs 
 #pragma unroll
             for (int b = 0; b < MB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
           lds_load_scales<NT, MB, SH>(sc_n, sc_m, wave, lane, tile_row(i / STEPS + 1), N, M, sr, skind,
-                                  XF8 && !NORM ? sg.xs : nullptr);
+                                      XF8 && !NORM ? sg.xs : nullptr);
           if constexpr (NORM && XF8) pick_row_scales();
           pick_rs();
         }
@@ -1599,7 +1599,7 @@ static bool launch_lds_steps(const void* x, GemvSegs& sg, int skind, int M, int 
   const int tpw12 = least_rows(12, rows12);
   const bool r12 = 5 * rows12 <= 4 * rows16;
   // two-tile workgroups: 2 x 12 rows where they cut the busiest CU's rows
-  // against 2 x 16 by a fifth or more (N = 4608-6144: 24 rows against 32)
+  // against 2 x 16 by a fifth or more (N = 4112-6144: 24 rows against 32)
   auto busiest = [&](int wrows) { return wrows * (((N + wrows - 1) / wrows + kCUs - 1) / kCUs); };
   const bool n24 = 5 * busiest(24) <= 4 * busiest(32);
   if constexpr (!XF8) {

@@ -17,10 +17,11 @@ Two references:
   rows and more, or the gate/up form at any M) -- the fused prologue
   reproduces the norm kernel's thread layout and reduction order.
 
-Shapes: every fused configuration (1 or up to 4 rows; K = 3, 4, 5 KiB
-values; one or two tiles per workgroup; the gate/up form), N not a multiple
-of 16, and the two-launch path the ops take for more rows, other K, or a
-residual_out that aliases residual.
+Shapes: every fused configuration (1 or up to 4 rows, the quantising form
+1 row; K = 3, 4, 5 KiB values; one or two tiles per workgroup; the gate/up
+form), N not a multiple of 16, and the two-launch path the ops take for
+more rows (the quantising form: from two rows), other K, or a residual_out
+that aliases residual.
 """
 
 import sys
